@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X INT4 expert-MLP hot path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c3|c4] [--tokens T]
+
+Prints ONE JSON line.  A "step" is one pass of the hot path over one batch of
+synthetic input already resident in HBM:
+
+  c1  one Mixtral expert SwiGLU (H 4096, I 14336, INT4 g128), T tokens (default 1)
+
+Weights are seeded N(0, 0.02) fp16 packed to INT4 by the GPU packer.  Steps
+rotate over enough distinct experts (>= 0.7 GB) that weights stream from HBM,
+not from the 256 MB Infinity Cache.  Steps are replayed from a HIP graph.
+
+roofline: the dominant kernel's algorithmic bytes per launch divided by its
+average duration, timed with HIP events around graph-replayed launches on the
+stream the kernel runs on.  cpu_baseline: the torch-CPU restatement of the
+reference's dequantise-then-matmul path (oracle/torch_ref.py) on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+METRIC = ("INT4 expert-MLP HBM GB/s (% of peak); Mixtral-shape decode tokens/sec, 1 GPU")
+
+
+def _log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def _chunk(k: int, cap: int = 50) -> int:
+    for c in range(min(cap, k), 0, -1):
+        if k % c == 0:
+            return c
+    return 1
+
+
+def _graph(fn, reps: int):
+    """Capture `reps` calls of fn into one HIP graph; None if capture fails."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm allocator on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+    except Exception as exc:  # pragma: no cover - reported in the JSON
+        _log("graph capture failed:", exc)
+        return None
+    return g
+
+
+def _time_graph(g: torch.cuda.CUDAGraph, replays: int) -> float:
+    """Average ms per replay, with events on the current stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / replays
+
+
+# ----------------------------------------------------------------------------- C1
+def bench_c1(args):
+    from hydranet_amd import _lib
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
+    from hydranet_amd.kernels import expert_mlp_int4_fused
+
+    H, I, g, T = 4096, 14336, 128, args.tokens
+    n_exp = 8  # 8 x 90.8 MB rotate: 727 MB > 256 MB Infinity Cache
+    slots = [make_expert_slot(expert_seed(0, e), H, I, g, slot_idx=e) for e in range(n_exp)]
+    x = normal_f16((T, H), 1234, std=1.0)
+    blob = slots[0].layout.total_size
+    bytes_step = blob + 2 * T * H * 2  # blob + x + y (SURVEY C1 accounting)
+
+    outs = [torch.empty(T, H, dtype=torch.float16, device="cuda") for _ in range(n_exp)]
+    hws = [torch.empty(T, I, dtype=torch.float16, device="cuda") for _ in range(n_exp)]
+    state = {"i": 0}
+
+    def step():
+        e = state["i"] % n_exp
+        state["i"] += 1
+        sl = slots[e]
+        _lib.call("hn_expert_mlp_int4", _lib.ptr(x), *[_lib.ptr(t) for t in (
+            sl.gate_packed, sl.gate_scales, sl.up_packed, sl.up_scales, sl.down_packed,
+            sl.down_scales)], _lib.ptr(outs[e]), T, H, I, g, _lib.ptr(hws[e]), _lib.stream())
+
+    # parity of the product entry point vs the CPU oracle on expert 0
+    y_gpu = expert_mlp_int4_fused(x, slots[0].gate_packed, slots[0].gate_scales,
+                                  slots[0].up_packed, slots[0].up_scales, slots[0].down_packed,
+                                  slots[0].down_scales, g)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    chunk = _chunk(args.steps)
+    state["i"] = 0
+    gr = _graph(step, chunk)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    if gr is not None:
+        for _ in range(args.steps // chunk):
+            gr.replay()
+    else:
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt * 1e3 / args.steps
+
+    # dominant kernel: gate+up+SiLU (two thirds of the bytes); also time down
+    reps = 16
+
+    def gate_up_only():
+        e = state["i"] % n_exp
+        state["i"] += 1
+        sl = slots[e]
+        _lib.call("hn_int4_gate_up_silu", _lib.ptr(x), H, _lib.ptr(sl.gate_packed),
+                  _lib.ptr(sl.gate_scales), _lib.ptr(sl.up_packed), _lib.ptr(sl.up_scales),
+                  H // 2, H // g, _lib.ptr(hws[e]), I, T, I, H, g, _lib.stream())
+
+    def down_only():
+        e = state["i"] % n_exp
+        state["i"] += 1
+        sl = slots[e]
+        _lib.call("hn_int4_linear", _lib.ptr(hws[e]), I, _lib.ptr(sl.down_packed), I // 2,
+                  _lib.ptr(sl.down_scales), I // g, _lib.ptr(outs[e]), H, T, H, I, g,
+                  _lib.stream())
+
+    kt = {}
+    for name, fn in (("gate_up_silu", gate_up_only), ("down", down_only)):
+        gk = _graph(fn, reps)
+        kt[name] = _time_graph(gk, 10) / reps if gk is not None else float("nan")
+    gu_bytes = 2 * (slots[0].layout.gate_packed_size + slots[0].layout.gate_scales_size) + \
+        T * H * 2 + T * I * 2
+    dn_bytes = slots[0].layout.down_packed_size + slots[0].layout.down_scales_size + \
+        T * I * 2 + T * H * 2
+    achieved = gu_bytes / (kt["gate_up_silu"] * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(bytes_step / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "ms_per_step": round(ms, 5),
+        "dtype": "fp16",
+        "config": {"workload": f"C1: one Mixtral expert SwiGLU 4096->14336->4096, INT4 g128, "
+                               f"T={T}", "tokens": T, "hidden": H, "intermediate": I,
+                   "group_size": g, "experts_rotated": n_exp, "bytes_per_step": bytes_step,
+                   "graph": gr is not None},
+        "roofline": {"bound": "hbm", "kernel": "skinny_kernel<2,8,1,false,16> (gate+up+SiLU)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": gu_bytes, "avg_us": round(kt["gate_up_silu"] * 1e3, 3),
+                     "down_avg_us": round(kt["down"] * 1e3, 3),
+                     "down_gbs": round(dn_bytes / (kt["down"] * 1e-3) / 1e9, 1),
+                     "expert_frac": round(bytes_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+    }
+    return result, (slots[0], x, y_gpu, g)
+
+
+def cpu_baseline_c1(ctx, budget_s: float):
+    """Torch-CPU restatement of the reference's dequantise-then-matmul path,
+    timed on this host.  TEST INFRASTRUCTURE (oracle) used only as the baseline."""
+    from oracle import torch_ref
+    from hydranet_amd.preprocess.synthetic import slot_to_cpu
+    slot, x, y_gpu, g = ctx
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    e = slot_to_cpu(slot)
+    xc = x.cpu()
+    times = []
+    y = None
+    t_start = time.perf_counter()
+    for i in range(64):
+        t0 = time.perf_counter()
+        y = torch_ref.expert_mlp(xc, *e, group_size=g)
+        times.append(time.perf_counter() - t0)
+        if i >= 3 and time.perf_counter() - t_start > budget_s:
+            break
+    runs = times[3:] if len(times) > 4 else times
+    med = statistics.median(runs)
+    err = (y_gpu.cpu().float() - y.float()).abs()
+    ok = bool((err <= 1e-2 + 2e-3 * y.float().abs()).all())
+    bytes_step = slot.layout.total_size + 2 * x.numel() * 2
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(bytes_step / med / 1e9, 3), "unit": "GB/s",
+            "ms_per_step": round(med * 1e3, 2), "cores": torch.get_num_threads(), "kind": "port",
+            "cpu": cpu_model,
+            "sample": f"{len(runs)} timed calls (3 warm-up) of one C1 expert, median; "
+                      f"dequant included per call"}, {"max_abs_err": float(err.max()),
+                                                     "ok": ok}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c1", choices=["c1"])
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only; the INT4 expert path is "
+                                   "benchmarked per GPU (see DESIGN.md for how it shards)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
+    res, ctx = bench_c1(args)
+    _log("gpu done", res["value"], res["unit"])
+    cpu = None
+    if not args.no_cpu:
+        cpu, parity = cpu_baseline_c1(ctx, args.cpu_budget)
+        res["parity"] = parity
+    out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": res.pop("dtype"), "data": "synthetic",
+           "config": res.pop("config"), "roofline": res.pop("roofline"), "cpu_baseline": cpu}
+    out.update(res)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

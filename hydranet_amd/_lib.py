@@ -1,0 +1,92 @@
+"""ctypes binding of libhn_int4.so (the C ABI declared in include/hn_int4.h).
+
+torch is imported first on purpose: torch ships the HIP runtime
+(libamdhip64.so.7), and loading it before this library makes the library bind
+to the same runtime instance, so torch's streams and allocations are valid
+here.  There is no fallback: if the library is missing or a call fails, the
+caller gets a RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see module doc)
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libhn_int4.so")
+
+P = ctypes.c_void_p
+L = ctypes.c_long
+I = ctypes.c_int
+F = ctypes.c_float
+
+SIGNATURES: dict[str, list] = {
+    "hn_int4_dequant": [P, L, P, L, P, L, L, L, L, P],
+    "hn_int4_quantize": [P, L, I, I, P, L, P, L, L, L, L, P],
+    "hn_int4_linear": [P, L, P, L, P, L, P, L, L, L, L, L, P],
+    "hn_int4_gate_up_silu": [P, L, P, P, P, P, L, L, P, L, L, L, L, L, P],
+    "hn_expert_mlp_int4": [P, P, P, P, P, P, P, P, L, L, L, L, P, P],
+    "hn_silu_mul": [P, L, P, L, P, L, L, L, P],
+    "hn_router_logits": [P, L, P, L, I, P, L, L, L, P],
+    "hn_router_topk": [P, P, L, L, L, I, F, F, P, P, P],
+    "hn_moe_permute": [P, L, L, L, P, P, P, P, P, P],
+    "hn_moe_gather": [P, L, P, L, P, L, P, L, L, L, P],
+    "hn_moe_unpermute": [P, L, P, P, P, L, L, P, L, P, L, L, P],
+    "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, P, P, P],
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m hydranet_amd.build` "
+                "(the INT4 path has no CPU fallback)")
+        h = ctypes.CDLL(LIB_PATH)
+        h.hn_last_error_string.restype = ctypes.c_char_p
+        h.hn_abi_version.restype = ctypes.c_int
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        _lib = h
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().hn_last_error_string().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (rc={rc}): {msg}")
+
+
+def ptr(t) -> ctypes.c_void_p:
+    if t is None:
+        return ctypes.c_void_p(None)
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream(device=None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu(*tensors) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "hydranet_amd INT4 kernels run on the GPU only; got a tensor on "
+                f"{t.device} (there is no CPU fallback)")
+
+
+def aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous inner dim and a 16-byte aligned base, copying if needed."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 != 0 or (t.dim() > 1 and
+                                                         (t.stride(-2) * t.element_size()) % 16):
+        t = t.contiguous()
+        if t.data_ptr() % 16 != 0:
+            t = t.clone()
+    return t

@@ -1,0 +1,97 @@
+// Shared device/host helpers for the gfx950 INT4 expert-MLP kernels.
+//
+// Packed INT4 format (HydraNet blob layout, preprocess/pack_weights.py:160-181):
+//   packed[n, j] (uint8) holds W[n, 2j] in the low nibble and W[n, 2j+1] in the
+//   high nibble, stored as (q + 8) with q in [-8, 7];
+//   scales[n, k / group] (fp16);  W[n, k] = fp16((nibble - 8) * scale).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 h16;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define HN_WAVE 64
+
+// ---------------------------------------------------------------------------
+// Error plumbing for the C ABI (thread-local last error string).
+// ---------------------------------------------------------------------------
+#ifdef __cplusplus
+extern "C" {
+#endif
+void hn_set_error(const char* fmt, ...);
+#ifdef __cplusplus
+}
+#endif
+
+#define HN_ARG_CHECK(cond, ...)              \
+  do {                                       \
+    if (!(cond)) {                           \
+      hn_set_error(__VA_ARGS__);             \
+      return -22; /* -EINVAL */              \
+    }                                        \
+  } while (0)
+
+#define HN_LAUNCH_CHECK(what)                                              \
+  do {                                                                     \
+    hipError_t _e = hipGetLastError();                                     \
+    if (_e != hipSuccess) {                                                \
+      hn_set_error("%s: launch failed: %s", what, hipGetErrorString(_e));  \
+      return (int)_e;                                                      \
+    }                                                                      \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Nibble unpacking.
+//
+// A 32-bit word w of packed data holds 8 consecutive k (k0..k7); nibble k_i
+// sits at bits [4i, 4i+4).  The fp16 "magic number" trick places a nibble in
+// the mantissa of 1024.0 (0x6400): (w & 0x000F000F) | 0x64006400 is the pair
+// (1024 + n0, 1024 + n4).  The high nibble of each byte is used in place as
+// 1024 + 16 n, then rescaled with an exact fma.  Output order of the eight
+// values is k = (0,4, 1,5, 2,6, 3,7): the activation operand of the matrix
+// product is permuted the same way (see hn_perm8), so the reduction
+// over k is unchanged.
+//
+// Every step is exact in fp16: (1024 + n) - 1032 = n - 8, and
+// (1024 + 16 n) * 0.0625 - 72 = n - 8, both representable.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ half2_t hn_bits_h2(uint32_t v) {
+  return __builtin_bit_cast(half2_t, v);
+}
+
+__device__ __forceinline__ void hn_unpack8_centered(uint32_t w, half2_t out[4]) {
+  const uint32_t lo0 = (w & 0x000F000Fu) | 0x64006400u;
+  const uint32_t hi0 = (w & 0x00F000F0u) | 0x64006400u;
+  const uint32_t w8 = w >> 8;
+  const uint32_t lo1 = (w8 & 0x000F000Fu) | 0x64006400u;
+  const uint32_t hi1 = (w8 & 0x00F000F0u) | 0x64006400u;
+  const half2_t bias_lo = {(h16)-1032.0f, (h16)-1032.0f};
+  const half2_t sixteenth = {(h16)0.0625f, (h16)0.0625f};
+  const half2_t bias_hi = {(h16)-72.0f, (h16)-72.0f};
+  out[0] = hn_bits_h2(lo0) + bias_lo;                       // k0, k4
+  out[1] = __builtin_elementwise_fma(hn_bits_h2(hi0), sixteenth, bias_hi);  // k1, k5
+  out[2] = hn_bits_h2(lo1) + bias_lo;                       // k2, k6
+  out[3] = __builtin_elementwise_fma(hn_bits_h2(hi1), sixteenth, bias_hi);  // k3, k7
+}
+
+// Position j of an 8-block in unpack order holds source index hn_perm8(j).
+__host__ __device__ constexpr int hn_perm8(int j) { return (j >> 1) + ((j & 1) << 2); }
+
+__device__ __forceinline__ half8_t hn_cat4(const half2_t p[4]) {
+  half8_t r;
+  r[0] = p[0][0]; r[1] = p[0][1];
+  r[2] = p[1][0]; r[3] = p[1][1];
+  r[4] = p[2][0]; r[5] = p[2][1];
+  r[6] = p[3][0]; r[7] = p[3][1];
+  return r;
+}
+
+__device__ __forceinline__ float hn_silu(float g) {
+  return g / (1.0f + expf(-g));
+}
+
+static inline int hn_cdiv(long a, long b) { return (int)((a + b - 1) / b); }

@@ -1,0 +1,115 @@
+/*
+ * hn_int4.h — C ABI of libhn_int4.so, the gfx950 INT4 expert-MLP hot path.
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer unless stated otherwise; the
+ *    library never allocates, frees or retains them.  Workspaces are passed in.
+ *  - fp16 data is IEEE binary16 ("half"); packed weights are uint8 with two
+ *    nibbles per byte (low nibble = even k), stored as q + 8, q in [-8, 7];
+ *    scales are fp16, one per (row, group of `group` consecutive k).
+ *  - ld_* arguments are row strides: bytes for packed weights, elements for
+ *    everything else.  Inner dimensions are contiguous.
+ *  - `stream` is a hipStream_t (e.g. torch.cuda.current_stream().cuda_stream);
+ *    every call only enqueues work on it.
+ *  - Return value: 0 on success, a negative errno-style code for a rejected
+ *    argument, or a positive hipError_t from the launch.  The message is in
+ *    hn_last_error_string() (thread-local).
+ */
+#ifndef HN_INT4_H
+#define HN_INT4_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* hn_last_error_string(void);
+int hn_abi_version(void);
+
+/* Dequantise packed[N, K/2] + scales[N, K/group] into out[N, K] fp16, bit-exact
+ * with fp16((nibble - 8) * scale).  Replaces GpuExpertSlot._dequant_tensor
+ * (cache/packed_expert_store.py:287-315), ExpertWeightPacker.dequantize_tensor
+ * (preprocess/pack_weights.py:230-268), ExpertMLPTriton._dequant
+ * (kernels/expert_mlp.py:305-330).  K % 32 == 0. */
+int hn_int4_dequant(const void* packed, long ld_p, const void* scales, long ld_s, void* out,
+                    long ld_o, long N, long K, long group, void* stream);
+
+/* Quantise w[N, K] (dtype 0 = fp16, 1 = fp32) into packed/scales.
+ * mode 0 = ExpertWeightPacker.quantize_tensor (preprocess/pack_weights.py:133-181),
+ * mode 1 = Int4Linear.quantize_weight (kernels/int4_linear.py:68-107). */
+int hn_int4_quantize(const void* w, long ld_w, int dtype, int mode, void* packed, long ld_p,
+                     void* scales, long ld_s, long N, long K, long group, void* stream);
+
+/* out[M, N] = fp16(x[M, K] @ deq(W)^T), fp32 accumulation.  Replaces the
+ * int4_matmul_kernel launch in int4_gemm.int4_linear (kernels/int4_gemm.py:124-172)
+ * and int4_expert_mlp.int4_linear (kernels/int4_expert_mlp.py:99-156).
+ * K % 32 == 0, group a multiple of 32 dividing K, 16-byte aligned rows. */
+int hn_int4_linear(const void* x, long ld_x, const void* wq, long ld_q, const void* ws, long ld_s,
+                   void* out, long ld_o, long M, long N, long K, long group, void* stream);
+
+/* h[M, N] = fp16(silu(fp16(x @ deq(Wg)^T)) * fp16(x @ deq(Wu)^T)): the gate and up
+ * projections of expert_mlp_int4_fused plus fused_silu_mul
+ * (kernels/int4_gemm.py:175-208, 241-247) in one launch. */
+int hn_int4_gate_up_silu(const void* x, long ld_x, const void* gq, const void* gs, const void* uq,
+                         const void* us, long ld_q, long ld_s, void* h, long ld_h, long M, long N,
+                         long K, long group, void* stream);
+
+/* out[T, H] = down(silu(gate(x)) * up(x)) for one expert; h_ws is a [T, I] fp16
+ * workspace.  Replaces int4_gemm.expert_mlp_int4_fused (kernels/int4_gemm.py:211-254)
+ * and int4_expert_mlp.expert_mlp_int4 (kernels/int4_expert_mlp.py:213-252). */
+int hn_expert_mlp_int4(const void* x, const void* gq, const void* gs, const void* uq,
+                       const void* us, const void* dq, const void* ds, void* out, long T, long H,
+                       long I, long group, void* h_ws, void* stream);
+
+/* out = fp16(silu(float(g)) * float(u)).  Replaces fused_silu_mul / silu_mul
+ * (kernels/int4_gemm.py:196-208, kernels/int4_expert_mlp.py:189-210). */
+int hn_silu_mul(const void* g, long ld_g, const void* u, long ld_u, void* out, long ld_o, long M,
+                long N, void* stream);
+
+/* logits[T, E] fp32 = h[T, H] @ W^T.  w_dtype 0: fp16 gate, logits rounded to fp16
+ * (TopKRouter.gate(...).float(), model/router.py:102); w_dtype 1: fp32 weight
+ * (GLM4SigmoidRouter, model/glm4.py:279). */
+int hn_router_logits(const void* h, long ld_h, const void* w, long ld_w, int w_dtype,
+                     void* logits, long T, long E, long H, void* stream);
+
+/* Top-k routing from fp32 logits.  mode 0: softmax over the selected logits and
+ * renormalise (model/router.py:109-120); mode 1: sigmoid, optional selection-only
+ * bias[E] (may be NULL), weights / (sum + eps) * scaling (model/glm4.py:282-309).
+ * Ties go to the lower expert index.  idx_out int32 [T, k], w_out fp16 [T, k]. */
+int hn_router_topk(const void* logits, const void* bias, long T, long E, long k, int mode,
+                   float eps, float scaling, int* idx_out, void* w_out, void* stream);
+
+/* Stable counting sort of the [T*k] assignments by expert (the per-expert
+ * torch.where loop of MixtralMoELayer.forward, model/mixtral.py:296-338).
+ * offsets[E+1], perm[T*k] (sorted position -> assignment), inv[T*k]
+ * (assignment -> sorted position), active[E] (experts with tokens, ascending),
+ * n_active[1].  E <= 256. */
+int hn_moe_permute(const int* idx, long T, long k, long E, int* offsets, int* perm, int* inv,
+                   int* active, int* n_active, void* stream);
+
+/* x_perm[p] = x[perm[p] / k] for p < offsets[E] (flat_hidden[token_indices],
+ * model/mixtral.py:338).  rows = grid bound (T*k). */
+int hn_moe_gather(const void* x, long ld_x, const int* perm, long k, const int* offsets, long E,
+                  void* x_perm, long ld_p, long rows, long H, void* stream);
+
+/* out[T, H] = (shared +) sum over the token's experts (ascending id) of
+ * fp16(y_perm[inv[t*k+s]] * w[t, s]) with fp16 accumulation: output.index_add_
+ * (model/mixtral.py:365-368) and shared + routed (model/glm4.py:473). */
+int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* idx, const void* w,
+                     long T, long k, const void* shared, long ld_sh, void* out, long ld_o, long H,
+                     void* stream);
+
+/* Grouped SwiGLU over every active expert of one MoE layer in two launches.
+ * x_perm [rows, H] sorted by expert; table: E x {gate_q, gate_s, up_q, up_s,
+ * down_q, down_s} device pointers (u64); active / n_active / offsets from
+ * hn_moe_permute; h_ws [rows, I] fp16 workspace; y_perm [rows, H] fp16 out.
+ * Replaces the per-expert loop calling expert_mlp_int4_fused
+ * (model/mixtral.py:327-354, model/glm4.py:421-455). */
+int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int* active,
+                               const int* n_active, const int* offsets, long E_max,
+                               long max_rows_per_expert, long H, long I, long group, void* h_ws,
+                               void* y_perm, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HN_INT4_H */

@@ -1,0 +1,188 @@
+"""Write the golden vectors in tests/golden/ by running the REFERENCE's own code.
+
+Run in the build container only (the reference tree is not on the GPU box):
+
+    python tests/golden/make_golden.py /root/reference
+
+The reference package is mapped to the name ``hydranet`` without executing its
+package __init__ files (only the modules listed below are imported).  What it
+pins, per fixture (all small, CPU, seeded):
+
+  quantize_tensor.npz   ExpertWeightPacker.quantize_tensor      (preprocess/pack_weights.py:133-181)
+                        + dequantize_tensor                      (:230-268)
+  quantize_weight.npz   Int4Linear.quantize_weight               (kernels/int4_linear.py:68-107)
+  expert_mlp.npz        ExpertMLPTriton.forward torch path       (kernels/expert_mlp.py:254-330)
+  topk_router.npz       TopKRouter.forward, affinity off          (model/router.py:73-130)
+  sigmoid_router.npz    GLM4SigmoidRouter.forward                 (model/glm4.py:261-309)
+  blob_layout.json      BlobLayout.from_dims at Mixtral/GLM dims  (cache/packed_expert_store.py:77-108)
+
+Only data (inputs and the reference's outputs) is written; no reference
+source is copied.
+"""
+from __future__ import annotations
+
+import importlib
+import json
+import os
+import sys
+import types
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _map_reference(root: str) -> None:
+    # bare package objects (their __init__ files would pull in the engine);
+    # hydranet.cache is imported normally because model/glm4.py needs its exports
+    for name, sub in [("hydranet", ""), ("hydranet.preprocess", "preprocess"),
+                      ("hydranet.kernels", "kernels"), ("hydranet.model", "model")]:
+        mod = types.ModuleType(name)
+        mod.__path__ = [os.path.join(root, sub)] if sub else [root]
+        sys.modules[name] = mod
+
+
+def _f16(seed: int, shape, scale: float) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g, dtype=torch.float32) * scale).to(torch.float16)
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def quantize_cases():
+    cases = {}
+    cases["randn_64x256_g128"] = (_f16(1, (64, 256), 0.02), 128)
+    cases["randn_16x1408_g128"] = (_f16(2, (16, 1408), 0.02), 128)
+    cases["randn_32x256_g64"] = (_f16(3, (32, 256), 0.1), 64)
+    cases["randn_32x128_g32"] = (_f16(4, (32, 128), 1.0), 32)
+    # exact .5 ties after w / s (absmax 7 -> s = 1), negatives, zeros,
+    # an all-zero group (scale underflows to 0), subnormal-only group, huge values
+    t = torch.zeros(4, 256, dtype=torch.float32)
+    t[0, :128] = torch.tensor([7.0, -7.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, -3.5, 6.5, -6.5]
+                              + [0.25 * i for i in range(116)])
+    t[0, 128:] = torch.linspace(-1.0, 1.0, 128)
+    t[1, :128] = 0.0
+    t[1, 128:] = torch.linspace(-3e-7, 3e-7, 128)
+    t[2, :] = torch.linspace(-60000.0, 60000.0, 256)
+    t[3, :] = -0.0
+    t[3, 5] = 1e-3
+    cases["edge_4x256_g128"] = (t.to(torch.float16), 128)
+    return cases
+
+
+def main(root: str) -> None:
+    _map_reference(root)
+    pw = importlib.import_module("hydranet.preprocess.pack_weights")
+    il = importlib.import_module("hydranet.kernels.int4_linear")
+    em = importlib.import_module("hydranet.kernels.expert_mlp")
+    cfg = importlib.import_module("hydranet.config")
+    router = importlib.import_module("hydranet.model.router")
+    glm4 = importlib.import_module("hydranet.model.glm4")
+    store = importlib.import_module("hydranet.cache.packed_expert_store")
+
+    # ---- ExpertWeightPacker.quantize_tensor / dequantize_tensor
+    out = {}
+    for name, (w, g) in quantize_cases().items():
+        packer = pw.ExpertWeightPacker(pw.QuantConfig(bits=4, group_size=g, symmetric=True))
+        packed, scales = packer.quantize_tensor(w)
+        deq = packer.dequantize_tensor(packed, scales, w.shape[0], w.shape[1])
+        out[f"{name}/w"] = _bits(w)
+        out[f"{name}/group"] = np.array(g)
+        out[f"{name}/packed"] = packed.numpy()
+        out[f"{name}/scales"] = _bits(scales)
+        out[f"{name}/dequant"] = _bits(deq)
+    np.savez_compressed(os.path.join(HERE, "quantize_tensor.npz"), **out)
+
+    # ---- Int4Linear.quantize_weight (fp32 and fp16 inputs)
+    out = {}
+    g = torch.Generator().manual_seed(11)
+    for dt, dname in [(torch.float32, "f32"), (torch.float16, "f16")]:
+        for gs in (128, 64, 32):
+            w = (torch.randn(24, 256, generator=g) * 0.05).to(dt)
+            if gs == 32:
+                w[0, :32] = 0  # degenerate group
+            packed, scale = il.Int4Linear.quantize_weight(w, gs)
+            key = f"{dname}_g{gs}"
+            out[f"{key}/w"] = w.numpy() if dt == torch.float32 else _bits(w)
+            out[f"{key}/packed"] = packed.numpy()
+            out[f"{key}/scales"] = _bits(scale)
+    np.savez_compressed(os.path.join(HERE, "quantize_weight.npz"), **out)
+
+    # ---- ExpertMLPTriton.forward (torch dequantise-then-matmul path), CPU
+    out = {}
+    H, I, gs = 128, 256, 128
+    packer = pw.ExpertWeightPacker(pw.QuantConfig(group_size=gs))
+    wts = {"gate_proj": _f16(21, (I, H), 0.02), "up_proj": _f16(22, (I, H), 0.02),
+           "down_proj": _f16(23, (H, I), 0.02)}
+    pe = packer.pack_expert(0, 0, wts)
+    x = _f16(24, (5, H), 1.0)
+    mlp = em.ExpertMLPTriton(H, I, gs, device=torch.device("cpu"))
+    y = mlp.forward(x, pe.gate_proj_packed, pe.gate_proj_scales, pe.up_proj_packed,
+                    pe.up_proj_scales, pe.down_proj_packed, pe.down_proj_scales)
+    for k_, t_ in [("gate_packed", pe.gate_proj_packed), ("up_packed", pe.up_proj_packed),
+                   ("down_packed", pe.down_proj_packed)]:
+        out[k_] = t_.numpy()
+    for k_, t_ in [("gate_scales", pe.gate_proj_scales), ("up_scales", pe.up_proj_scales),
+                   ("down_scales", pe.down_proj_scales), ("x", x), ("y", y)]:
+        out[k_] = _bits(t_)
+    out["dims"] = np.array([H, I, gs])
+    np.savez_compressed(os.path.join(HERE, "expert_mlp.npz"), **out)
+
+    # ---- TopKRouter.forward (fp16 gate, affinity off), with forced ties
+    out = {}
+    mc = cfg.MixtralConfig()
+    mc.hidden_dim = 256
+    r = router.TopKRouter(mc, cfg.ExpertCacheConfig(enable_affinity_bonus=False), 0)
+    gw = _f16(31, (8, 256), 0.02)
+    gw[5] = gw[2]          # experts 2 and 5 tie on every token
+    r.gate.weight.data = gw.clone()
+    r.eval()
+    h = _f16(32, (1, 24, 256), 1.0)
+    h[0, 3] = 0.0          # all eight logits tie
+    h[0, 7] = h[0, 6]
+    with torch.no_grad():
+        for k in (1, 2):
+            ro = r(h, top_k_override=k, apply_affinity=False)
+            out[f"k{k}/idx"] = ro.expert_indices.numpy().astype(np.int32)
+            out[f"k{k}/w"] = _bits(ro.expert_weights)
+            out[f"k{k}/logits"] = ro.router_logits.numpy()
+    out["gate"] = _bits(gw)
+    out["h"] = _bits(h)
+    np.savez_compressed(os.path.join(HERE, "topk_router.npz"), **out)
+
+    # ---- GLM4SigmoidRouter.forward (fp32 weight, top-8 of 128)
+    out = {}
+    gc = cfg.GLM4AirConfig()
+    gc.hidden_dim = 256
+    sr = glm4.GLM4SigmoidRouter(gc, 1)
+    g2 = torch.Generator().manual_seed(41)
+    sr.weight.data = torch.randn(gc.num_experts, 256, generator=g2) * 0.02
+    h = _f16(42, (1, 32, 256), 1.0)
+    with torch.no_grad():
+        ti, tw = sr(h)
+    out["w"] = sr.weight.data.numpy()
+    out["h"] = _bits(h)
+    out["idx"] = ti.numpy().astype(np.int32)
+    out["wts"] = _bits(tw)
+    out["cfg"] = np.array([gc.num_experts, gc.experts_per_token, gc.n_group, gc.topk_group,
+                           int(gc.norm_topk_prob)], dtype=np.int64)
+    out["scaling"] = np.array(gc.routed_scaling_factor, dtype=np.float64)
+    np.savez_compressed(os.path.join(HERE, "sigmoid_router.npz"), **out)
+
+    # ---- BlobLayout
+    lay = {}
+    for name, (hd, idim, gs) in {"mixtral": (4096, 14336, 128), "glm4_air": (4096, 1408, 128),
+                                 "small": (128, 256, 128)}.items():
+        L = store.BlobLayout.from_dims(hd, idim, gs)
+        lay[name] = {"dims": [hd, idim, gs], "total_size": L.total_size,
+                     **{f: getattr(L, f) for f in L.__dataclass_fields__}}
+    with open(os.path.join(HERE, "blob_layout.json"), "w") as f:
+        json.dump(lay, f, indent=1, sort_keys=True)
+    print("golden vectors written to", HERE)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

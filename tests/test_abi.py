@@ -1,0 +1,48 @@
+"""CPU checks of the C ABI: the library loads and exports every function that
+include/hn_int4.h declares, and the ctypes table covers exactly that set.
+No kernel is launched."""
+import ctypes
+import os
+import re
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = []
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            src = open(os.path.join(ROOT, "include", fn)).read()
+            names += re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(hn_\w+)\s*\(", src, re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "hn_int4_linear" in names and "hn_expert_mlp_int4" in names
+    assert len(names) >= 14
+
+
+def test_library_exports_every_declared_symbol():
+    from hydranet_amd import _lib
+    h = _lib.lib()
+    for name in _declared():
+        assert hasattr(h, name), name
+    assert h.hn_abi_version() == 1
+
+
+def test_ctypes_table_matches_header():
+    from hydranet_amd import _lib
+    declared = set(_declared()) - {"hn_last_error_string", "hn_abi_version"}
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_argument_errors_raise_without_gpu():
+    # rejected arguments return before any HIP call
+    from hydranet_amd import _lib
+    import pytest
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        _lib.call("hn_int4_linear", None, 8, None, 16, None, 1, None, 8, 1, 1, 48, 16, None)
+    with pytest.raises(RuntimeError, match="mode must be"):
+        _lib.call("hn_router_topk", None, None, 1, 8, 2, 5, ctypes.c_float(0), ctypes.c_float(1),
+                  None, None, None)

@@ -1,0 +1,202 @@
+"""GPU parity: libhn_int4.so kernels vs the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact for quantise / dequantise / indices / permutation; fp16
+outputs of the matrix products within max-abs 1e-2 and relative 2e-3
+(|got - ref| <= 1e-2 + 2e-3 |ref|), the tolerance stated for this path.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import torch_ref
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+ATOL, RTOL = 1e-2, 2e-3
+DEV = "cuda:0"
+
+
+def _f16(bits):
+    return np.asarray(bits, dtype=np.uint16).view(np.float16)
+
+
+def _rand_f16(seed, shape, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.float16)
+
+
+def _close(got: torch.Tensor, ref: torch.Tensor):
+    got = got.float().cpu()
+    ref = ref.float().cpu()
+    err = (got - ref).abs()
+    bound = ATOL + RTOL * ref.abs()
+    assert torch.isfinite(got).all()
+    assert bool((err <= bound).all()), f"max err {err.max().item():.3g}"
+
+
+# --------------------------------------------------------------------------- quantise/dequantise
+def test_dequant_bit_exact_golden():
+    from hydranet_amd.kernels.int4_gemm import dequantize_int4
+    z = np.load(os.path.join(GOLD, "quantize_tensor.npz"), allow_pickle=False)
+    for n in sorted({k.split("/")[0] for k in z.files}):
+        g = int(z[f"{n}/group"])
+        p = torch.from_numpy(z[f"{n}/packed"]).to(DEV)
+        s = torch.from_numpy(_f16(z[f"{n}/scales"]).copy()).to(DEV)
+        got = dequantize_int4(p, s, g).cpu().numpy().view(np.uint16)
+        np.testing.assert_array_equal(got, z[f"{n}/dequant"], err_msg=n)
+
+
+def test_dequant_bit_exact_random_scales_incl_subnormal():
+    from hydranet_amd.kernels.int4_gemm import dequantize_int4
+    rng = np.random.default_rng(0)
+    N, K, g = 257, 512, 128
+    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sbits = rng.integers(0, 0x7C00, (N, K // g), dtype=np.uint16)  # finite, incl. subnormal
+    sbits[:, 0] |= (rng.integers(0, 2, N) << 15).astype(np.uint16)  # some negative scales
+    s = sbits.view(np.float16)
+    ref = oracle.dequant(packed, s, g)
+    got = dequantize_int4(torch.from_numpy(packed).to(DEV), torch.from_numpy(s.copy()).to(DEV), g)
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_quantize_bit_exact_golden_both_modes():
+    from hydranet_amd.kernels.int4_gemm import quantize_int4
+    z = np.load(os.path.join(GOLD, "quantize_tensor.npz"), allow_pickle=False)
+    for n in sorted({k.split("/")[0] for k in z.files}):
+        w = torch.from_numpy(_f16(z[f"{n}/w"]).copy()).to(DEV)
+        p, s = quantize_int4(w, int(z[f"{n}/group"]), mode=0)
+        np.testing.assert_array_equal(p.cpu().numpy(), z[f"{n}/packed"], err_msg=n)
+        np.testing.assert_array_equal(s.cpu().numpy().view(np.uint16), z[f"{n}/scales"], err_msg=n)
+    z = np.load(os.path.join(GOLD, "quantize_weight.npz"), allow_pickle=False)
+    for key in sorted({k.split("/")[0] for k in z.files}):
+        w = z[f"{key}/w"]
+        w = torch.from_numpy(_f16(w).copy() if key.startswith("f16") else w.copy()).to(DEV)
+        p, s = quantize_int4(w, int(key.split("_g")[1]), mode=1)
+        np.testing.assert_array_equal(p.cpu().numpy(), z[f"{key}/packed"], err_msg=key)
+        np.testing.assert_array_equal(s.cpu().numpy().view(np.uint16), z[f"{key}/scales"],
+                                      err_msg=key)
+
+
+def test_quantize_bit_exact_random_large():
+    from hydranet_amd.kernels.int4_gemm import quantize_int4
+    w = _rand_f16(3, (512, 4096), 0.02)
+    pr, sr = oracle.quantize(w.numpy(), 128, mode=0)
+    p, s = quantize_int4(w.to(DEV), 128, mode=0)
+    np.testing.assert_array_equal(p.cpu().numpy(), pr)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint16), sr.view(np.uint16))
+
+
+# --------------------------------------------------------------------------- int4_linear
+@pytest.mark.parametrize("M,N,K,g", [(1, 64, 256, 128), (1, 4096, 4096, 128), (2, 80, 512, 128),
+                                     (4, 1408, 4096, 128), (16, 272, 1024, 128),
+                                     (17, 96, 384, 128), (33, 48, 256, 128), (3, 64, 256, 64),
+                                     (5, 48, 256, 32), (1, 4096, 1408, 128), (8, 32, 160, 32)])
+def test_int4_linear_vs_oracle(M, N, K, g):
+    from hydranet_amd.kernels.int4_gemm import int4_linear
+    w = _rand_f16(M * 7 + N, (N, K), 0.02)
+    x = _rand_f16(M + K, (M, K), 1.0)
+    p, s = oracle.quantize(w.numpy(), g, mode=0)
+    ref = torch.from_numpy(oracle.int4_linear(x.numpy(), p, s, g).astype(np.float32))
+    got = int4_linear(x.to(DEV), torch.from_numpy(p).to(DEV), torch.from_numpy(s.copy()).to(DEV), g)
+    assert got.shape == (M, N) and got.dtype == torch.float16
+    _close(got, ref)
+    # and vs a plain fp32 reference of the dequantised weights
+    deq = torch.from_numpy(oracle.dequant(p, s, g).astype(np.float32))
+    _close(got, x.float() @ deq.t())
+
+
+def test_int4_linear_3d_and_shape_asserts():
+    from hydranet_amd.kernels import int4_gemm, int4_expert_mlp
+    w = _rand_f16(1, (64, 256), 0.02)
+    p, s = oracle.quantize(w.numpy(), 128)
+    pd, sd = torch.from_numpy(p).to(DEV), torch.from_numpy(s.copy()).to(DEV)
+    x = _rand_f16(2, (2, 3, 256)).to(DEV)
+    y = int4_gemm.int4_linear(x, pd, sd)
+    assert y.shape == (2, 3, 64)
+    y2 = int4_expert_mlp.int4_linear(x, pd, sd)
+    assert torch.equal(y, y2)
+    with pytest.raises(AssertionError):
+        int4_gemm.int4_linear(x[..., :128], pd, sd)
+    with pytest.raises(AssertionError):
+        int4_expert_mlp.int4_linear(x, pd[:, :64], sd)
+
+
+def test_silu_mul_vs_oracle():
+    from hydranet_amd.kernels.int4_gemm import fused_silu_mul
+    from hydranet_amd.kernels.int4_expert_mlp import silu_mul
+    g = _rand_f16(5, (3, 1000), 2.0)
+    u = _rand_f16(6, (3, 1000), 1.0)
+    ref = (torch.nn.functional.silu(g.float()) * u.float()).half()
+    got = fused_silu_mul(g.to(DEV), u.to(DEV))
+    assert (got.cpu().float() - ref.float()).abs().max() <= 1e-3
+    got3 = silu_mul(g.view(1, 3, 1000).to(DEV), u.view(1, 3, 1000).to(DEV))
+    assert torch.equal(got3.view(3, 1000), got)
+
+
+# --------------------------------------------------------------------------- expert MLP
+def test_expert_mlp_vs_reference_golden():
+    from hydranet_amd.kernels import expert_mlp_int4_fused
+    z = np.load(os.path.join(GOLD, "expert_mlp.npz"), allow_pickle=False)
+    H, I, gs = (int(v) for v in z["dims"])
+    t = {k: torch.from_numpy(z[k]).to(DEV) for k in ("gate_packed", "up_packed", "down_packed")}
+    for k in ("gate_scales", "up_scales", "down_scales", "x"):
+        t[k] = torch.from_numpy(_f16(z[k]).copy()).to(DEV)
+    y = expert_mlp_int4_fused(t["x"], t["gate_packed"], t["gate_scales"], t["up_packed"],
+                              t["up_scales"], t["down_packed"], t["down_scales"], gs)
+    _close(y, torch.from_numpy(_f16(z["y"]).astype(np.float32)))
+
+
+def _expert(seed, H, I, g=128):
+    ws = [_rand_f16(seed * 10 + i, shp, 0.02) for i, shp in enumerate([(I, H), (I, H), (H, I)])]
+    out = []
+    for w in ws:
+        p, s = oracle.quantize(w.numpy(), g, mode=0)
+        out += [torch.from_numpy(p), torch.from_numpy(s.copy())]
+    return out  # gp, gs, up, us, dp, ds (CPU)
+
+
+@pytest.mark.parametrize("T,H,I", [(1, 4096, 14336), (4, 4096, 1408), (16, 512, 1024),
+                                   (3, 256, 384)])
+def test_expert_mlp_vs_torch_ref(T, H, I):
+    from hydranet_amd.kernels import expert_mlp_int4_fused
+    from hydranet_amd.kernels.int4_expert_mlp import expert_mlp_int4_from_slot
+    e = _expert(T + H, H, I)
+    x = _rand_f16(1234, (T, H), 1.0)
+    ref = torch_ref.expert_mlp(x, *e, group_size=128)
+    ed = [t.to(DEV) for t in e]
+    got = expert_mlp_int4_fused(x.to(DEV), *ed, group_size=128)
+    assert got.shape == (T, H)
+    _close(got, ref)
+
+    class Slot:
+        pass
+    slot = Slot()
+    for name, t in zip(("gate_packed", "gate_scales", "up_packed", "up_scales", "down_packed",
+                        "down_scales"), ed):
+        setattr(slot, name, t)
+    got2 = expert_mlp_int4_from_slot(x.to(DEV), slot, 128)
+    assert torch.equal(got, got2)
+
+
+def test_expert_mlp_zero_tokens():
+    from hydranet_amd.kernels import expert_mlp_int4_fused
+    e = [t.to(DEV) for t in _expert(9, 256, 384)]
+    y = expert_mlp_int4_fused(torch.empty(0, 256, dtype=torch.float16, device=DEV), *e)
+    assert y.shape == (0, 256)
+
+
+def test_int4linear_module():
+    from hydranet_amd.kernels import Int4Linear
+    lin = torch.nn.Linear(256, 96, bias=True).half()
+    q = Int4Linear.from_float(lin, group_size=128, device=torch.device(DEV))
+    p, s = oracle.quantize(lin.weight.data.numpy(), 128, mode=1)
+    np.testing.assert_array_equal(q.weight_packed.cpu().numpy(), p)
+    x = _rand_f16(8, (4, 256))
+    ref = oracle.int4_linear(x.numpy(), p, s, 128).astype(np.float32) + \
+        lin.bias.data.float().numpy()
+    got = q(x.to(DEV))
+    _close(got, torch.from_numpy(ref))
