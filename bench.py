@@ -92,6 +92,7 @@ def bench_c1(args):
 
     outs = [torch.empty(T, H, dtype=torch.float16, device="cuda") for _ in range(n_exp)]
     hws = [torch.empty(T, I, dtype=torch.float16, device="cuda") for _ in range(n_exp)]
+    work = _lib.skinny_workspace(2, T, H, I, 0, "cuda")
     state = {"i": 0}
 
     def step():
@@ -100,7 +101,8 @@ def bench_c1(args):
         sl = slots[e]
         _lib.call("hn_expert_mlp_int4", _lib.ptr(x), *[_lib.ptr(t) for t in (
             sl.gate_packed, sl.gate_scales, sl.up_packed, sl.up_scales, sl.down_packed,
-            sl.down_scales)], _lib.ptr(outs[e]), T, H, I, g, _lib.ptr(hws[e]), _lib.stream())
+            sl.down_scales)], _lib.ptr(outs[e]), T, H, I, g, _lib.ptr(hws[e]), _lib.ptr(work),
+            work.numel(), _lib.stream())
 
     # parity of the product entry point vs the CPU oracle on expert 0
     y_gpu = expert_mlp_int4_fused(x, slots[0].gate_packed, slots[0].gate_scales,
@@ -134,7 +136,8 @@ def bench_c1(args):
         sl = slots[e]
         _lib.call("hn_int4_gate_up_silu", _lib.ptr(x), H, _lib.ptr(sl.gate_packed),
                   _lib.ptr(sl.gate_scales), _lib.ptr(sl.up_packed), _lib.ptr(sl.up_scales),
-                  H // 2, H // g, _lib.ptr(hws[e]), I, T, I, H, g, _lib.stream())
+                  H // 2, H // g, _lib.ptr(hws[e]), I, T, I, H, g, _lib.ptr(work), work.numel(),
+                  _lib.stream())
 
     def down_only():
         e = state["i"] % n_exp
@@ -142,7 +145,7 @@ def bench_c1(args):
         sl = slots[e]
         _lib.call("hn_int4_linear", _lib.ptr(hws[e]), I, _lib.ptr(sl.down_packed), I // 2,
                   _lib.ptr(sl.down_scales), I // g, _lib.ptr(outs[e]), H, T, H, I, g,
-                  _lib.stream())
+                  _lib.ptr(work), work.numel(), _lib.stream())
 
     kt = {}
     for name, fn in (("gate_up_silu", gate_up_only), ("down", down_only)):
@@ -164,7 +167,7 @@ def bench_c1(args):
                                f"T={T}", "tokens": T, "hidden": H, "intermediate": I,
                    "group_size": g, "experts_rotated": n_exp, "bytes_per_step": bytes_step,
                    "graph": gr is not None},
-        "roofline": {"bound": "hbm", "kernel": "skinny_kernel<2,8,1,false,16> (gate+up+SiLU)",
+        "roofline": {"bound": "hbm", "kernel": "skinny_kernel<2,1,false,1,1> (gate+up+SiLU)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": gu_bytes, "avg_us": round(kt["gate_up_silu"] * 1e3, 3),
@@ -173,6 +176,61 @@ def bench_c1(args):
                      "expert_frac": round(bytes_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
     }
     return result, (slots[0], x, y_gpu, g)
+
+
+# ----------------------------------------------------------------------------- C2
+def bench_c2(args, T: int, n_layers: int = 4):
+    """One Mixtral MoE layer at decode: router + permute + grouped SwiGLU + unpermute.
+    Steps rotate over n_layers layers of 8 experts (2.9 GB for 4 layers)."""
+    from hydranet_amd import _lib
+    from hydranet_amd.model.moe import MixtralMoELayer, ExpertTable
+    from hydranet_amd.model.router import mixtral_route
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
+
+    H, I, g, E = 4096, 14336, 128, 8
+    layers = []
+    for L in range(n_layers):
+        slots = [make_expert_slot(expert_seed(L, e), H, I, g, slot_idx=e) for e in range(E)]
+        layer = MixtralMoELayer(H, E, 2, layer_idx=L, slots=slots).cuda()
+        layer.router.gate.weight.data = normal_f16((E, H), 7000 + L)
+        layers.append(layer)
+    x = normal_f16((1, T, H), 1234 + T, std=1.0)
+    blob = layers[0].experts.table.slots[0].layout.total_size
+    # algorithmic bytes per layer step: unique experts' blobs + gate + x + y
+    step_bytes = []
+    for layer in layers:
+        idx, _, _ = mixtral_route(x.view(T, H), layer.router.gate.weight, 2)
+        uniq = int(torch.unique(idx).numel())
+        step_bytes.append(uniq * blob + E * H * 2 + 2 * T * H * 2)
+    state = {"i": 0}
+
+    def step():
+        layer = layers[state["i"] % n_layers]
+        state["i"] += 1
+        layer(x, top_k=2)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    chunk = _chunk(args.steps)
+    state["i"] = 0
+    gr = _graph(step, chunk)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    if gr is not None:
+        for _ in range(args.steps // chunk):
+            gr.replay()
+    else:
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    total_bytes = sum(step_bytes[i % n_layers] for i in range(args.steps))
+    gbs = total_bytes / (ms * 1e-3 * args.steps) / 1e9
+    return {"tokens": T, "ms_per_step": round(ms, 5), "GB_s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+            "avg_unique_experts": sum((b - E * H * 2 - 4 * T * H) // blob for b in step_bytes)
+            / n_layers, "graph": gr is not None}
 
 
 def cpu_baseline_c1(ctx, budget_s: float):
@@ -221,7 +279,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c1", choices=["c1"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2"])
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -238,11 +296,29 @@ def main():
     torch.cuda.set_device(0)
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
     res, ctx = bench_c1(args)
-    _log("gpu done", res["value"], res["unit"])
+    _log("c1 done", res["value"], res["unit"])
+    c1 = {"GB_s": res["value"], "frac": res["roofline"]["expert_frac"],
+          "ms_per_step": res["ms_per_step"], "tokens_per_s": res["tokens_per_s"]}
     cpu = None
     if not args.no_cpu:
         cpu, parity = cpu_baseline_c1(ctx, args.cpu_budget)
         res["parity"] = parity
+    if args.workload == "c2":
+        sweep = {}
+        for T in (1, 4, 16):
+            sweep[f"T{T}"] = bench_c2(args, T)
+            _log("c2", T, sweep[f"T{T}"])
+        head = sweep["T16"]
+        res["metric"] = METRIC
+        res["value"] = head["GB_s"]
+        res["ms_per_step"] = head["ms_per_step"]
+        res["tokens_per_s"] = head["tokens_per_s"]
+        res["config"] = {"workload": "C2: one Mixtral MoE layer at decode (8 experts "
+                                     "4096->14336->4096 INT4 g128, softmax top-2), T=16 tokens; "
+                                     "router + permute + grouped SwiGLU + unpermute",
+                         "tokens": 16, "experts": 8, "top_k": 2, "layers_rotated": 4,
+                         "sweep": sweep, "c1_single_expert_T1": c1,
+                         "graph": head["graph"]}
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",

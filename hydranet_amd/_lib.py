@@ -24,17 +24,20 @@ F = ctypes.c_float
 SIGNATURES: dict[str, list] = {
     "hn_int4_dequant": [P, L, P, L, P, L, L, L, L, P],
     "hn_int4_quantize": [P, L, I, I, P, L, P, L, L, L, L, P],
-    "hn_int4_linear": [P, L, P, L, P, L, P, L, L, L, L, L, P],
-    "hn_int4_gate_up_silu": [P, L, P, P, P, P, L, L, P, L, L, L, L, L, P],
-    "hn_expert_mlp_int4": [P, P, P, P, P, P, P, P, L, L, L, L, P, P],
+    "hn_skinny_workspace_bytes": [I, L, L, L, L],
+    "hn_int4_linear": [P, L, P, L, P, L, P, L, L, L, L, L, P, L, P],
+    "hn_int4_gate_up_silu": [P, L, P, P, P, P, L, L, P, L, L, L, L, L, P, L, P],
+    "hn_expert_mlp_int4": [P, P, P, P, P, P, P, P, L, L, L, L, P, P, L, P],
     "hn_silu_mul": [P, L, P, L, P, L, L, L, P],
     "hn_router_logits": [P, L, P, L, I, P, L, L, L, P],
     "hn_router_topk": [P, P, L, L, L, I, F, F, P, P, P],
     "hn_moe_permute": [P, L, L, L, P, P, P, P, P, P],
     "hn_moe_gather": [P, L, P, L, P, L, P, L, L, L, P],
     "hn_moe_unpermute": [P, L, P, P, P, L, L, P, L, P, L, L, P],
-    "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, P, P, P],
+    "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],
 }
+
+RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long}
 
 _lib = None
 
@@ -52,7 +55,7 @@ def lib() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(h, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         _lib = h
     return _lib
 
@@ -62,6 +65,27 @@ def call(name: str, *args) -> None:
     if rc != 0:
         msg = lib().hn_last_error_string().decode(errors="replace")
         raise RuntimeError(f"{name} failed (rc={rc}): {msg}")
+
+
+_WORKSPACES: dict = {}
+
+
+def workspace(nbytes: int, device) -> torch.Tensor:
+    """Zero-filled scratch for the split-K counters and partials, cached per
+    device and grown on demand.  The kernels leave the counters at zero, so
+    the buffer is only filled once per allocation.  Calls that share a device
+    run in stream order; concurrent calls on different streams would race."""
+    dev = torch.device(device)
+    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+def skinny_workspace(kind: int, M: int, N: int, K: int, E: int, device) -> torch.Tensor:
+    return workspace(lib().hn_skinny_workspace_bytes(kind, M, N, K, E), device)
 
 
 def ptr(t) -> ctypes.c_void_p:

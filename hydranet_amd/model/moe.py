@@ -1,0 +1,204 @@
+"""MoE layers over the grouped gfx950 INT4 kernels.
+
+``moe_experts_forward`` replaces the per-expert Python loop of
+MixtralMoELayer.forward (model/mixtral.py:290-370) and GLM4MoELayer.forward
+(model/glm4.py:385-473):
+
+  reference (per layer)                     here (per layer, no host sync)
+  unique().tolist()          (D2H)          hn_moe_permute: counts, offsets, stable
+  for e: where(idx == e)     (D2H x2)         permutation, active list (one WG)
+         x[tok]; 4 launches                 hn_moe_gather: x_perm
+         index_add_(fp16)                   hn_grouped_expert_mlp_int4: 2 launches over
+                                              every active expert
+                                            hn_moe_unpermute: fp16 index_add_ order
+
+Expert weights come from a device table of slab pointers, one row per expert
+(``ExpertTable``), built once when every expert is resident.  If a cache
+manager holds only some experts, the active experts are fetched to the host
+(one D2H), made resident through the manager (its get_int4_slot records
+hits/misses and loads misses), and the table is refreshed for that call.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import _lib
+from .router import GLM4SigmoidRouter, TopKRouter
+
+
+class ExpertTable:
+    """Device table [E, 6] u64: gate_q, gate_s, up_q, up_s, down_q, down_s per expert."""
+
+    def __init__(self, num_experts: int, device):
+        self.num_experts = num_experts
+        self.device = torch.device(device)
+        self.host = torch.zeros((num_experts, 6), dtype=torch.int64)
+        self.dev = torch.zeros((num_experts, 6), dtype=torch.int64, device=self.device)
+        self.slots = [None] * num_experts
+        self.dims = None
+
+    def set(self, e: int, slot) -> None:
+        dims = (slot.hidden_dim, slot.intermediate_dim, slot.group_size)
+        if self.dims is None:
+            self.dims = dims
+        elif self.dims != dims:
+            raise ValueError(f"expert {e} dims {dims} != table dims {self.dims}")
+        self.slots[e] = slot
+        self.host[e] = torch.tensor(slot.data_ptrs(), dtype=torch.int64)
+
+    def upload(self) -> None:
+        self.dev.copy_(self.host)
+
+    @classmethod
+    def from_slots(cls, slots: Sequence, device=None) -> "ExpertTable":
+        t = cls(len(slots), device or slots[0].device)
+        for e, s in enumerate(slots):
+            t.set(e, s)
+        t.upload()
+        return t
+
+
+def moe_experts_forward(hidden: torch.Tensor, idx: torch.Tensor, w: torch.Tensor,
+                        table: ExpertTable, shared: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[T, H] = (shared +) sum_k w[t, k] * expert_{idx[t, k]}(hidden[t]).
+
+    hidden [T, H] fp16; idx [T, k] int32; w [T, k] fp16; all on the GPU.
+    Accumulation follows the reference: per expert fp16(y * w), added in
+    ascending expert order into an fp16 buffer."""
+    _lib.require_gpu(hidden, idx, w)
+    T, H = hidden.shape
+    k = idx.shape[1]
+    E = table.num_experts
+    Ht, I, g = table.dims
+    assert Ht == H, f"hidden {H} != expert hidden {Ht}"
+    dev = hidden.device
+    st = _lib.stream(dev)
+    x = _lib.aligned_rows(hidden.to(torch.float16))
+    idx32 = idx.to(torch.int32).contiguous()
+    wt = w.to(torch.float16).contiguous()
+    n = T * k
+    meta = torch.empty(3 * E + 2 + 2 * max(n, 1), dtype=torch.int32, device=dev)
+    offsets = meta[: E + 1]
+    active = meta[E + 1: 2 * E + 1]
+    n_active = meta[2 * E + 1: 2 * E + 2]
+    perm = meta[2 * E + 2: 2 * E + 2 + max(n, 1)]
+    inv = meta[2 * E + 2 + max(n, 1): 2 * E + 2 + 2 * max(n, 1)]
+    _lib.call("hn_moe_permute", _lib.ptr(idx32), T, k, E, _lib.ptr(offsets), _lib.ptr(perm),
+              _lib.ptr(inv), _lib.ptr(active), _lib.ptr(n_active), st)
+    x_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
+    _lib.call("hn_moe_gather", _lib.ptr(x), x.stride(0), _lib.ptr(perm), k, _lib.ptr(offsets), E,
+              _lib.ptr(x_perm), H, n, H, st)
+    h_ws = torch.empty((max(n, 1), I), dtype=torch.float16, device=dev)
+    y_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
+    work = _lib.skinny_workspace(3, n, H, I, E, dev)
+    _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(x_perm), _lib.ptr(table.dev),
+              _lib.ptr(active), _lib.ptr(n_active), _lib.ptr(offsets), E, T, n, H, I, g,
+              _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work), work.numel(), st)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    sh = None
+    if shared is not None:
+        sh = _lib.aligned_rows(shared.reshape(T, H).to(torch.float16))
+    _lib.call("hn_moe_unpermute", _lib.ptr(y_perm), H, _lib.ptr(inv), _lib.ptr(idx32),
+              _lib.ptr(wt), T, k, _lib.ptr(sh), H if sh is None else sh.stride(0), _lib.ptr(out), H,
+              H, st)
+    return out
+
+
+class _ResidentExperts:
+    """Expert source for a layer: fixed slots, or a cache manager (offload case)."""
+
+    def __init__(self, num_experts: int, layer_idx: int, slots=None, cache_manager=None):
+        self.num_experts = num_experts
+        self.layer_idx = layer_idx
+        self.cache_manager = cache_manager
+        self.table: Optional[ExpertTable] = None
+        if slots is not None:
+            self.table = ExpertTable.from_slots(slots)
+
+    def table_for(self, idx: torch.Tensor) -> ExpertTable:
+        cm = self.cache_manager
+        if cm is None:
+            return self.table
+        if self.table is None:
+            self.table = ExpertTable(self.num_experts, idx.device)
+        needed = torch.unique(idx).tolist()  # one D2H when experts may be missing
+        hits = [e for e in needed if cm.is_cached(self.layer_idx, e)]
+        misses = [e for e in needed if e not in hits]
+        for e in misses:  # start the loads of misses before touching hits
+            cm.prefetch_int4_slot(self.layer_idx, e)
+        for e in hits + misses:
+            self.table.set(e, cm.get_int4_slot(self.layer_idx, e))
+        self.table.upload()
+        return self.table
+
+
+class MixtralMoELayer(nn.Module):
+    """Mixtral sparse-MoE block (model/mixtral.py:232-370) on the grouped kernels."""
+
+    def __init__(self, hidden_dim: int = 4096, num_experts: int = 8, experts_per_token: int = 2,
+                 layer_idx: int = 0, slots=None, cache_manager=None,
+                 enable_affinity_bonus: bool = False):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.num_experts = num_experts
+        self.router = TopKRouter(hidden_dim, num_experts, experts_per_token,
+                                 enable_affinity_bonus=enable_affinity_bonus)
+        self.experts = _ResidentExperts(num_experts, layer_idx, slots, cache_manager)
+        if cache_manager is not None:
+            self.router.set_cache_checker(lambda e: cache_manager.is_cached(layer_idx, e))
+
+    def forward(self, hidden_states: torch.Tensor, top_k: int = 2) -> torch.Tensor:
+        B, S, H = hidden_states.shape
+        ro = self.router(hidden_states, top_k_override=top_k)
+        flat = hidden_states.reshape(B * S, H)
+        idx = ro.expert_indices.reshape(B * S, top_k)
+        table = self.experts.table_for(idx)
+        out = moe_experts_forward(flat, idx, ro.expert_weights.reshape(B * S, top_k), table)
+        return out.view(B, S, H)
+
+
+class GLM4DenseMLP(nn.Module):
+    """fp16 dense SwiGLU (model/glm4.py:220-235); shared expert of GLM4MoELayer."""
+
+    def __init__(self, hidden_dim: int, intermediate_dim: int):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_dim, intermediate_dim, bias=False)
+        self.up_proj = nn.Linear(hidden_dim, intermediate_dim, bias=False)
+        self.down_proj = nn.Linear(intermediate_dim, hidden_dim, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class GLM4MoELayer(nn.Module):
+    """GLM-4.5-Air MoE block (model/glm4.py:312-473): fp16 shared expert plus
+    routed INT4 experts, out = shared + routed (fp16 add fused into unpermute)."""
+
+    def __init__(self, hidden_dim: int = 4096, moe_intermediate_dim: int = 1408,
+                 num_experts: int = 128, experts_per_token: int = 8, layer_idx: int = 0,
+                 slots=None, cache_manager=None, routed_scaling_factor: float = 1.0):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.router = GLM4SigmoidRouter(hidden_dim, num_experts, experts_per_token,
+                                        routed_scaling_factor=routed_scaling_factor)
+        self.shared_expert = GLM4DenseMLP(hidden_dim, moe_intermediate_dim)
+        self.experts = _ResidentExperts(num_experts, layer_idx, slots, cache_manager)
+        self._last_selected_experts: list = []
+
+    def get_last_selected_experts(self) -> list:
+        return self._last_selected_experts
+
+    def forward(self, hidden_states: torch.Tensor, skip_routed: bool = False) -> torch.Tensor:
+        B, S, H = hidden_states.shape
+        shared = self.shared_expert(hidden_states)
+        if skip_routed:
+            return shared
+        idx, w = self.router(hidden_states)
+        table = self.experts.table_for(idx)
+        out = moe_experts_forward(hidden_states.reshape(B * S, H), idx, w, table,
+                                  shared=shared.reshape(B * S, H))
+        return out.view(B, S, H)

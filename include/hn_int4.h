@@ -39,26 +39,36 @@ int hn_int4_dequant(const void* packed, long ld_p, const void* scales, long ld_s
 int hn_int4_quantize(const void* w, long ld_w, int dtype, int mode, void* packed, long ld_p,
                      void* scales, long ld_s, long N, long K, long group, void* stream);
 
+/* Workspace bytes for the skinny (decode) kernels below.  kind 0: hn_int4_linear
+ * (M, N, K); 1: hn_int4_gate_up_silu (M, N=I, K=H); 2: hn_expert_mlp_int4
+ * (M=T, N=H, K=I); 3: hn_grouped_expert_mlp_int4 (M=rows, N=H, K=I, E).  The
+ * workspace must be zero-filled once when allocated; the kernels leave its
+ * counters at zero.  Calls that run concurrently need distinct workspaces.
+ * No counterpart in the reference (Triton needs no split-K workspace). */
+long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long E);
+
 /* out[M, N] = fp16(x[M, K] @ deq(W)^T), fp32 accumulation.  Replaces the
  * int4_matmul_kernel launch in int4_gemm.int4_linear (kernels/int4_gemm.py:124-172)
  * and int4_expert_mlp.int4_linear (kernels/int4_expert_mlp.py:99-156).
  * K % 32 == 0, group a multiple of 32 dividing K, 16-byte aligned rows. */
 int hn_int4_linear(const void* x, long ld_x, const void* wq, long ld_q, const void* ws, long ld_s,
-                   void* out, long ld_o, long M, long N, long K, long group, void* stream);
+                   void* out, long ld_o, long M, long N, long K, long group, void* work,
+                   long work_bytes, void* stream);
 
 /* h[M, N] = fp16(silu(fp16(x @ deq(Wg)^T)) * fp16(x @ deq(Wu)^T)): the gate and up
  * projections of expert_mlp_int4_fused plus fused_silu_mul
  * (kernels/int4_gemm.py:175-208, 241-247) in one launch. */
 int hn_int4_gate_up_silu(const void* x, long ld_x, const void* gq, const void* gs, const void* uq,
                          const void* us, long ld_q, long ld_s, void* h, long ld_h, long M, long N,
-                         long K, long group, void* stream);
+                         long K, long group, void* work, long work_bytes, void* stream);
 
 /* out[T, H] = down(silu(gate(x)) * up(x)) for one expert; h_ws is a [T, I] fp16
  * workspace.  Replaces int4_gemm.expert_mlp_int4_fused (kernels/int4_gemm.py:211-254)
  * and int4_expert_mlp.expert_mlp_int4 (kernels/int4_expert_mlp.py:213-252). */
 int hn_expert_mlp_int4(const void* x, const void* gq, const void* gs, const void* uq,
                        const void* us, const void* dq, const void* ds, void* out, long T, long H,
-                       long I, long group, void* h_ws, void* stream);
+                       long I, long group, void* h_ws, void* work, long work_bytes,
+                       void* stream);
 
 /* out = fp16(silu(float(g)) * float(u)).  Replaces fused_silu_mul / silu_mul
  * (kernels/int4_gemm.py:196-208, kernels/int4_expert_mlp.py:189-210). */
@@ -98,16 +108,18 @@ int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* i
                      long T, long k, const void* shared, long ld_sh, void* out, long ld_o, long H,
                      void* stream);
 
-/* Grouped SwiGLU over every active expert of one MoE layer in two launches.
- * x_perm [rows, H] sorted by expert; table: E x {gate_q, gate_s, up_q, up_s,
- * down_q, down_s} device pointers (u64); active / n_active / offsets from
- * hn_moe_permute; h_ws [rows, I] fp16 workspace; y_perm [rows, H] fp16 out.
+/* Grouped SwiGLU over every active expert of one MoE layer in two launches
+ * (<= 64 rows per expert).  x_perm [rows, H] sorted by expert; table: E x
+ * {gate_q, gate_s, up_q, up_s, down_q, down_s} device pointers (u64); active /
+ * n_active / offsets from hn_moe_permute; h_ws [rows, I] fp16 buffer;
+ * y_perm [rows, H] fp16 out; work: hn_skinny_workspace_bytes(3, rows, H, I, E).
  * Replaces the per-expert loop calling expert_mlp_int4_fused
  * (model/mixtral.py:327-354, model/glm4.py:421-455). */
 int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int* active,
-                               const int* n_active, const int* offsets, long E_max,
-                               long max_rows_per_expert, long H, long I, long group, void* h_ws,
-                               void* y_perm, void* stream);
+                               const int* n_active, const int* offsets, long E,
+                               long max_rows_per_expert, long rows, long H, long I, long group,
+                               void* h_ws, void* y_perm, void* work, long work_bytes,
+                               void* stream);
 
 #ifdef __cplusplus
 }

@@ -37,12 +37,23 @@ def test_ctypes_table_matches_header():
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
 
 
+def test_workspace_query():
+    from hydranet_amd import _lib
+    h = _lib.lib()
+    # C1 expert: gate/up splits K=4096 in 4 chunks -> partials for 2 matrices
+    b = h.hn_skinny_workspace_bytes(2, 1, 4096, 14336, 0)
+    assert b >= 4 * 2 * 14336 * 4
+    # a small single-chunk problem needs only the counter region
+    assert h.hn_skinny_workspace_bytes(0, 1, 64, 256, 0) == 256
+
+
 def test_argument_errors_raise_without_gpu():
     # rejected arguments return before any HIP call
     from hydranet_amd import _lib
     import pytest
     with pytest.raises(RuntimeError, match="multiple of 32"):
-        _lib.call("hn_int4_linear", None, 8, None, 16, None, 1, None, 8, 1, 1, 48, 16, None)
+        _lib.call("hn_int4_linear", None, 8, None, 16, None, 1, None, 8, 1, 1, 48, 16, None, 0,
+                  None)
     with pytest.raises(RuntimeError, match="mode must be"):
         _lib.call("hn_router_topk", None, None, 1, 8, 2, 5, ctypes.c_float(0), ctypes.c_float(1),
                   None, None, None)

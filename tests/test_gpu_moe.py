@@ -1,0 +1,243 @@
+"""GPU parity of the MoE routing/dispatch path against the CPU oracle.
+
+Bit-exact: router top-k indices given the same logits, the permutation
+(offsets / perm / inv / active list), the gathered rows, the unpermute
+accumulation given the same expert outputs.  Tolerance (max-abs 1e-2,
+rel 2e-3): logits-derived weights (1 fp16 ulp), expert MLP outputs and MoE
+layer outputs.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import torch_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _f16(bits):
+    return np.asarray(bits, dtype=np.uint16).view(np.float16)
+
+
+def _close(got, ref, atol=1e-2, rtol=2e-3):
+    got = got.float().cpu()
+    ref = ref.float().cpu()
+    err = (got - ref).abs()
+    assert torch.isfinite(got).all()
+    assert bool((err <= atol + rtol * ref.abs()).all()), f"max err {err.max().item():.3g}"
+
+
+def _randn(seed, shape, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).half()
+
+
+# --------------------------------------------------------------------------- routers
+@pytest.mark.parametrize("T", [1, 4, 16, 2048])
+def test_mixtral_router_vs_oracle(T):
+    from hydranet_amd.model.router import mixtral_route, topk_from_logits
+    h = _randn(T, (T, 4096))
+    gate = _randn(99, (8, 4096), 0.02)
+    idx, w, logits = mixtral_route(h.to(DEV), gate.to(DEV), 2)
+    lg_ref = oracle.router_logits(h.numpy(), gate.numpy())
+    _close(logits, torch.from_numpy(lg_ref), atol=2e-3, rtol=2e-3)
+    # indices are pinned given identical logits
+    lg = logits.cpu().numpy()
+    idx_ref, w_ref = oracle.router_topk(lg, 2, mode=0)
+    np.testing.assert_array_equal(idx.cpu().numpy(), idx_ref)
+    np.testing.assert_allclose(w.cpu().float().numpy(), w_ref.astype(np.float32), atol=1e-3)
+    np.testing.assert_allclose(w.cpu().float().sum(-1).numpy(), 1.0, atol=2e-3)
+
+
+def test_router_topk_golden_and_ties():
+    from hydranet_amd.model.router import topk_from_logits
+    z = np.load(os.path.join(GOLD, "topk_router.npz"), allow_pickle=False)
+    for k in (1, 2):
+        lg = z[f"k{k}/logits"].reshape(-1, 8)
+        idx, w = topk_from_logits(torch.from_numpy(lg).to(DEV), k, 0)
+        idx_o, w_o = oracle.router_topk(lg, k, mode=0)
+        np.testing.assert_array_equal(idx.cpu().numpy(), idx_o)  # lower index wins ties
+        ref = z[f"k{k}/idx"].reshape(-1, k)
+        srt = -np.sort(-lg, axis=1)
+        tie_free = srt[:, k - 1] != srt[:, k]
+        np.testing.assert_array_equal(idx.cpu().numpy()[tie_free], ref[tie_free])
+        np.testing.assert_allclose(w.cpu().float().numpy(),
+                                   _f16(z[f"k{k}/w"]).reshape(-1, k).astype(np.float32), atol=1e-3)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_glm_router_vs_oracle(bias):
+    from hydranet_amd.model.router import glm_route
+    T = 32
+    h = _randn(5, (T, 4096))
+    g = torch.Generator().manual_seed(6)
+    w = torch.randn(128, 4096, generator=g) * 0.02
+    b = (torch.rand(128, generator=g) * 0.2 - 0.1) if bias else None
+    idx, wt, logits = glm_route(h.to(DEV), w.to(DEV), 8, bias=None if b is None else b.to(DEV))
+    lg_ref = torch.nn.functional.linear(h.float(), w).numpy()
+    _close(logits, torch.from_numpy(lg_ref), atol=1e-4, rtol=1e-4)
+    idx_o, w_o = oracle.router_topk(logits.cpu().numpy(), 8, mode=1,
+                                    bias=None if b is None else b.numpy())
+    np.testing.assert_array_equal(idx.cpu().numpy(), idx_o)
+    np.testing.assert_allclose(wt.cpu().float().numpy(), w_o.astype(np.float32), atol=1e-3)
+    np.testing.assert_allclose(wt.cpu().float().sum(-1).numpy(), 1.0, atol=1e-2)
+
+
+def test_sigmoid_router_golden():
+    from hydranet_amd.model.router import GLM4SigmoidRouter
+    z = np.load(os.path.join(GOLD, "sigmoid_router.npz"), allow_pickle=False)
+    r = GLM4SigmoidRouter(256, 128, 8).to(DEV)
+    r.weight.data = torch.from_numpy(z["w"]).to(DEV)
+    h = torch.from_numpy(_f16(z["h"]).copy()).view(1, 32, 256).to(DEV)
+    idx, w = r(h)
+    np.testing.assert_array_equal(idx.cpu().numpy(), z["idx"])
+    np.testing.assert_allclose(w.cpu().float().numpy(), _f16(z["wts"]).astype(np.float32),
+                               atol=1e-3)
+
+
+# --------------------------------------------------------------------------- permute
+def _moe_meta(idx_np, E):
+    from hydranet_amd import _lib
+    T, k = idx_np.shape
+    n = T * k
+    idx = torch.from_numpy(idx_np.astype(np.int32)).to(DEV)
+    meta = torch.full((3 * E + 2 + 2 * max(n, 1),), -7, dtype=torch.int32, device=DEV)
+    offsets, active = meta[:E + 1], meta[E + 1:2 * E + 1]
+    n_active, perm = meta[2 * E + 1:2 * E + 2], meta[2 * E + 2:2 * E + 2 + max(n, 1)]
+    inv = meta[2 * E + 2 + max(n, 1):]
+    _lib.call("hn_moe_permute", _lib.ptr(idx), T, k, E, _lib.ptr(offsets), _lib.ptr(perm),
+              _lib.ptr(inv), _lib.ptr(active), _lib.ptr(n_active), _lib.stream())
+    return idx, offsets, perm[:n], inv[:n], active, n_active
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 2, 8), (4, 2, 8), (16, 2, 8), (32, 8, 128), (2048, 2, 8),
+                                   (3000, 8, 128), (0, 2, 8)])
+def test_permute_bit_exact(T, k, E):
+    rng = np.random.default_rng(T + E)
+    if T:
+        p = rng.zipf(1.1, size=10 * E) % E  # skewed popularity
+        idx_np = np.stack([rng.choice(E, size=k, replace=False,
+                                      p=np.bincount(p, minlength=E) / p.size) for _ in range(T)])
+    else:
+        idx_np = np.zeros((0, k), np.int64)
+    _, offsets, perm, inv, active, n_active = _moe_meta(idx_np, E)
+    o_off, o_perm, o_inv, o_act = oracle.moe_permute(idx_np, E)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), o_off)
+    np.testing.assert_array_equal(perm.cpu().numpy(), o_perm)
+    np.testing.assert_array_equal(inv.cpu().numpy(), o_inv)
+    na = int(n_active.item())
+    assert na == len(o_act)
+    np.testing.assert_array_equal(active.cpu().numpy()[:na], o_act)
+
+
+def test_gather_and_unpermute_bit_exact():
+    from hydranet_amd import _lib
+    T, k, E, H = 37, 8, 128, 512
+    rng = np.random.default_rng(1)
+    idx_np = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)])
+    idx, offsets, perm, inv, active, n_active = _moe_meta(idx_np, E)
+    x = _randn(2, (T, H)).to(DEV)
+    xp = torch.empty(T * k, H, dtype=torch.float16, device=DEV)
+    _lib.call("hn_moe_gather", _lib.ptr(x), H, _lib.ptr(perm), k, _lib.ptr(offsets), E,
+              _lib.ptr(xp), H, T * k, H, _lib.stream())
+    ref_rows = x.cpu()[torch.from_numpy(perm.cpu().numpy() // k).long()]
+    assert torch.equal(xp.cpu(), ref_rows)
+    y = _randn(3, (T * k, H)).to(DEV)
+    w = torch.from_numpy(rng.uniform(0, 0.3, (T, k)).astype(np.float16)).to(DEV)
+    sh = _randn(4, (T, H)).to(DEV)
+    for shared in (None, sh):
+        out = torch.empty(T, H, dtype=torch.float16, device=DEV)
+        _lib.call("hn_moe_unpermute", _lib.ptr(y), H, _lib.ptr(inv), _lib.ptr(idx), _lib.ptr(w),
+                  T, k, _lib.ptr(shared), H, _lib.ptr(out), H, H, _lib.stream())
+        ref = oracle.moe_unpermute(y.cpu().numpy(), inv.cpu().numpy(), idx_np.astype(np.int32),
+                                   w.cpu().numpy(),
+                                   None if shared is None else shared.cpu().numpy())
+        np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+# --------------------------------------------------------------------------- MoE layers
+def _slots(n, H, I, seed0=0):
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, expert_seed
+    return [make_expert_slot(expert_seed(0, e, 42 + seed0), H, I, 128, slot_idx=e)
+            for e in range(n)]
+
+
+@pytest.fixture(scope="module")
+def mixtral_experts():
+    from hydranet_amd.preprocess.synthetic import slot_to_cpu
+    slots = _slots(8, 4096, 14336)
+    return slots, {e: slot_to_cpu(s) for e, s in enumerate(slots)}
+
+
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_mixtral_moe_layer_c2(T, mixtral_experts):
+    """Config C2: 8 Mixtral experts, softmax top-2, T tokens of decode."""
+    from hydranet_amd.model.moe import MixtralMoELayer
+    slots, cpu = mixtral_experts
+    layer = MixtralMoELayer(4096, 8, 2, slots=slots).to(DEV)
+    gate = _randn(7, (8, 4096), 0.02)
+    layer.router.gate.weight.data = gate.to(DEV)
+    h = _randn(100 + T, (1, T, 4096))
+    out = layer(h.to(DEV), top_k=2)
+    ro = layer.router(h.to(DEV), top_k_override=2)
+    idx = ro.expert_indices.view(T, 2).long().cpu()
+    w = ro.expert_weights.view(T, 2).cpu()
+    ref = torch_ref.moe_dispatch(h.view(T, 4096), idx, w, cpu)
+    _close(out.view(T, 4096), ref)
+    # and the oracle's own routing from the same logits picks the same experts
+    lg = ro.router_logits.view(T, 8).cpu().numpy()
+    idx_o, _ = oracle.router_topk(lg, 2, mode=0)
+    np.testing.assert_array_equal(idx.numpy(), idx_o)
+
+
+def test_grouped_matches_single_expert_path(mixtral_experts):
+    from hydranet_amd.kernels import expert_mlp_int4_fused
+    from hydranet_amd.model.moe import ExpertTable, moe_experts_forward
+    slots, _ = mixtral_experts
+    T = 6
+    h = _randn(3, (T, 4096)).to(DEV)
+    idx = torch.tensor([[0, 3], [3, 5], [0, 5], [7, 1], [3, 0], [6, 2]], dtype=torch.int32,
+                       device=DEV)
+    w = torch.full((T, 2), 0.5, dtype=torch.float16, device=DEV)
+    out = moe_experts_forward(h, idx, w, ExpertTable.from_slots(slots))
+    ref = torch.zeros(T, 4096, dtype=torch.float16, device=DEV)
+    for e in range(8):
+        tok, kp = torch.where(idx.long() == e)
+        if len(tok):
+            s = slots[e]
+            y = expert_mlp_int4_fused(h[tok], s.gate_packed, s.gate_scales, s.up_packed,
+                                      s.up_scales, s.down_packed, s.down_scales)
+            ref.index_add_(0, tok, y * w[tok, kp].unsqueeze(-1))
+    _close(out, ref)
+
+
+def test_glm_moe_layer_c3():
+    """Config C3: 128 GLM experts (4096->1408), fp16 shared expert, sigmoid top-8
+    with a seeded selection bias, T = 32."""
+    from hydranet_amd.model.moe import GLM4MoELayer
+    from hydranet_amd.preprocess.synthetic import slot_to_cpu
+    slots = _slots(128, 4096, 1408, seed0=1000)
+    layer = GLM4MoELayer(4096, 1408, 128, 8, slots=slots).to(DEV).half()
+    g = torch.Generator().manual_seed(8)
+    layer.router.weight.data = (torch.randn(128, 4096, generator=g) * 0.02).float().to(DEV)
+    bias = (torch.rand(128, generator=g) * 0.2 - 0.1).float()
+    layer.router.selection_bias = bias.to(DEV)
+    for lin in (layer.shared_expert.gate_proj, layer.shared_expert.up_proj,
+                layer.shared_expert.down_proj):
+        lin.weight.data = (torch.randn(*lin.weight.shape, generator=g) * 0.02).half().to(DEV)
+    h = _randn(9, (1, 32, 4096))
+    out = layer(h.to(DEV))
+    idx, w = layer.router(h.to(DEV))
+    used = sorted(set(idx.view(-1).tolist()))
+    cpu = {e: slot_to_cpu(slots[e]) for e in used}
+    shared = tuple(l.weight.data.cpu() for l in (layer.shared_expert.gate_proj,
+                                                  layer.shared_expert.up_proj,
+                                                  layer.shared_expert.down_proj))
+    ref = torch_ref.glm_moe(h.view(32, 4096), None, cpu, shared,
+                            routing=(idx.long().cpu(), w.cpu()))
+    _close(out.view(32, 4096), ref)
