@@ -78,6 +78,45 @@ __device__ __forceinline__ void hn_unpack8_centered(uint32_t w, half2_t out[4]) 
   out[3] = __builtin_elementwise_fma(hn_bits_h2(hi1), sixteenth, bias_hi);  // k3, k7
 }
 
+// Same unpack, producing the MFMA operand directly.  gfx9 VOP3/VOP3P
+// encodings take no literal constants and at most one SGPR, so the masks live
+// in SGPRs and the magic number and the fp16 constants in VGPRs (made opaque
+// once per kernel with hn_vgpr); v_and_or_b32 is written out because the
+// compiler otherwise splits it into v_and + v_or.
+struct HnUnpackRegs {
+  uint32_t m_lo, m_hi;                       // SGPR: 0x000F000F, 0x00F000F0
+  uint32_t magic;                            // VGPR: 0x64006400
+  uint32_t bias_lo, sixteenth, bias_hi;      // VGPR: half2 (-1032), (1/16), (-72)
+};
+
+__device__ __forceinline__ uint32_t hn_vgpr(uint32_t v) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
+  return r;
+}
+
+__device__ __forceinline__ uint32_t hn_and_or(uint32_t w, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(m), "v"(o));
+  return r;
+}
+
+__device__ __forceinline__ half8_t hn_unpack8_regs(uint32_t w, const HnUnpackRegs& c) {
+  const half2_t bias_lo = hn_bits_h2(c.bias_lo);
+  const half2_t sixteenth = hn_bits_h2(c.sixteenth);
+  const half2_t bias_hi = hn_bits_h2(c.bias_hi);
+  const uint32_t w8 = w >> 8;
+  const half2_t p0 = hn_bits_h2(hn_and_or(w, c.m_lo, c.magic)) + bias_lo;
+  const half2_t p1 = __builtin_elementwise_fma(hn_bits_h2(hn_and_or(w, c.m_hi, c.magic)),
+                                               sixteenth, bias_hi);
+  const half2_t p2 = hn_bits_h2(hn_and_or(w8, c.m_lo, c.magic)) + bias_lo;
+  const half2_t p3 = __builtin_elementwise_fma(hn_bits_h2(hn_and_or(w8, c.m_hi, c.magic)),
+                                               sixteenth, bias_hi);
+  const u32x4 r = {__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                   __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)};
+  return __builtin_bit_cast(half8_t, r);
+}
+
 // Position j of an 8-block in unpack order holds source index hn_perm8(j).
 __host__ __device__ constexpr int hn_perm8(int j) { return (j >> 1) + ((j & 1) << 2); }
 

@@ -9,21 +9,23 @@
 //
 // Decode is HBM-bound: the design goal is that every packed byte is requested
 // from HBM as early as possible and exactly once.
-//  * Work unit of one wave = (tile of 16 weight rows, k-chunk of <= 16/MATS
-//    groups of 128 k).  Per group each lane issues ONE 16-byte load: row
-//    (n0 + lane%16), bytes [16*(lane/16), +16) of the group's 64 bytes.  Those
-//    16 bytes are the B operand of four v_mfma_f32_16x16x32_f16 steps.  All of
-//    a wave's loads are in flight at once (no branches around loads; invalid
-//    lanes read a clamped address and get scale 0).
-//  * A workgroup = 4 waves on 4 consecutive tiles sharing one k-chunk; the
-//    activations of that k-chunk are loaded FIRST (so waiting for them, in
-//    vmcnt order, does not wait for the weights), permuted to the unpack order
-//    and staged in LDS for the A operand.
+//  * Work unit of one wave = (tile of 16 weight rows, gpw <= 16/MATS groups of
+//    128 k).  Per group each lane issues ONE 16-byte load: row (n0 + lane%16),
+//    bytes [16*(lane/16), +16) of the group's 64 bytes.  Those 16 bytes are the
+//    B operand of four v_mfma_f32_16x16x32_f16 steps.  All of a wave's loads
+//    are in flight at once (no branches around loads; invalid lanes read a
+//    clamped address and get scale 0).
+//  * A workgroup = TG tiles x KW waves per tile.  The KW waves of a tile split
+//    its k-chunk and reduce through LDS (fixed order), so a tile is finished
+//    on chip and the epilogue writes the result directly.  The activations of
+//    the workgroup's k-chunk are staged once in LDS (permuted to the unpack
+//    order) for the A operand.
+//  * Only when the activation chunk would not fit in LDS is K also split over
+//    workgroups (blockIdx.y): each split writes fp32 partials, the last split
+//    of a tile (atomic counter, reset to 0 by it) sums them in split order —
+//    deterministic — and runs the epilogue.
 //  * Tokens beyond 16 (up to 64) reuse the unpacked B operand with another
 //    MFMA per 16-token chunk.
-//  * K is split over blockIdx.y.  Each split writes fp32 partials; the last
-//    split to finish a tile (atomic counter, which it resets to 0) sums the
-//    partials in split order — deterministic — and runs the epilogue.
 //  * Group scales multiply the fp32 MFMA partial of each 128-k group when
 //    group % 128 == 0; for group 32/64 the unpacked fp16 values are multiplied
 //    by the per-lane scale first, which is the reference's fp16 dequantised
@@ -33,9 +35,10 @@
 namespace {
 
 constexpr int kTileN = 16;
-constexpr int kWaves = 4;                // waves (tiles) per workgroup
+constexpr int kMaxWaves = 8;             // waves per workgroup (TG * KW)
 constexpr int kLoadsPerLane = 16;        // 16-byte weight loads in flight per lane
-constexpr int kXChunkBytes = 32 * 1024;  // LDS activation chunk budget
+constexpr int kLdsBudget = 64 * 1024;    // activation chunk + wave reduction
+constexpr int kMaxKS = 64;               // cross-workgroup k-splits
 
 struct W4Mat {
   const uint8_t* q;  // [N, K/2] packed nibbles
@@ -57,8 +60,11 @@ struct SkinnyArgs {
   W4Mat w[2];
   h16* out; long ld_o;
   int N, K, group;
-  int ks;          // k-splits (gridDim.y)
-  int gpc;         // groups per k-chunk
+  int ks;          // k-splits over workgroups (gridDim.y)
+  int gpc;         // groups per workgroup k-chunk
+  int gpw;         // groups per wave (gpc split over the KW waves of a tile)
+  int kw;          // waves per tile
+  int tg;          // tiles per workgroup
   int ldx;         // LDS row stride of the x chunk (halves)
   float* partial;  // [ks][MATS][part_rows][N] fp32 when ks > 1
   int* counters;   // [E?][tiles] zero on entry, left zero on exit
@@ -70,74 +76,65 @@ struct SkinnyArgs {
   const int* offsets;
   int phase;       // 0 = gate/up (+SiLU), 1 = down
   int H, I;
+  // unpack constants as registers (see hn_unpack8_regs)
+  uint32_t m_lo, m_hi, magic;
 };
 
 template <int MATS, int EPI, bool PREMUL, int NCH, int XR>
 __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __restrict__ x,
                                             int Mc, const W4Mat* mats, h16* __restrict__ out,
                                             float* __restrict__ part, int* __restrict__ ctr,
-                                            int tile0, unsigned char* smem) {
-  constexpr int BATCH = kLoadsPerLane / MATS;
+                                            unsigned char* smem) {
+  constexpr int BATCH = kLoadsPerLane / MATS;  // loads per lane per matrix (even)
+  static_assert(BATCH % 2 == 0, "groups are loaded in pairs");
   const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int col = lane & 15;  // weight row in the tile (B/D), token in a 16-chunk (A)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
+  const int col = lane & 15;  // MFMA column (weight row in the tile) / token in a 16-chunk
   const int q = lane >> 4;    // 32-k sub-block of a 128-k group
   const int N = A.N, K = A.K, group = A.group;
   const int G = (K + 127) >> 7;
   const int ks = blockIdx.y;
-  const int g0 = ks * A.gpc;
-  const int gn = min(A.gpc, G - g0);  // groups in this k-chunk (>= 1)
-  const int tile = tile0 + wave;
+  HnUnpackRegs ur;
+  ur.m_lo = A.m_lo;
+  ur.m_hi = A.m_hi;
+  ur.magic = hn_vgpr(A.magic);
+  ur.bias_lo = hn_vgpr(0xE408E408u);    // half2(-1032, -1032)
+  ur.sixteenth = hn_vgpr(0x2C002C00u);  // half2(0.0625, 0.0625)
+  ur.bias_hi = hn_vgpr(0xD480D480u);    // half2(-72, -72)
+  const int g0 = ks * A.gpc;                 // first group of the workgroup chunk
+  const int gn = min(A.gpc, G - g0);         // groups in the chunk (>= 1)
+  const int gn2 = (gn + 1) & ~1;             // staged groups (pairs; the pad is zero)
+  const int kwi = wave % A.kw;               // k-slice of this wave within the chunk
+  const int tile = blockIdx.x * A.tg + wave / A.kw;
+  const int gl0 = kwi * A.gpw;               // first chunk-local group of this wave (even)
+  const int gw = max(0, min(A.gpw, gn - gl0));  // groups of this wave (uniform)
   const int tiles = (N + kTileN - 1) / kTileN;
   const bool tile_ok = tile < tiles;
   const int n0 = tile * kTileN;
-  const int row = n0 + col;
-  const bool row_ok = tile_ok && row < N;
-  const int row_c = min(row, N - 1);
   const int ldx = A.ldx;
   h16* xs = reinterpret_cast<h16*>(smem);
 
-  // ---- 1. activation chunk -> registers (issued before the weights; branch-free
-  //         so the wait for them lands after the weight loads are issued)
-  constexpr int kXRegs = XR;  // XR x 16 B of activations per thread
-  const int blocks8 = gn * 16;
+  // ---- 1. activation chunk -> registers -> LDS (permuted to the unpack order)
+  const int blocks8 = gn2 * 16;
   const int nblk = Mc * blocks8;
-  half8_t xr[kXRegs];
+  half8_t xr[XR];
 #pragma unroll
-  for (int j = 0; j < kXRegs; ++j) {
-    const int i = min(tid + j * kWaves * 64, nblk - 1);
+  for (int j = 0; j < XR; ++j) {
+    const int i = min(tid + j * nthr, nblk - 1);
     const int m = i / blocks8;
     const int b = i - m * blocks8;
     const int k = min(g0 * 128 + b * 8, K - 8);
     xr[j] = *reinterpret_cast<const half8_t*>(x + (long)m * A.ld_x + k);
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weights
-
-  // ---- 2. weights and scales of this wave's unit, all in flight
-  u32x4 wq[MATS][BATCH];
-  h16 sc[MATS][BATCH];
 #pragma unroll
-  for (int i = 0; i < BATCH; ++i) {
-    const int g = min(g0 + i, G - 1);
-    const int kk_c = min(g * 128 + 32 * q, K - 32);
-#pragma unroll
-    for (int mt = 0; mt < MATS; ++mt) {
-      wq[mt][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-          mats[mt].q + (long)row_c * mats[mt].ld_q + (long)(kk_c >> 1)));
-      sc[mt][i] = mats[mt].s[(long)row_c * mats[mt].ld_s + (PREMUL ? kk_c : g * 128) / group];
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- 3. stage the activations (waits for them only), permuted to unpack order
-#pragma unroll
-  for (int j = 0; j < kXRegs; ++j) {
-    const int i = tid + j * kWaves * 64;
+  for (int j = 0; j < XR; ++j) {
+    const int i = tid + j * nthr;
     if (i < nblk) {
       const int m = i / blocks8;
       const int b = i - m * blocks8;
-      const bool in_k = g0 * 128 + b * 8 < K;
+      const bool in_k = (b < gn * 16) && (g0 * 128 + b * 8 < K);
       half8_t p;
 #pragma unroll
       for (int t = 0; t < 8; ++t) p[t] = in_k ? xr[j][hn_perm8(t)] : (h16)0.0f;
@@ -145,58 +142,167 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
     }
   }
   __syncthreads();
+  // weights are issued only now: the waits for them then complete in issue
+  // order, so a wave unpacks group i while groups i+1.. are still in flight
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- 4. unpack + MFMA
-  float4_t acc[NCH][MATS];
+  // ---- 2. weights: each load instruction reads 8 rows x 128 B (full cache
+  //         lines, non-temporal).  Load "lo" covers tile rows 0-7, load "hi"
+  //         rows 8-15, both over the group pair (g, g+1).  Lane mapping:
+  //           lo: row col%8,     chunk (col<8 ? q : 4+q)
+  //           hi: row 8 + col%8, chunk (col>=8 ? q : 4+q)
+  //         so lane l finds (row col, chunk q) of group g in lo if col<8 else hi
+  //         (the "even" MFMA operand), and (row col^8, chunk q) of group g+1 in
+  //         hi if col<8 else lo (the "odd" operand, whose MFMA columns are the
+  //         weight rows XOR 8).  Buffer loads: rows past N and groups past the
+  //         wave's range are out of the descriptor's range and return 0
+  //         without a memory access.
+  constexpr uint32_t kOOB = 0x7ffffff0u;
+  constexpr int PAIRS = BATCH / 2;
+  u32x4 wlo[MATS][PAIRS], whi[MATS][PAIRS];
+  h16 se[MATS][PAIRS], so[MATS][PAIRS];  // scales: even group (row col), odd (row col^8)
+  const int rlo = n0 + (col & 7), rhi = n0 + 8 + (col & 7);
+  const int clo = (col < 8) ? q : 4 + q, chi = (col >= 8) ? q : 4 + q;
+  const int re = n0 + col, ro = n0 + (col ^ 8);
+  __amdgpu_buffer_rsrc_t rq[MATS], rs[MATS];
+  uint32_t vlo[MATS], vhi[MATS], vse[MATS], vso[MATS];
+#pragma unroll
+  for (int mt = 0; mt < MATS; ++mt) {
+    rq[mt] = __builtin_amdgcn_make_buffer_rsrc((void*)mats[mt].q, (short)0,
+                                               (int)((long)N * mats[mt].ld_q), 0x00020000);
+    rs[mt] = __builtin_amdgcn_make_buffer_rsrc((void*)mats[mt].s, (short)0,
+                                               (int)((long)N * mats[mt].ld_s * 2), 0x00020000);
+    vlo[mt] = (tile_ok && rlo < N) ? (uint32_t)(rlo * mats[mt].ld_q + 16 * clo) : kOOB;
+    vhi[mt] = (tile_ok && rhi < N) ? (uint32_t)(rhi * mats[mt].ld_q + 16 * chi) : kOOB;
+    vse[mt] = (tile_ok && re < N) ? (uint32_t)(re * mats[mt].ld_s * 2) : kOOB;
+    vso[mt] = (tile_ok && ro < N) ? (uint32_t)(ro * mats[mt].ld_s * 2) : kOOB;
+  }
+  constexpr int kAuxNT = 2;  // non-temporal: streamed once
+#pragma unroll
+  for (int pi = 0; pi < PAIRS; ++pi) {
+    const int g = g0 + gl0 + 2 * pi;   // even group of the pair
+    const bool pv = 2 * pi < gw;       // uniform
+    const bool ov = 2 * pi + 1 < gw;   // odd group valid (uniform)
+#pragma unroll
+    for (int mt = 0; mt < MATS; ++mt) {
+      const uint32_t so_q = pv ? (uint32_t)(g * 64) : kOOB;
+      wlo[mt][pi] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+          rq[mt], vlo[mt], so_q, kAuxNT));
+      whi[mt][pi] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+          rq[mt], vhi[mt], so_q, kAuxNT));
+      if (PREMUL) {
+        const uint32_t ie = (uint32_t)((g * 128 + 32 * q) / group);
+        const uint32_t io = (uint32_t)(((g + 1) * 128 + 32 * q) / group);
+        se[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
+            rs[mt], vse[mt] + 2 * ie, pv ? 0u : kOOB, 0));
+        so[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
+            rs[mt], vso[mt] + 2 * io, ov ? 0u : kOOB, 0));
+      } else {
+        se[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
+            rs[mt], vse[mt], pv ? (uint32_t)(2 * ((g * 128) / group)) : kOOB, 0));
+        so[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
+            rs[mt], vso[mt], ov ? (uint32_t)(2 * (((g + 1) * 128) / group)) : kOOB, 0));
+      }
+    }
+  }
+
+  // ---- 4. unpack + MFMA.  acc_e: columns = tile rows; acc_o: columns = rows ^ 8.
+  float4_t acc[NCH][MATS], acco[NCH][MATS];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
 #pragma unroll
-    for (int mt = 0; mt < MATS; ++mt) acc[c][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-
+    for (int mt = 0; mt < MATS; ++mt) {
+      acc[c][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      acco[c][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  const bool low_col = col < 8;
 #pragma unroll
-  for (int i = 0; i < BATCH; ++i) {
-    if (i < gn) {  // uniform
-      const bool ok = row_ok && ((g0 + i) * 128 + 32 * q < K);
+  for (int pi = 0; pi < PAIRS; ++pi) {
 #pragma unroll
-      for (int mt = 0; mt < MATS; ++mt) {
-        const h16 s16 = ok ? sc[mt][i] : (h16)0.0f;
-        half8_t b[4];
+    for (int half = 0; half < 2; ++half) {
+      if (2 * pi + half < gw) {  // uniform
+        const int gl = gl0 + 2 * pi + half;  // chunk-local group
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          half2_t p[4];
-          hn_unpack8_centered(wq[mt][i][t], p);
-          if (PREMUL) {
-            const half2_t s2 = {s16, s16};
+        for (int mt = 0; mt < MATS; ++mt) {
+          const h16 s16 = half ? so[mt][pi] : se[mt][pi];
+          // even operand: lo for col<8, hi otherwise; odd operand: the reverse
+          const bool take_lo = half ? !low_col : low_col;
+          u32x4 w;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) p[j] = p[j] * s2;
-          }
-          b[t] = hn_cat4(p);
-        }
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          const int tok = c * 16 + col;
-          float4_t cc = {0.f, 0.f, 0.f, 0.f};
-          if (PREMUL) cc = acc[c][mt];
+          for (int d = 0; d < 4; ++d) w[d] = take_lo ? wlo[mt][pi][d] : whi[mt][pi][d];
+          half8_t b[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            half8_t a = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-            if (tok < Mc)
-              a = *reinterpret_cast<const half8_t*>(xs + tok * ldx + i * 128 + 32 * q + 8 * t);
-            cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[t], cc, 0, 0, 0);
+            b[t] = hn_unpack8_regs(w[t], ur);
+            if (PREMUL) {
+              const half8_t s8 = {s16, s16, s16, s16, s16, s16, s16, s16};
+              b[t] = b[t] * s8;
+            }
           }
-          if (PREMUL) {
-            acc[c][mt] = cc;
-          } else {
-            const float s = (float)s16;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[c][mt][r] = __builtin_fmaf(s, cc[r], acc[c][mt][r]);
+          for (int c = 0; c < NCH; ++c) {
+            // rows of A past the valid tokens only feed rows of C that are never
+            // stored, so those lanes read a clamped valid row instead of branching
+            const int tok = min(c * 16 + col, Mc - 1);
+            const h16* arow = xs + tok * ldx + gl * 128 + 32 * q;
+            float4_t& dst = half ? acco[c][mt] : acc[c][mt];
+            float4_t cc = {0.f, 0.f, 0.f, 0.f};
+            if (PREMUL) cc = dst;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const half8_t a = *reinterpret_cast<const half8_t*>(arow + 8 * t);
+              cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[t], cc, 0, 0, 0);
+            }
+            if (PREMUL) {
+              dst = cc;
+            } else {
+              const float sf = (float)s16;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) dst[r] = __builtin_fmaf(sf, cc[r], dst[r]);
+            }
           }
         }
       }
     }
   }
+  // fold the odd accumulator back: column c of acco belongs to row c ^ 8
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int mt = 0; mt < MATS; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[c][mt][r] += __shfl_xor(acco[c][mt][r], 8, 16);
+  const int row = n0 + col;
+  const bool row_ok = tile_ok && row < N;
 
-  // ---- 5. output: D lane layout is row (n0 + col), tokens 16c + 4q + r
+  // ---- 5. reduce the KW waves of each tile through LDS (fixed order)
+  if (A.kw > 1) {
+    // the reduction area reuses the activation chunk once every wave is done with it
+    __syncthreads();
+    float4_t* red = reinterpret_cast<float4_t*>(smem);
+    if (kwi > 0) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int mt = 0; mt < MATS; ++mt) red[((wave * NCH + c) * MATS + mt) * 64 + lane] =
+            acc[c][mt];
+    }
+    __syncthreads();
+    if (kwi > 0) return;
+    for (int j = 1; j < A.kw; ++j) {
+      const int w2 = wave + j;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int mt = 0; mt < MATS; ++mt) {
+          const float4_t v = red[((w2 * NCH + c) * MATS + mt) * 64 + lane];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[c][mt][r] += v[r];
+        }
+    }
+  }
+
+  // ---- 6. output: D lane layout is row (n0 + col), tokens 16c + 4q + r
   if (!tile_ok) return;
   if (A.ks == 1) {
     if (row_ok) {
@@ -218,10 +324,10 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
     }
     return;
   }
-  // split-K: write partials, last split of this tile reduces in split order.
-  // Partials and counters are relaxed agent-scope atomics (sc1 accesses,
-  // coherent across XCDs without writing back or invalidating the L2); the
-  // s_waitcnt orders "partials stored" before "counter incremented".
+  // split over workgroups: write partials, the last split of this tile reduces
+  // in split order.  Partials and counters are relaxed agent-scope atomics (sc1
+  // accesses, coherent across XCDs without writing back or invalidating the
+  // L2); the s_waitcnt orders "partials stored" before "counter incremented".
   const long plane = A.part_rows * (long)N;
   if (row_ok) {
 #pragma unroll
@@ -244,19 +350,30 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
   last = __shfl(last, 0, 64);
   if (!last) return;
   if (lane == 0) __hip_atomic_store(ctr + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // this wave now owns the tile's 16 rows x Mc tokens: lanes walk (token, row)
+  // this wave now owns the tile's 16 rows x Mc tokens: lanes walk (token, row);
+  // all partial loads of an element are issued together (one round trip)
   for (int e = lane; e < Mc * kTileN; e += 64) {
     const int m = e / kTileN;
     const int rr = n0 + (e % kTileN);
     if (rr >= N) continue;
     float v[MATS];
 #pragma unroll
-    for (int mt = 0; mt < MATS; ++mt) {
-      float s = 0.f;
-      for (int k2 = 0; k2 < A.ks; ++k2)
-        s += __hip_atomic_load(part + (long)(k2 * MATS + mt) * plane + (long)m * N + rr,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v[mt] = s;
+    for (int mt = 0; mt < MATS; ++mt) v[mt] = 0.f;
+    for (int kb = 0; kb < A.ks; kb += 8) {
+      float pv[MATS][8];
+#pragma unroll
+      for (int mt = 0; mt < MATS; ++mt)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int kc = min(kb + j, A.ks - 1);
+          pv[mt][j] = __hip_atomic_load(part + (long)(kc * MATS + mt) * plane + (long)m * N + rr,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+      for (int mt = 0; mt < MATS; ++mt)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (kb + j < A.ks) v[mt] += pv[mt][j];
     }
     h16 o;
     if (EPI == 1) o = (h16)(hn_silu((float)(h16)v[0]) * (float)(h16)v[MATS - 1]);
@@ -266,18 +383,18 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
 }
 
 template <int MATS, int EPI, bool PREMUL, int NCH, int XR>
-__global__ __launch_bounds__(kWaves * 64) void skinny_kernel(SkinnyArgs A) {
+__global__ __launch_bounds__(kMaxWaves * 64) void skinny_kernel(SkinnyArgs A) {
   extern __shared__ __align__(16) unsigned char smem[];
   const W4Mat mats[2] = {A.w[0], A.w[1]};
   skinny_unit<MATS, EPI, PREMUL, NCH, XR>(A, A.x, A.M, mats, A.out, A.partial, A.counters,
-                                      blockIdx.x * kWaves, smem);
+                                          smem);
 }
 
 // Grouped launch over the experts of one MoE layer; tokens are permuted so
 // expert e owns rows [offsets[e], offsets[e+1]).  blockIdx.z walks the
 // active-expert list (device), so no host sync is needed.
 template <int PHASE, bool PREMUL, int NCH, int XR>
-__global__ __launch_bounds__(kWaves * 64) void grouped_kernel(SkinnyArgs A) {
+__global__ __launch_bounds__(kMaxWaves * 64) void grouped_kernel(SkinnyArgs A) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int a = blockIdx.z;
   if (a >= *A.n_active) return;
@@ -293,12 +410,12 @@ __global__ __launch_bounds__(kWaves * 64) void grouped_kernel(SkinnyArgs A) {
   if (PHASE == 0) {
     const W4Mat mats[2] = {{ew.gate_q, ew.gate_s, H / 2, H / g}, {ew.up_q, ew.up_s, H / 2, H / g}};
     skinny_unit<2, 1, PREMUL, NCH, XR>(A, A.x + (long)t0 * A.ld_x, Me, mats,
-                                   A.out + (long)t0 * A.ld_o, part, ctr, blockIdx.x * kWaves, smem);
+                                       A.out + (long)t0 * A.ld_o, part, ctr, smem);
   } else {
     const W4Mat mats[2] = {{ew.down_q, ew.down_s, I / 2, I / g},
                            {ew.down_q, ew.down_s, I / 2, I / g}};
     skinny_unit<1, 0, PREMUL, NCH, XR>(A, A.x + (long)t0 * A.ld_x, Me, mats,
-                                   A.out + (long)t0 * A.ld_o, part, ctr, blockIdx.x * kWaves, smem);
+                                       A.out + (long)t0 * A.ld_o, part, ctr, smem);
   }
 }
 
@@ -317,29 +434,49 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const h16* __restrict__ g
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// k-split plan: groups per chunk limited by the load budget and the LDS chunk.
+// Launch plan.  A tile's whole K is reduced inside one workgroup (ks = 1)
+// whenever its activation chunk fits the LDS budget; otherwise K is chunked
+// over workgroups and reduced through the partials.
 struct Plan {
-  int ks, gpc, ldx, nch, xr;
+  int ks, gpc, gpw, kw, tg, ldx, nch, xr;
   size_t lds;
 };
 
 Plan make_plan(int rows, int K, int mats) {
   Plan p;
   const int G = (K + 127) / 128;
-  int gpc = kLoadsPerLane / mats;
-  const int by_lds = kXChunkBytes / (rows * 256 + 16 * rows);
-  if (by_lds < gpc) gpc = by_lds < 1 ? 1 : by_lds;
-  // the x staging registers hold at most 8 x 16 B per thread
-  while (gpc > 1 && rows * gpc * 16 > 8 * kWaves * 64) --gpc;
-  if (gpc > G) gpc = G;
+  const int gpw_max = kLoadsPerLane / mats;
+  p.nch = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
+  auto fits = [&](int gpc) {
+    const int kw = (gpc + gpw_max - 1) / gpw_max;
+    if (kw > kMaxWaves) return false;
+    const int tg = kw >= 4 ? 1 : 4 / kw;
+    const size_t xb = (size_t)rows * (((gpc + 1) & ~1) * 128 + 8) * 2;
+    const size_t rb = (size_t)tg * kw * p.nch * mats * 1024;
+    const int xr_need = (rows * ((gpc + 1) & ~1) * 16 + tg * kw * 64 - 1) / (tg * kw * 64);
+    return (xb > rb ? xb : rb) <= (size_t)kLdsBudget && xr_need <= 8;
+  };
+  int gpc = G;
+  if (!fits(gpc)) {
+    // largest chunk that fits, then balanced over the splits
+    gpc = 1;
+    while (gpc < G && fits(gpc + 1)) ++gpc;
+    const int ks = (G + gpc - 1) / gpc;
+    gpc = (G + ks - 1) / ks;
+  }
   p.gpc = gpc;
   p.ks = (G + gpc - 1) / gpc;
-  p.ldx = gpc * 128 + 8;
-  p.nch = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
-  // activation registers per thread (variants 1, 2, 8; 8 whenever NCH > 1)
-  const int need = (rows * gpc * 16 + kWaves * 64 - 1) / (kWaves * 64);
-  p.xr = (p.nch == 1 && need <= 1) ? 1 : (p.nch == 1 && need <= 2) ? 2 : 8;
-  p.lds = (size_t)rows * p.ldx * 2;
+  p.kw = (gpc + gpw_max - 1) / gpw_max;
+  p.gpw = (gpc + p.kw - 1) / p.kw;
+  p.gpw += p.gpw & 1;  // groups are loaded in pairs: waves start on even groups
+  p.tg = p.kw >= 4 ? 1 : 4 / p.kw;
+  p.ldx = ((gpc + 1) & ~1) * 128 + 8;
+  const int nthr = p.tg * p.kw * 64;
+  const int need = (rows * ((gpc + 1) & ~1) * 16 + nthr - 1) / nthr;
+  p.xr = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+  const size_t xb = (size_t)rows * p.ldx * 2;
+  const size_t rb = p.kw > 1 ? (size_t)p.tg * p.kw * p.nch * mats * 1024 : 0;
+  p.lds = xb > rb ? xb : rb;
   return p;
 }
 
@@ -349,6 +486,8 @@ Plan make_plan(int rows, int K, int mats) {
       hipLaunchKernelGGL((KERNEL<__VA_ARGS__, 1, 1>), grid, block, p.lds, s, A);           \
     else if (p.nch == 1 && p.xr == 2)                                                      \
       hipLaunchKernelGGL((KERNEL<__VA_ARGS__, 1, 2>), grid, block, p.lds, s, A);           \
+    else if (p.nch == 1 && p.xr == 4)                                                      \
+      hipLaunchKernelGGL((KERNEL<__VA_ARGS__, 1, 4>), grid, block, p.lds, s, A);           \
     else if (p.nch == 1)                                                                   \
       hipLaunchKernelGGL((KERNEL<__VA_ARGS__, 1, 8>), grid, block, p.lds, s, A);           \
     else if (p.nch == 2)                                                                   \
@@ -357,16 +496,28 @@ Plan make_plan(int rows, int K, int mats) {
       hipLaunchKernelGGL((KERNEL<__VA_ARGS__, 4, 8>), grid, block, p.lds, s, A);           \
   } while (0)
 
+void apply_plan(SkinnyArgs& A, const Plan& p) {
+  A.m_lo = 0x000F000Fu;
+  A.m_hi = 0x00F000F0u;
+  A.magic = 0x64006400u;
+  A.ks = p.ks;
+  A.gpc = p.gpc;
+  A.gpw = p.gpw;
+  A.kw = p.kw;
+  A.tg = p.tg;
+  A.ldx = p.ldx;
+}
+
 template <int MATS, int EPI, bool PREMUL>
 int launch_single(SkinnyArgs& A, const Plan& p, hipStream_t s) {
-  dim3 grid(hn_cdiv(hn_cdiv(A.N, kTileN), kWaves), p.ks, 1), block(kWaves * 64);
+  dim3 grid(hn_cdiv(hn_cdiv(A.N, kTileN), p.tg), p.ks, 1), block(p.tg * p.kw * 64);
   HN_SKINNY_VARIANTS(skinny_kernel, MATS, EPI, PREMUL);
   return 0;
 }
 
 template <int PHASE, bool PREMUL>
 void launch_grouped(SkinnyArgs& A, const Plan& p, int E_max, hipStream_t s) {
-  dim3 grid(hn_cdiv(hn_cdiv(A.N, kTileN), kWaves), p.ks, E_max), block(kWaves * 64);
+  dim3 grid(hn_cdiv(hn_cdiv(A.N, kTileN), p.tg), p.ks, E_max), block(p.tg * p.kw * 64);
   HN_SKINNY_VARIANTS(grouped_kernel, PHASE, PREMUL);
 }
 
@@ -420,6 +571,8 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
   if (int rc = check_common(who, M, N, K, group, x, ld_x)) return rc;
   HN_ARG_CHECK(aligned16(w0.q) && w0.ld_q % 16 == 0 && aligned16(w1.q) && w1.ld_q % 16 == 0,
                "%s: packed weight rows must be 16-byte aligned", who);
+  HN_ARG_CHECK(N * w0.ld_q < (1L << 31) && N * w0.ld_s * 2 < (1L << 31),
+               "%s: one weight matrix must stay below 2 GiB", who);
   if (M == 0 || N == 0) return 0;
   const bool premul = (group % 128) != 0;
   const int tiles = hn_cdiv(N, kTileN);
@@ -441,9 +594,7 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
     A.N = (int)N;
     A.K = (int)K;
     A.group = (int)group;
-    A.ks = p.ks;
-    A.gpc = p.gpc;
-    A.ldx = p.ldx;
+    apply_plan(A, p);
     A.counters = (int*)ws;
     A.partial = ws ? (float*)((char*)ws + cb) : nullptr;
     A.part_rows = rows;
@@ -559,7 +710,7 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
     A.x = (const h16*)x_perm; A.ld_x = H;
     A.out = (h16*)h_ws; A.ld_o = I;
     A.N = (int)I; A.K = (int)H;
-    A.ks = p.ks; A.gpc = p.gpc; A.ldx = p.ldx;
+    apply_plan(A, p);
     A.partial = partial;
     A.phase = 0;
     if (premul) launch_grouped<0, true>(A, p, (int)E, s);
@@ -571,7 +722,7 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
     A.x = (const h16*)h_ws; A.ld_x = I;
     A.out = (h16*)y_perm; A.ld_o = H;
     A.N = (int)H; A.K = (int)I;
-    A.ks = p.ks; A.gpc = p.gpc; A.ldx = p.ldx;
+    apply_plan(A, p);
     A.partial = partial;
     A.phase = 1;
     if (premul) launch_grouped<1, true>(A, p, (int)E, s);

@@ -40,11 +40,12 @@ def test_ctypes_table_matches_header():
 def test_workspace_query():
     from hydranet_amd import _lib
     h = _lib.lib()
-    # C1 expert: gate/up splits K=4096 in 4 chunks -> partials for 2 matrices
-    b = h.hn_skinny_workspace_bytes(2, 1, 4096, 14336, 0)
-    assert b >= 4 * 2 * 14336 * 4
-    # a small single-chunk problem needs only the counter region
+    # one token: every tile reduces K inside a workgroup -> counters only
+    assert h.hn_skinny_workspace_bytes(2, 1, 4096, 14336, 0) <= 4096
     assert h.hn_skinny_workspace_bytes(0, 1, 64, 256, 0) == 256
+    # 64 tokens x K=14336 do not fit one workgroup's LDS -> fp32 partials
+    b = h.hn_skinny_workspace_bytes(0, 64, 4096, 14336, 0)
+    assert b >= 2 * 64 * 4096 * 4
 
 
 def test_argument_errors_raise_without_gpu():
