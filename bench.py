@@ -167,7 +167,9 @@ def bench_c1(args):
                                f"T={T}", "tokens": T, "hidden": H, "intermediate": I,
                    "group_size": g, "experts_rotated": n_exp, "bytes_per_step": bytes_step,
                    "graph": gr is not None},
-        "roofline": {"bound": "hbm", "kernel": "skinny_kernel<2,1,false,1,1> (gate+up+SiLU)",
+        "roofline": {"bound": "hbm",
+                     "kernel": ("stream_kernel (gate+up+SiLU, persistent)" if args.decode_path == 0
+                                else "skinny_kernel (gate+up+SiLU, split-K)"),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": gu_bytes, "avg_us": round(kt["gate_up_silu"] * 1e3, 3),
@@ -283,6 +285,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-path", type=int, default=0, choices=[0, 1],
+                    help="0: streaming kernels where they apply (default); 1: split-K only")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -294,6 +298,8 @@ def main():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
     torch.cuda.set_device(0)
+    from hydranet_amd import _lib
+    _lib.call("hn_set_decode_path", args.decode_path)
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
     res, ctx = bench_c1(args)
     _log("c1 done", res["value"], res["unit"])

@@ -35,6 +35,7 @@ SIGNATURES: dict[str, list] = {
     "hn_moe_gather": [P, L, P, L, P, L, P, L, L, L, P],
     "hn_moe_unpermute": [P, L, P, P, P, L, L, P, L, P, L, L, P],
     "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],
+    "hn_set_decode_path": [I],
 }
 
 RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long}

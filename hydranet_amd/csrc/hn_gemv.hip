@@ -555,6 +555,28 @@ extern "C" long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long
   return (long)(ctr_bytes(ctr) + (a > b ? a : b));
 }
 
+// Persistent streaming kernels (hn_stream.hip): return 1 when a shape is not
+// theirs, 0 after a launch, < 0 on error.
+extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const void* q0,
+                                     const void* s0, const void* q1, const void* s1, long ld_q,
+                                     long ld_s, void* out, long ld_o, long M, long N, long K,
+                                     long group, void* stream);
+extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const void* table,
+                                      const int* active, const int* n_active, const int* offsets,
+                                      long E, long max_rows, long H, long I, long group, void* out,
+                                      long ld_o, void* stream, int dry_run);
+
+// Decode kernel family: 0 = automatic (streaming kernels where they apply),
+// 1 = split-K kernels only.  Process-wide; for A/B measurement and tests.
+static int g_decode_path = 0;
+constexpr long kStreamMaxRows = 16;
+
+extern "C" int hn_set_decode_path(int path) {
+  HN_ARG_CHECK(path == 0 || path == 1, "hn_set_decode_path: path must be 0 or 1 (got %d)", path);
+  g_decode_path = path;
+  return 0;
+}
+
 static int check_common(const char* who, long M, long N, long K, long group, const void* x,
                         long ld_x) {
   HN_ARG_CHECK(M >= 0 && N >= 0 && K >= 0, "%s: negative dims", who);
@@ -575,6 +597,11 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
                "%s: one weight matrix must stay below 2 GiB", who);
   if (M == 0 || N == 0) return 0;
   const bool premul = (group % 128) != 0;
+  if (g_decode_path == 0 && !premul && M <= kStreamMaxRows) {
+    const int rc = hn_stream_linear_impl(mats, x, ld_x, w0.q, w0.s, w1.q, w1.s, w0.ld_q, w0.ld_s,
+                                         out, ld_o, M, N, K, group, s);
+    if (rc <= 0) return rc;
+  }
   const int tiles = hn_cdiv(N, kTileN);
   for (long m0 = 0; m0 < M; m0 += kMaxRows) {
     const int rows = (int)((M - m0) > kMaxRows ? kMaxRows : (M - m0));
@@ -690,6 +717,17 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
                need);
   hipStream_t s = (hipStream_t)stream;
   const bool premul = (group % 128) != 0;
+  if (g_decode_path == 0 && !premul && max_rows_per_expert <= kStreamMaxRows &&
+      hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
+                             max_rows_per_expert, H, I, group, h_ws, I, s, 1) == 0 &&
+      hn_stream_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E,
+                             max_rows_per_expert, H, I, group, y_perm, H, s, 1) == 0) {
+    int rc = hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
+                                    max_rows_per_expert, H, I, group, h_ws, I, s, 0);
+    if (rc) return rc;
+    return hn_stream_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E,
+                                  max_rows_per_expert, H, I, group, y_perm, H, s, 0);
+  }
   const int rmax = (int)max_rows_per_expert;
   SkinnyArgs A = {};
   A.table = (const ExpertW4*)table;

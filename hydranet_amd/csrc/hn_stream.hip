@@ -1,0 +1,708 @@
+// Persistent streaming W4A16 kernels for decode, gfx950.
+//
+//   out[m, n] = sum_k x[m, k] * W[n, k],  W[n, k] = (nibble - 8) * scale[n, k / 128]
+//
+// Replaces, for up to 8 tokens per weight matrix and group size 128, the
+// per-expert Triton int4_matmul_kernel launches (kernels/int4_gemm.py:25-121)
+// and their SwiGLU epilogue (kernels/int4_gemm.py:175-193), one launch per
+// projection over every active expert of a layer.
+//
+// Work decomposition
+//  * A "column" is (problem, token chunk, 16-row tile).  A problem is one
+//    weight matrix (or the gate/up pair) with its tokens: one expert in a
+//    grouped MoE launch.  The grid is one workgroup per CU; each walks a
+//    contiguous range of columns, so the active-expert count is read on the
+//    device and the work is balanced over the CUs.
+//  * The KW <= 8 waves of a workgroup split K (LPW groups of 128 k each).  A
+//    wave keeps NBUF register buffers of weights and issues the loads of
+//    column c + NBUF - 1 before it unpacks column c.
+//  * Weight loads: 8 rows x 128 B per instruction (full cache lines,
+//    non-temporal), "lo" = tile rows 0-7, "hi" = rows 8-15, each over a group
+//    pair (g, g+1): lanes with MFMA column < 8 receive group g of row col % 8,
+//    lanes >= 8 group g+1 of the same row.
+//  * The MFMA A operand has two rows per token: row 2t + p holds token t's
+//    activations of group g + p.  One MFMA chain over a lo (hi) load thus
+//    yields group g of rows 0-7 (8-15) in its even D rows and group g + 1 in
+//    its odd D rows; a single lane exchange per column (DPP row_ror:8) adds
+//    the two.  Up to 8 tokens per chunk.
+//
+// Arithmetic (biased nibbles)
+//  * A packed dword w holds k0..k7 (k0 in bits 0-3).  (w & 0x000F000F) |
+//    0x64006400 is the fp16 pair (1024 + n_k0, 1024 + n_k4); with mask
+//    0x00F000F0 it is (1024 + 16 n_k1, 1024 + 16 n_k5); w >> 8 gives k2,k6 and
+//    k3,k7 the same way.  Five VALU operations per dword; the fp16 values are
+//    exact.  Output order k = (0,4,1,5,2,6,3,7) (hn_perm8).
+//  * The activations are staged in that order with the odd k (high nibbles)
+//    multiplied by 1/16 (exact for normal fp16), so every product in the
+//    MFMA is x * (n + bias): bias 1024 for even k, 64 for odd k.  The exact
+//    correction C(t, g) = sum_even 1032 x + sum_odd 1152 x/16 over the group
+//    is computed once per staged chunk in fp32; the MFMA chain starts from
+//    -C, so after it the accumulator holds sum_k x (n - 8) for that group.
+//  * The group scale multiplies that fp32 partial (v_fma_mix_f32, the scale
+//    read as fp16).  Products in the chain are exact; the fp32 sums carry
+//    magnitudes ~1024 |x|, i.e. a relative error ~1e-5 of the result, well
+//    inside the fp16 output rounding.
+#include "hn_common.h"
+
+namespace {
+
+constexpr int kTileN = 16;
+constexpr uint32_t kOOB = 0x7ffffff0u;
+constexpr int kMaxActive = 256;
+constexpr int kMaxWaves = 8;  // per workgroup, one workgroup per CU: 2 per SIMD
+constexpr int kMaxTc = 8;     // tokens per chunk (two MFMA rows each)
+
+struct SExpert {
+  const uint8_t* gate_q; const h16* gate_s;
+  const uint8_t* up_q;   const h16* up_s;
+  const uint8_t* down_q; const h16* down_s;
+};
+
+struct StreamArgs {
+  // single problem
+  const h16* x; int ld_x; int M;
+  const uint8_t* q[2];
+  const h16* s[2];
+  h16* out; int ld_o;
+  int phase;  // grouped: 0 gate/up + SiLU (N = I, K = H); 1 down (N = H, K = I)
+  // shape, shared by every problem of the launch
+  int N, K;
+  int ld_q;   // packed row stride (bytes)
+  int ld_s;   // scale row stride (elements)
+  int tc;     // tokens per chunk
+  int ldx;    // LDS row stride of the staged activations (halves)
+  int npair;  // group pairs per staged row (KW * LPW / 2)
+  uint32_t m_lo, m_hi, magic;
+};
+
+template <int MATS, int PAIRS>
+struct WBuf {
+  u32x4 lo[MATS][PAIRS], hi[MATS][PAIRS];
+  h16 slo[MATS][PAIRS], shi[MATS][PAIRS];
+};
+
+struct Problem {
+  const h16* x;
+  h16* out;
+  int rows;  // tokens of this problem
+  const uint8_t* q[2];
+  const h16* s[2];
+};
+
+// Grouped-launch metadata.  The kernel takes these as separate __restrict__
+// arguments: it never writes them, which lets the compiler read them with
+// scalar loads (a vector load here would make the next wait on the weight
+// loads count it, in order, behind them).
+struct Meta {
+  const SExpert* __restrict__ table;
+  const int* __restrict__ active;
+  const int* __restrict__ offsets;
+};
+
+template <bool GROUPED>
+__device__ __forceinline__ Problem resolve(const StreamArgs& A, const Meta& mt, int a) {
+  Problem p;
+  if (!GROUPED) {
+    p.x = A.x;
+    p.out = A.out;
+    p.rows = A.M;
+    p.q[0] = A.q[0]; p.s[0] = A.s[0];
+    p.q[1] = A.q[1]; p.s[1] = A.s[1];
+  } else {
+    const int e = mt.active[a];
+    const int t0 = mt.offsets[e];
+    p.rows = mt.offsets[e + 1] - t0;
+    const SExpert& ew = mt.table[e];
+    if (A.phase == 0) {
+      p.q[0] = ew.gate_q; p.s[0] = ew.gate_s;
+      p.q[1] = ew.up_q;   p.s[1] = ew.up_s;
+    } else {
+      p.q[0] = ew.down_q; p.s[0] = ew.down_s;
+      p.q[1] = ew.down_q; p.s[1] = ew.down_s;
+    }
+    p.x = A.x + (long)t0 * A.ld_x;
+    p.out = A.out + (long)t0 * A.ld_o;
+  }
+  return p;
+}
+
+// One column's loads for this wave: group pairs [g0, g0 + gw) of tile `tile`.
+// Lane (col, q): lo = row n0 + col%8, hi = row n0 + 8 + col%8, 16 bytes at
+// chunk q of group g (col < 8) or g + 1 (col >= 8); the scale of that (row,
+// group).  Per-pair offsets are immediate offsets; the wave-uniform base is
+// soffset, moved out of the descriptor's range for pairs past gw (those
+// loads return 0 without touching memory; gw == 0 issues no traffic).
+// A group g + 1 past K (odd gw) is read but meets zero activations.
+template <int MATS, int PAIRS>
+__device__ __forceinline__ void issue(WBuf<MATS, PAIRS>& b, const Problem& pr,
+                                      const StreamArgs& A, int tile, int g0, int gw, int col,
+                                      int q) {
+  const int N = A.N, ldq = A.ld_q, lds2 = 2 * A.ld_s;
+  const int rlo = tile * kTileN + (col & 7), rhi = rlo + 8;
+  const int odd = col >= 8 ? 1 : 0;
+  const int ch = q + 4 * odd;
+  const uint32_t vlo = rlo < N ? (uint32_t)(rlo * ldq + 16 * ch) : kOOB;
+  const uint32_t vhi = rhi < N ? (uint32_t)(rhi * ldq + 16 * ch) : kOOB;
+  const uint32_t vslo = rlo < N ? (uint32_t)(rlo * lds2 + 2 * odd) : kOOB;
+  const uint32_t vshi = rhi < N ? (uint32_t)(rhi * lds2 + 2 * odd) : kOOB;
+  const uint32_t sq = (uint32_t)(g0 * 64), ss = (uint32_t)(g0 * 2);
+  __amdgpu_buffer_rsrc_t rq[MATS], rs[MATS];
+#pragma unroll
+  for (int mt = 0; mt < MATS; ++mt) {
+    rq[mt] = __builtin_amdgcn_make_buffer_rsrc((void*)pr.q[mt], (short)0, N * ldq, 0x00020000);
+    rs[mt] = __builtin_amdgcn_make_buffer_rsrc((void*)pr.s[mt], (short)0, N * lds2, 0x00020000);
+  }
+  // issue order = use order (pair, matrix, lo/hi)
+#pragma unroll
+  for (int pi = 0; pi < PAIRS; ++pi) {
+    const bool pv = 2 * pi < gw;
+    const uint32_t soq = pv ? sq : kOOB, sos = pv ? ss : kOOB;
+#pragma unroll
+    for (int mt = 0; mt < MATS; ++mt) {
+      b.lo[mt][pi] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vlo + 128 * pi, soq, 2));
+      b.slo[mt][pi] = __builtin_bit_cast(
+          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vslo + 4 * pi, sos, 0));
+      b.hi[mt][pi] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vhi + 128 * pi, soq, 2));
+      b.shi[mt][pi] = __builtin_bit_cast(
+          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vshi + 4 * pi, sos, 0));
+    }
+  }
+}
+
+// Biased unpack of one packed dword: (1024 + n) for even k, (1024 + 16 n)
+// for odd k, in the order (k0,k4, k1,k5, k2,k6, k3,k7).
+__device__ __forceinline__ half8_t unpack_biased(uint32_t w, const HnUnpackRegs& c) {
+  const uint32_t w8 = w >> 8;
+  const u32x4 r = {hn_and_or(w, c.m_lo, c.magic), hn_and_or(w, c.m_hi, c.magic),
+                   hn_and_or(w8, c.m_lo, c.magic), hn_and_or(w8, c.m_hi, c.magic)};
+  return __builtin_bit_cast(half8_t, r);
+}
+
+// Unpack + MFMA of one column for this wave.  acc_lo / acc_hi: D rows 4q + r
+// (token 2q + r/2, group parity r%2) of the lo / hi chains.
+template <int MATS, int PAIRS>
+__device__ __forceinline__ void compute(const WBuf<MATS, PAIRS>& b, const h16* xs,
+                                        const float* cs, int ldx, int pb0, int gw, int arow_i,
+                                        int q, const HnUnpackRegs& ur, float4_t acc_lo[MATS],
+                                        float4_t acc_hi[MATS]) {
+#pragma unroll
+  for (int mt = 0; mt < MATS; ++mt) {
+    acc_lo[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    acc_hi[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int pi = 0; pi < PAIRS; ++pi) {
+    if (2 * pi < gw) {  // uniform
+      const h16* arow = xs + arow_i * ldx + (pb0 + pi) * 128 + 32 * q;
+      half8_t a[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[t] = *reinterpret_cast<const half8_t*>(arow + 8 * t);
+      const float4_t negc = *reinterpret_cast<const float4_t*>(cs + (pb0 + pi) * 16 + 4 * q);
+#pragma unroll
+      for (int mt = 0; mt < MATS; ++mt) {
+        float4_t cl = negc, ch = negc;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], unpack_biased(b.lo[mt][pi][t], ur),
+                                                      cl, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], unpack_biased(b.hi[mt][pi][t], ur),
+                                                      ch, 0, 0, 0);
+        const float sl = (float)b.slo[mt][pi], sh = (float)b.shi[mt][pi];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc_lo[mt][r] = __builtin_fmaf(sl, cl[r], acc_lo[mt][r]);
+          acc_hi[mt][r] = __builtin_fmaf(sh, ch[r], acc_hi[mt][r]);
+        }
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float xor8(float v) {  // lane col ^ 8 of the same 16-lane row
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+}
+
+// Activation staging.  Token t, group g goes to LDS row 2t + (g & 1), columns
+// (g >> 1) * 128 + k % 128, in unpack order with odd k scaled by 1/16; groups
+// past K are zero.  Out-of-range threads repeat the last block (same value to
+// the same address), so loads and stores are branch-free.
+struct StageGeom {
+  int m0, Mc, blk_per_tok, nblk;
+};
+
+__device__ __forceinline__ void stage_load(const StreamArgs& A, const h16* x,
+                                           const StageGeom& sg, int base, half8_t v[4]) {
+  const int tid = threadIdx.x, nthr = blockDim.x, K = A.K;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = min(base + tid + j * nthr, sg.nblk - 1);
+    const int t = i / sg.blk_per_tok;
+    const int k = min((i - t * sg.blk_per_tok) * 8, K - 8);
+    v[j] = *reinterpret_cast<const half8_t*>(x + (long)(sg.m0 + t) * A.ld_x + k);
+  }
+}
+
+__device__ __forceinline__ void stage_store(const StreamArgs& A, const StageGeom& sg, int base,
+                                            const half8_t v[4], h16* xs) {
+  const int tid = threadIdx.x, nthr = blockDim.x, K = A.K;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = min(base + tid + j * nthr, sg.nblk - 1);
+    const int t = i / sg.blk_per_tok;
+    const int b = i - t * sg.blk_per_tok;
+    const int g = b >> 4;
+    const bool in_k = b * 8 < K;
+    half8_t p;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const h16 s = v[j][hn_perm8(e)];
+      p[e] = in_k ? ((e & 2) ? s * (h16)0.0625f : s) : (h16)0.0f;
+    }
+    *reinterpret_cast<half8_t*>(xs + (2 * t + (g & 1)) * A.ldx + (g >> 1) * 128 + (b & 15) * 8) = p;
+  }
+}
+
+// Bias corrections of the staged chunk: cs[pair * 16 + R] = -C for MFMA row
+// R = 2t + p (token t, group 2 * pair + p); 0 for rows past the chunk.
+__device__ __forceinline__ void stage_corrections(const StreamArgs& A, int Mc, const h16* xs,
+                                                  float* cs) {
+  const int n = A.npair * 16;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int pb = i >> 4, R = i & 15;
+    float c = 0.f;
+    if ((R >> 1) < Mc) {
+      const h16* src = xs + R * A.ldx + pb * 128;
+      for (int j = 0; j < 16; ++j) {
+        const half8_t v = *reinterpret_cast<const half8_t*>(src + 8 * j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c = __builtin_fmaf((float)v[e], (e & 2) ? 1152.f : 1032.f, c);
+      }
+    }
+    cs[i] = -c;
+  }
+}
+
+// Whole staging of one chunk (used when the staged chunk changes mid-stream).
+__device__ __forceinline__ void stage(const StreamArgs& A, const h16* x, const StageGeom& sg,
+                                      h16* xs, float* cs) {
+  const int nthr = blockDim.x;
+  __syncthreads();  // the previous chunk is no longer read
+  for (int base = 0; base < sg.nblk; base += 4 * nthr) {
+    half8_t v[4];
+    stage_load(A, x, sg, base, v);
+    stage_store(A, sg, base, v, xs);
+  }
+  __syncthreads();
+  stage_corrections(A, sg.Mc, xs, cs);
+  __syncthreads();
+}
+
+// Column cursor: column -> (problem, chunk, tile).  Columns only move
+// forward; the current problem's chunk range [lo, hi) sits in scalar registers.
+struct Cursor {
+  int a, lo, hi;
+};
+
+__device__ __forceinline__ void locate(Cursor& cu, const int* chunk_off, int nprob, int tiles,
+                                       int c, int& prob, int& chunk, int& tile) {
+  const int gc = c / tiles;
+  tile = c - gc * tiles;
+  while (gc >= cu.hi && cu.a + 1 < nprob) {
+    ++cu.a;
+    cu.lo = cu.hi;
+    cu.hi = __builtin_amdgcn_readfirstlane(chunk_off[cu.a + 1]);
+  }
+  prob = cu.a;
+  chunk = gc - cu.lo;
+}
+
+// At most 8 waves per workgroup and one workgroup per CU: 2 waves per SIMD,
+// 256 VGPRs each.
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF>
+__global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
+                                                     const SExpert* __restrict__ table,
+                                                     const int* __restrict__ active,
+                                                     const int* __restrict__ n_active,
+                                                     const int* __restrict__ offsets) {
+  constexpr int PAIRS = LPW / 2;
+  static_assert(NBUF == 2 || NBUF == 3, "two or three column buffers");
+  const Meta meta = {table, active, offsets};
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int chunk_off[kMaxActive + 1];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int KW = blockDim.x >> 6;
+  const int col = lane & 15;
+  const int q = lane >> 4;
+  const int N = A.N, TC = A.tc;
+  const int G = A.K >> 7;
+  const int tiles = (N + kTileN - 1) / kTileN;
+  const int g0 = wave * LPW;                   // this wave's first group
+  const int gw = max(0, min(LPW, G - g0));     // its groups (uniform)
+  const int pb0 = g0 >> 1;                     // its first group pair
+  h16* xs = reinterpret_cast<h16*>(smem);
+  float* cs = reinterpret_cast<float*>(smem + (size_t)TC * 2 * A.ldx * 2);
+  float2* red = reinterpret_cast<float2*>(cs + A.npair * 16);
+  constexpr int kRedSlots = (kMaxWaves - 1) * MATS * 64;  // per parity
+  HnUnpackRegs ur;
+  ur.m_lo = A.m_lo;
+  ur.m_hi = A.m_hi;
+  ur.magic = hn_vgpr(A.magic);
+
+  // ---- token chunks per problem -> prefix (chunk_off); columns = chunks * tiles
+  int nprob = 1;
+  if (GROUPED) {
+    nprob = min(*n_active, kMaxActive);
+    for (int i = tid; i < nprob; i += blockDim.x) {
+      const int e = active[i];
+      const int rows = offsets[e + 1] - offsets[e];
+      chunk_off[i + 1] = (rows + TC - 1) / TC;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      chunk_off[0] = 0;
+      for (int i = 1; i <= nprob; ++i) chunk_off[i] += chunk_off[i - 1];
+    }
+  } else if (tid == 0) {
+    chunk_off[0] = 0;
+    chunk_off[1] = (A.M + TC - 1) / TC;
+  }
+  // reduction slots of waves this workgroup does not have stay zero
+  for (int i = tid; i < 2 * kRedSlots; i += blockDim.x) {
+    const int slot = (i / (MATS * 64)) % (kMaxWaves - 1);
+    if (slot >= KW - 1) red[i] = float2{0.f, 0.f};
+  }
+  __syncthreads();
+  if (nprob <= 0) return;
+  const int C = __builtin_amdgcn_readfirstlane(chunk_off[nprob]) * tiles;
+  const int cb = (int)((long)C * blockIdx.x / gridDim.x);
+  const int ce = (int)((long)C * (blockIdx.x + 1) / gridDim.x);
+  if (cb >= ce) return;  // uniform over the workgroup
+
+  const int off1 = __builtin_amdgcn_readfirstlane(chunk_off[1]);
+  Cursor cu_i = {0, 0, off1}, cu_c = {0, 0, off1};
+  int pi_last;        // problem of the last issued column
+  Problem pi_pr;      // its weights
+  int st_p, st_ch;    // staged (problem, chunk)
+  Problem st_pr;      // its activations / output
+  StageGeom sg;
+  int ci = cb;        // next column to issue
+  int parity = 0;
+  const int blk_per_tok = A.npair * 2 * 16;
+
+  auto issue_next = [&](WBuf<MATS, PAIRS>& b) {
+    const bool more = ci < ce;
+    int p = 0, ch = 0, t = 0;
+    if (more) {
+      locate(cu_i, chunk_off, nprob, tiles, ci, p, ch, t);
+      if (p != pi_last) {
+        pi_pr = resolve<GROUPED>(A, meta, p);
+        pi_last = p;
+      }
+    }
+    issue<MATS, PAIRS>(b, pi_pr, A, t, g0, more ? gw : 0, col, q);
+    ++ci;
+  };
+  auto geom = [&](int ch) {
+    StageGeom g;
+    g.m0 = ch * TC;
+    g.Mc = min(TC, st_pr.rows - g.m0);
+    g.blk_per_tok = blk_per_tok;
+    g.nblk = g.Mc * blk_per_tok;
+    return g;
+  };
+
+  WBuf<MATS, PAIRS> b0, b1, b2;
+  // ---- prologue: the first chunk's activations are requested before the
+  //      first columns' weights and waited for alone
+  {
+    int p, ch, t;
+    locate(cu_c, chunk_off, nprob, tiles, cb, p, ch, t);
+    st_p = p;
+    st_ch = ch;
+    st_pr = resolve<GROUPED>(A, meta, p);
+    pi_pr = st_pr;
+    pi_last = p;
+    sg = geom(ch);
+    half8_t v[4];
+    stage_load(A, st_pr.x, sg, 0, v);
+    issue_next(b0);
+    if (NBUF == 3) issue_next(b1);
+    stage_store(A, sg, 0, v, xs);
+    for (int base = 4 * (int)blockDim.x; base < sg.nblk; base += 4 * blockDim.x) {
+      stage_load(A, st_pr.x, sg, base, v);
+      stage_store(A, sg, base, v, xs);
+    }
+    __syncthreads();
+    stage_corrections(A, sg.Mc, xs, cs);
+    __syncthreads();
+  }
+
+  // One column: restage if its chunk changes (before the next column's loads
+  // go out, so waiting for the activations never waits for those), issue
+  // column c + NBUF - 1, unpack/MFMA column c, reduce over the waves.
+  auto step = [&](int c, const WBuf<MATS, PAIRS>& cur, WBuf<MATS, PAIRS>& nxt) {
+    int t = 0;
+    if (c < ce) {  // uniform
+      int p, ch;
+      locate(cu_c, chunk_off, nprob, tiles, c, p, ch, t);
+      if (p != st_p || ch != st_ch) {
+        if (p != st_p) st_pr = resolve<GROUPED>(A, meta, p);
+        st_p = p;
+        st_ch = ch;
+        sg = geom(ch);
+        stage(A, st_pr.x, sg, xs, cs);
+      }
+    }
+    issue_next(nxt);
+    if (c < ce) {
+      const int Mc = sg.Mc;
+      const int arow_i = 2 * min(col >> 1, Mc - 1) + (col & 1);
+      float4_t acc_lo[MATS], acc_hi[MATS];
+      compute<MATS, PAIRS>(cur, xs, cs, A.ldx, pb0, gw, arow_i, q, ur, acc_lo, acc_hi);
+      // lane (col, q): row n0 + col, tokens 2q, 2q + 1 (both group parities)
+      float2 v[MATS];
+      const bool low = col < 8;
+#pragma unroll
+      for (int mt = 0; mt < MATS; ++mt) {
+        const float e0 = low ? acc_lo[mt][0] : acc_hi[mt][1];
+        const float u0 = low ? acc_hi[mt][0] : acc_lo[mt][1];
+        const float e1 = low ? acc_lo[mt][2] : acc_hi[mt][3];
+        const float u1 = low ? acc_hi[mt][2] : acc_lo[mt][3];
+        v[mt] = float2{e0 + xor8(u0), e1 + xor8(u1)};
+      }
+      // KW-wave reduction through LDS (parity-buffered: one barrier per
+      // column), summed in wave order by wave 0, which writes the tile
+      float2* rb = red + parity * kRedSlots;
+      if (wave > 0) {
+#pragma unroll
+        for (int mt = 0; mt < MATS; ++mt) rb[((wave - 1) * MATS + mt) * 64 + lane] = v[mt];
+      }
+      __syncthreads();
+      if (wave == 0) {
+        float2 o[kMaxWaves - 1][MATS];
+#pragma unroll
+        for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
+#pragma unroll
+          for (int mt = 0; mt < MATS; ++mt) o[w2][mt] = rb[(w2 * MATS + mt) * 64 + lane];
+#pragma unroll
+        for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
+#pragma unroll
+          for (int mt = 0; mt < MATS; ++mt) {
+            v[mt].x += o[w2][mt].x;
+            v[mt].y += o[w2][mt].y;
+          }
+        const int row = t * kTileN + col;
+        if (row < N) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int m = 2 * q + j;
+            if (m < Mc) {
+              const float g = j ? v[0].y : v[0].x;
+              h16 o16;
+              if (EPI == 1) {
+                const float u = j ? v[MATS - 1].y : v[MATS - 1].x;
+                o16 = (h16)(hn_silu((float)(h16)g) * (float)(h16)u);
+              } else {
+                o16 = (h16)g;
+              }
+              st_pr.out[(long)(sg.m0 + m) * A.ld_o + row] = o16;
+            }
+          }
+        }
+      }
+      parity ^= 1;
+    }
+  };
+
+  for (int c = cb; c < ce; c += NBUF) {
+    if (NBUF == 2) {
+      step(c, b0, b1);
+      step(c + 1, b1, b0);
+    } else {
+      step(c, b0, b2);
+      step(c + 1, b1, b0);
+      step(c + 2, b2, b1);
+    }
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kLdsPerCu = 160 * 1024;
+constexpr int kStaticLds = 1040;  // chunk_off[]
+
+struct GroupedPtrs {
+  const SExpert* table;
+  const int* active;
+  const int* n_active;
+  const int* offsets;
+};
+
+struct StreamPlan {
+  bool ok;
+  int lpw, nbuf, kw, tc, ldx, npair;
+  int lds;  // dynamic LDS bytes per workgroup
+};
+
+// One workgroup per CU of KW <= 8 waves; LPW (2..16) groups of 128 k per wave
+// per column, the smallest that covers K with 8 waves; three column buffers
+// when they fit the register budget, else two.  tc <= 8 tokens per chunk,
+// limited by the LDS left after the corrections and the reduction buffers.
+StreamPlan stream_plan(long K, int mats, long rows) {
+  StreamPlan p{};
+  const long G = K / 128;
+  int lpw = 2;
+  while (lpw < 16 && (G + lpw - 1) / lpw > kMaxWaves) lpw *= 2;
+  const long kw = (G + lpw - 1) / lpw;
+  if (kw > kMaxWaves || rows < 1 || K % 128 != 0) return p;
+  p.lpw = lpw;
+  p.nbuf = mats * lpw * 3 <= 24 ? 3 : 2;
+  p.kw = (int)kw;
+  p.npair = (int)(kw * lpw / 2);
+  p.ldx = p.npair * 128 + 8;  // row stride = 16 B mod 256 B: conflict-free A reads
+  const int red = 2 * (kMaxWaves - 1) * mats * 64 * 8;
+  const int cs = p.npair * 16 * 4;
+  const int per_tok = 2 * p.ldx * 2;
+  const int want = (int)(rows < kMaxTc ? rows : kMaxTc);
+  const int tcmax = (kLdsPerCu - kStaticLds - red - cs) / per_tok;
+  p.tc = tcmax < want ? tcmax : want;
+  if (p.tc < 1) return p;
+  p.lds = p.tc * per_tok + cs + red;
+  p.ok = true;
+  return p;
+}
+
+int num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF>
+int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
+  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF>;
+  static int attr = -1;  // per instantiation
+  if (attr < 0) {
+    attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               kLdsPerCu - kStaticLds) == hipSuccess ? 1 : 0;
+    if (!attr) (void)hipGetLastError();  // plans then stay within 64 KiB
+  }
+  if (!attr && p.lds > 64 * 1024 - kStaticLds) return 1;
+  hipLaunchKernelGGL(kern, dim3(num_cus()), dim3(p.kw * 64), (size_t)p.lds, s, A, g.table,
+                     g.active, g.n_active, g.offsets);
+  return 0;
+}
+
+template <bool GROUPED, int MATS, int EPI>
+int launch_stream(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p,
+                  hipStream_t s) {
+  if constexpr (MATS == 2) {
+    if (p.lpw == 2) return launch_one<GROUPED, MATS, EPI, 2, 3>(A, g, p, s);
+    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 3>(A, g, p, s);
+    if (p.lpw == 8) return launch_one<GROUPED, MATS, EPI, 8, 2>(A, g, p, s);
+  } else {
+    if (p.lpw == 2) return launch_one<GROUPED, MATS, EPI, 2, 3>(A, g, p, s);
+    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 3>(A, g, p, s);
+    if (p.lpw == 8) return launch_one<GROUPED, MATS, EPI, 8, 3>(A, g, p, s);
+    if (p.lpw == 16) return launch_one<GROUPED, MATS, EPI, 16, 2>(A, g, p, s);
+  }
+  return 1;
+}
+
+void fill_common(StreamArgs& A, const StreamPlan& p, long N, long K) {
+  A.N = (int)N;
+  A.K = (int)K;
+  A.tc = p.tc;
+  A.ldx = p.ldx;
+  A.npair = p.npair;
+  A.m_lo = 0x000F000Fu;
+  A.m_hi = 0x00F000F0u;
+  A.magic = 0x64006400u;
+}
+
+}  // namespace
+
+// Streaming decode, single problem (the entry points of hn_gemv.hip call this
+// first).  Returns 1 when the shape is not handled here (the caller then uses
+// the split-K kernels), 0 after a launch, a HIP error code if the launch failed.
+extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const void* q0,
+                                     const void* s0, const void* q1, const void* s1, long ld_q,
+                                     long ld_s, void* out, long ld_o, long M, long N, long K,
+                                     long group, void* stream) {
+  const StreamPlan p = stream_plan(K, mats, M);
+  if (!p.ok || group != 128 || M > p.tc) return 1;
+  if (mats == 2 && p.lpw > 8) return 1;
+  if (N * ld_q >= (1L << 31) || N * ld_s * 2 >= (1L << 31) || ld_x >= (1L << 31) ||
+      ld_o >= (1L << 31))
+    return 1;
+  StreamArgs A = {};
+  A.x = (const h16*)x;
+  A.ld_x = (int)ld_x;
+  A.M = (int)M;
+  A.q[0] = (const uint8_t*)q0; A.s[0] = (const h16*)s0;
+  A.q[1] = (const uint8_t*)q1; A.s[1] = (const h16*)s1;
+  A.ld_q = (int)ld_q;
+  A.ld_s = (int)ld_s;
+  A.out = (h16*)out;
+  A.ld_o = (int)ld_o;
+  fill_common(A, p, N, K);
+  hipStream_t s = (hipStream_t)stream;
+  const GroupedPtrs g = {};
+  const int rc = mats == 2 ? launch_stream<false, 2, 1>(A, g, p, s)
+                           : launch_stream<false, 1, 0>(A, g, p, s);
+  if (rc) return rc;
+  HN_LAUNCH_CHECK("hn_stream_linear");
+  return 0;
+}
+
+// Streaming decode, grouped over the active experts of one MoE layer; phase 0
+// is gate/up + SiLU into h, phase 1 the down projection.  dry_run: only say
+// whether the shape is handled (0) or not (1).
+extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const void* table,
+                                      const int* active, const int* n_active, const int* offsets,
+                                      long E, long max_rows, long H, long I, long group, void* out,
+                                      long ld_o, void* stream, int dry_run) {
+  const int mats = phase == 0 ? 2 : 1;
+  const long K = phase == 0 ? H : I, N = phase == 0 ? I : H;
+  const StreamPlan p = stream_plan(K, mats, max_rows);
+  if (!p.ok || group != 128 || E > kMaxActive) return 1;
+  if (mats == 2 && p.lpw > 8) return 1;
+  if (N * (K / 2) >= (1L << 31) || N * (K / group) * 2 >= (1L << 31)) return 1;
+  if (dry_run) return 0;
+  StreamArgs A = {};
+  A.x = (const h16*)x;
+  A.ld_x = (int)ld_x;
+  A.phase = phase;
+  A.ld_q = (int)(K / 2);
+  A.ld_s = (int)(K / group);
+  A.out = (h16*)out;
+  A.ld_o = (int)ld_o;
+  fill_common(A, p, N, K);
+  const GroupedPtrs g = {(const SExpert*)table, active, n_active, offsets};
+  hipStream_t s = (hipStream_t)stream;
+  const int rc = mats == 2 ? launch_stream<true, 2, 1>(A, g, p, s)
+                           : launch_stream<true, 1, 0>(A, g, p, s);
+  if (rc) return rc;
+  HN_LAUNCH_CHECK("hn_stream_grouped");
+  return 0;
+}

@@ -121,6 +121,15 @@ int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int*
                                void* h_ws, void* y_perm, void* work, long work_bytes,
                                void* stream);
 
+/* Decode kernel family for hn_int4_linear, hn_int4_gate_up_silu,
+ * hn_expert_mlp_int4 and hn_grouped_expert_mlp_int4 (process-wide):
+ *   0  automatic: the persistent streaming kernels for group 128 and at most
+ *      16 rows per weight matrix, the split-K kernels otherwise (default);
+ *   1  split-K kernels only.
+ * Both give the same results to within fp32 summation order.  No counterpart
+ * in the reference; for A/B measurement and tests. */
+int hn_set_decode_path(int path);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,3 +31,13 @@ def _announce(item):
 def pytest_runtest_setup(item):
     if "gpu" in item.keywords:
         _announce(item)
+
+
+@pytest.fixture(params=[0, 1], ids=["stream", "splitk"])
+def decode_path(request):
+    """Run a decode test through both kernel families: 0 = automatic (the
+    persistent streaming kernels where they apply), 1 = split-K kernels only."""
+    from hydranet_amd import _lib
+    _lib.call("hn_set_decode_path", request.param)
+    yield request.param
+    _lib.call("hn_set_decode_path", 0)

@@ -94,8 +94,9 @@ def test_quantize_bit_exact_random_large():
 @pytest.mark.parametrize("M,N,K,g", [(1, 64, 256, 128), (1, 4096, 4096, 128), (2, 80, 512, 128),
                                      (4, 1408, 4096, 128), (16, 272, 1024, 128),
                                      (17, 96, 384, 128), (33, 48, 256, 128), (3, 64, 256, 64),
-                                     (5, 48, 256, 32), (1, 4096, 1408, 128), (8, 32, 160, 32)])
-def test_int4_linear_vs_oracle(M, N, K, g):
+                                     (5, 48, 256, 32), (1, 4096, 1408, 128), (8, 32, 160, 32),
+                                     (2, 40, 384, 128), (7, 24, 128, 128)])
+def test_int4_linear_vs_oracle(M, N, K, g, decode_path):
     from hydranet_amd.kernels.int4_gemm import int4_linear
     w = _rand_f16(M * 7 + N, (N, K), 0.02)
     x = _rand_f16(M + K, (M, K), 1.0)
@@ -160,8 +161,8 @@ def _expert(seed, H, I, g=128):
 
 
 @pytest.mark.parametrize("T,H,I", [(1, 4096, 14336), (4, 4096, 1408), (16, 512, 1024),
-                                   (3, 256, 384)])
-def test_expert_mlp_vs_torch_ref(T, H, I):
+                                   (3, 256, 384), (5, 4096, 14336)])
+def test_expert_mlp_vs_torch_ref(T, H, I, decode_path):
     from hydranet_amd.kernels import expert_mlp_int4_fused
     from hydranet_amd.kernels.int4_expert_mlp import expert_mlp_int4_from_slot
     e = _expert(T + H, H, I)

@@ -175,7 +175,7 @@ def mixtral_experts():
 
 
 @pytest.mark.parametrize("T", [1, 4, 16])
-def test_mixtral_moe_layer_c2(T, mixtral_experts):
+def test_mixtral_moe_layer_c2(T, mixtral_experts, decode_path):
     """Config C2: 8 Mixtral experts, softmax top-2, T tokens of decode."""
     from hydranet_amd.model.moe import MixtralMoELayer
     slots, cpu = mixtral_experts
@@ -216,9 +216,10 @@ def test_grouped_matches_single_expert_path(mixtral_experts):
     _close(out, ref)
 
 
-def test_glm_moe_layer_c3():
+@pytest.mark.parametrize("T", [32, 4])
+def test_glm_moe_layer_c3(T, decode_path):
     """Config C3: 128 GLM experts (4096->1408), fp16 shared expert, sigmoid top-8
-    with a seeded selection bias, T = 32."""
+    with a seeded selection bias, T = 32 (and T = 4 decode)."""
     from hydranet_amd.model.moe import GLM4MoELayer
     from hydranet_amd.preprocess.synthetic import slot_to_cpu
     slots = _slots(128, 4096, 1408, seed0=1000)
@@ -230,7 +231,7 @@ def test_glm_moe_layer_c3():
     for lin in (layer.shared_expert.gate_proj, layer.shared_expert.up_proj,
                 layer.shared_expert.down_proj):
         lin.weight.data = (torch.randn(*lin.weight.shape, generator=g) * 0.02).half().to(DEV)
-    h = _randn(9, (1, 32, 4096))
+    h = _randn(9, (1, T, 4096))
     out = layer(h.to(DEV))
     idx, w = layer.router(h.to(DEV))
     used = sorted(set(idx.view(-1).tolist()))
@@ -238,6 +239,6 @@ def test_glm_moe_layer_c3():
     shared = tuple(l.weight.data.cpu() for l in (layer.shared_expert.gate_proj,
                                                   layer.shared_expert.up_proj,
                                                   layer.shared_expert.down_proj))
-    ref = torch_ref.glm_moe(h.view(32, 4096), None, cpu, shared,
+    ref = torch_ref.glm_moe(h.view(T, 4096), None, cpu, shared,
                             routing=(idx.long().cpu(), w.cpu()))
-    _close(out.view(32, 4096), ref)
+    _close(out.view(T, 4096), ref)
