@@ -155,8 +155,8 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
   //         (the "even" MFMA operand), and (row col^8, chunk q) of group g+1 in
   //         hi if col<8 else lo (the "odd" operand, whose MFMA columns are the
   //         weight rows XOR 8).  Buffer loads: rows past N and groups past the
-  //         wave's range are out of the descriptor's range and return 0
-  //         without a memory access.
+  //         wave's range use a voffset past the descriptor's range and return
+  //         0 without a memory access.
   constexpr uint32_t kOOB = 0x7ffffff0u;
   constexpr int PAIRS = BATCH / 2;
   u32x4 wlo[MATS][PAIRS], whi[MATS][PAIRS];
@@ -183,25 +183,27 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
     const int g = g0 + gl0 + 2 * pi;   // even group of the pair
     const bool pv = 2 * pi < gw;       // uniform
     const bool ov = 2 * pi + 1 < gw;   // odd group valid (uniform)
+    // the range check covers voffset (+ immediate) only, never soffset: every
+    // offset, and the out-of-range marker, goes in voffset
 #pragma unroll
     for (int mt = 0; mt < MATS; ++mt) {
-      const uint32_t so_q = pv ? (uint32_t)(g * 64) : kOOB;
+      const uint32_t gq = (uint32_t)(g * 64);
       wlo[mt][pi] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-          rq[mt], vlo[mt], so_q, kAuxNT));
+          rq[mt], pv ? vlo[mt] + gq : kOOB, 0, kAuxNT));
       whi[mt][pi] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-          rq[mt], vhi[mt], so_q, kAuxNT));
+          rq[mt], pv ? vhi[mt] + gq : kOOB, 0, kAuxNT));
       if (PREMUL) {
         const uint32_t ie = (uint32_t)((g * 128 + 32 * q) / group);
         const uint32_t io = (uint32_t)(((g + 1) * 128 + 32 * q) / group);
         se[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
-            rs[mt], vse[mt] + 2 * ie, pv ? 0u : kOOB, 0));
+            rs[mt], pv ? vse[mt] + 2 * ie : kOOB, 0, 0));
         so[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
-            rs[mt], vso[mt] + 2 * io, ov ? 0u : kOOB, 0));
+            rs[mt], ov ? vso[mt] + 2 * io : kOOB, 0, 0));
       } else {
         se[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
-            rs[mt], vse[mt], pv ? (uint32_t)(2 * ((g * 128) / group)) : kOOB, 0));
+            rs[mt], pv ? vse[mt] + (uint32_t)(2 * ((g * 128) / group)) : kOOB, 0, 0));
         so[mt][pi] = __builtin_bit_cast(h16, __builtin_amdgcn_raw_buffer_load_b16(
-            rs[mt], vso[mt], ov ? (uint32_t)(2 * (((g + 1) * 128) / group)) : kOOB, 0));
+            rs[mt], ov ? vso[mt] + (uint32_t)(2 * (((g + 1) * 128) / group)) : kOOB, 0, 0));
       }
     }
   }

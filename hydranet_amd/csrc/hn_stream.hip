@@ -126,26 +126,29 @@ __device__ __forceinline__ Problem resolve(const StreamArgs& A, const Meta& mt, 
   return p;
 }
 
-// One column's loads for this wave: group pairs [g0, g0 + gw) of tile `tile`.
-// Lane (col, q): lo = row n0 + col%8, hi = row n0 + 8 + col%8, 16 bytes at
-// chunk q of group g (col < 8) or g + 1 (col >= 8); the scale of that (row,
-// group).  Per-pair offsets are immediate offsets; the wave-uniform base is
-// soffset, moved out of the descriptor's range for pairs past gw (those
-// loads return 0 without touching memory; gw == 0 issues no traffic).
-// A group g + 1 past K (odd gw) is read but meets zero activations.
+// One column's loads for this wave: group pairs [g0, g0 + 2 * PAIRS) of tile
+// `tile`.  Lane (col, q): lo = row n0 + col%8, hi = row n0 + 8 + col%8, 16
+// bytes at chunk q of group g (col < 8) or g + 1 (col >= 8); the scale of
+// that (row, group).  The whole offset is in voffset (+ the per-pair
+// immediate): the buffer range check covers voffset + immediate only, not
+// soffset, so soffset stays 0.  Rows past N and columns past the workgroup's
+// range (valid == false) use an offset past the descriptor's range: those
+// loads return 0 without touching memory.  Groups past K (the last wave of
+// a K that is not a multiple of 2 * LPW * 128) read the next row or nothing;
+// they meet zero activations and their products are skipped.
 template <int MATS, int PAIRS>
 __device__ __forceinline__ void issue(WBuf<MATS, PAIRS>& b, const Problem& pr,
-                                      const StreamArgs& A, int tile, int g0, int gw, int col,
-                                      int q) {
+                                      const StreamArgs& A, int tile, int g0, bool valid,
+                                      int col, int q) {
   const int N = A.N, ldq = A.ld_q, lds2 = 2 * A.ld_s;
   const int rlo = tile * kTileN + (col & 7), rhi = rlo + 8;
   const int odd = col >= 8 ? 1 : 0;
   const int ch = q + 4 * odd;
-  const uint32_t vlo = rlo < N ? (uint32_t)(rlo * ldq + 16 * ch) : kOOB;
-  const uint32_t vhi = rhi < N ? (uint32_t)(rhi * ldq + 16 * ch) : kOOB;
-  const uint32_t vslo = rlo < N ? (uint32_t)(rlo * lds2 + 2 * odd) : kOOB;
-  const uint32_t vshi = rhi < N ? (uint32_t)(rhi * lds2 + 2 * odd) : kOOB;
-  const uint32_t sq = (uint32_t)(g0 * 64), ss = (uint32_t)(g0 * 2);
+  const bool vl = valid && rlo < N, vh = valid && rhi < N;
+  const uint32_t vlo = vl ? (uint32_t)(rlo * ldq + 64 * g0 + 16 * ch) : kOOB;
+  const uint32_t vhi = vh ? (uint32_t)(rhi * ldq + 64 * g0 + 16 * ch) : kOOB;
+  const uint32_t vslo = vl ? (uint32_t)(rlo * lds2 + 2 * (g0 + odd)) : kOOB;
+  const uint32_t vshi = vh ? (uint32_t)(rhi * lds2 + 2 * (g0 + odd)) : kOOB;
   __amdgpu_buffer_rsrc_t rq[MATS], rs[MATS];
 #pragma unroll
   for (int mt = 0; mt < MATS; ++mt) {
@@ -155,18 +158,16 @@ __device__ __forceinline__ void issue(WBuf<MATS, PAIRS>& b, const Problem& pr,
   // issue order = use order (pair, matrix, lo/hi)
 #pragma unroll
   for (int pi = 0; pi < PAIRS; ++pi) {
-    const bool pv = 2 * pi < gw;
-    const uint32_t soq = pv ? sq : kOOB, sos = pv ? ss : kOOB;
 #pragma unroll
     for (int mt = 0; mt < MATS; ++mt) {
       b.lo[mt][pi] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vlo + 128 * pi, soq, 2));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vlo + 128 * pi, 0, 2));
       b.slo[mt][pi] = __builtin_bit_cast(
-          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vslo + 4 * pi, sos, 0));
+          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vslo + 4 * pi, 0, 0));
       b.hi[mt][pi] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vhi + 128 * pi, soq, 2));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vhi + 128 * pi, 0, 2));
       b.shi[mt][pi] = __builtin_bit_cast(
-          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vshi + 4 * pi, sos, 0));
+          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vshi + 4 * pi, 0, 0));
     }
   }
 }
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
         pi_last = p;
       }
     }
-    issue<MATS, PAIRS>(b, pi_pr, A, t, g0, more ? gw : 0, col, q);
+    issue<MATS, PAIRS>(b, pi_pr, A, t, g0, more, col, q);
     ++ci;
   };
   auto geom = [&](int ch) {
