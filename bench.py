@@ -235,6 +235,109 @@ def bench_c2(args, T: int, n_layers: int = 4):
             / n_layers, "graph": gr is not None}
 
 
+# ----------------------------------------------------------------------------- C4
+def zipf_logits(T: int, E: int, seed: int, s: float = 1.1, device="cuda"):
+    """Router logits N(0,1) + ln p_e with Zipf(s) expert popularity (seeded)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    p = torch.tensor([1.0 / (i + 1) ** s for i in range(E)], device=device)
+    return torch.randn(T, E, generator=g, device=device) + (p / p.sum()).log()
+
+
+def bench_c4(args):
+    """One Mixtral MoE layer at prefill: 2048 tokens, top-2 of 8 experts with
+    Zipf(1.1)-skewed router logits.  Step = top-k + permute + gather + grouped
+    gate/up+SiLU GEMM + grouped down GEMM + unpermute.  Work: 2 (T k) 3 H I flops."""
+    from hydranet_amd import _lib
+    from hydranet_amd.model.moe import ExpertTable, moe_experts_forward
+    from hydranet_amd.model.router import topk_from_logits
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
+
+    H, I, g, E, T, k = 4096, 14336, 128, 8, 2048, 2
+    slots = [make_expert_slot(expert_seed(0, e), H, I, g, slot_idx=e) for e in range(E)]
+    table = ExpertTable.from_slots(slots)
+    x = normal_f16((T, H), 4242, std=1.0)
+    logits = zipf_logits(T, E, 2048)
+    idx0, _ = topk_from_logits(logits, k, mode=0)
+    sizes = torch.bincount(idx0.view(-1).long(), minlength=E).tolist()
+    flops = 2.0 * T * k * 3 * H * I
+
+    def step():
+        idx, w = topk_from_logits(logits, k, mode=0)
+        moe_experts_forward(x, idx, w, table)
+
+    for _ in range(max(2, args.warmup // 4)):
+        step()
+    torch.cuda.synchronize()
+    steps = max(5, args.steps // 10)
+    gr = _graph(step, steps)
+    t0 = time.perf_counter()
+    if gr is not None:
+        gr.replay()
+    else:
+        for _ in range(steps):
+            step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    # the two grouped GEMM launches alone, on their own stream, HIP events
+    dev = x.device
+    st = torch.cuda.Stream()
+    idx, w = topk_from_logits(logits, k, mode=0)
+    n = T * k
+    meta = torch.empty(3 * E + 2 + 2 * n, dtype=torch.int32, device=dev)
+    offs, act, nact = meta[:E + 1], meta[E + 1:2 * E + 1], meta[2 * E + 1:2 * E + 2]
+    perm, inv = meta[2 * E + 2:2 * E + 2 + n], meta[2 * E + 2 + n:]
+    x_perm = torch.empty(n, H, dtype=torch.float16, device=dev)
+    h_ws = torch.empty(n, I, dtype=torch.float16, device=dev)
+    y_perm = torch.empty(n, H, dtype=torch.float16, device=dev)
+    sp = ctypes_stream(st)
+    torch.cuda.synchronize()
+    _lib.call("hn_moe_permute", _lib.ptr(idx), T, k, E, _lib.ptr(offs), _lib.ptr(perm),
+              _lib.ptr(inv), _lib.ptr(act), _lib.ptr(nact), sp)
+    _lib.call("hn_moe_gather", _lib.ptr(x), H, _lib.ptr(perm), k, _lib.ptr(offs), E,
+              _lib.ptr(x_perm), H, n, H, sp)
+    kt = {}
+    for phase, name in ((0, "gate_up_silu"), (1, "down")):
+        def launch():
+            _lib.call("hn_grouped_expert_phase_int4", phase, _lib.ptr(x_perm), _lib.ptr(table.dev),
+                      _lib.ptr(act), _lib.ptr(nact), _lib.ptr(offs), E, n, H, I, g,
+                      _lib.ptr(h_ws), _lib.ptr(y_perm), sp)
+        for _ in range(2):
+            launch()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        reps = 10
+        e0.record(st)
+        for _ in range(reps):
+            launch()
+        e1.record(st)
+        e1.synchronize()
+        kt[name] = e0.elapsed_time(e1) / reps
+    gu_flops = 2.0 * n * 2 * H * I
+    dn_flops = 2.0 * n * H * I
+    ach = gu_flops / (kt["gate_up_silu"] * 1e-3) / 1e12
+    return {"workload": "C4: one Mixtral MoE layer at prefill, 2048 tokens x 4096, top-2 of 8 "
+                        "experts (4096->14336->4096 INT4 g128), Zipf(1.1)-skewed routing; "
+                        "top-k + permute + gather + grouped gate/up GEMM + grouped down GEMM + "
+                        "unpermute",
+            "ms_per_step": round(ms, 4), "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "group_sizes": sizes,
+            "graph": gr is not None,
+            "roofline": {"bound": "mfma", "kernel": "gemm_kernel<grouped, gate+up+SiLU>",
+                         "achieved": round(ach, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4),
+                         "traffic": None, "flops_per_launch": gu_flops,
+                         "avg_us": round(kt["gate_up_silu"] * 1e3, 2),
+                         "down_avg_us": round(kt["down"] * 1e3, 2),
+                         "down_TFLOP_s": round(dn_flops / (kt["down"] * 1e-3) / 1e12, 1)}}
+
+
+def ctypes_stream(st):
+    import ctypes
+    return ctypes.c_void_p(st.cuda_stream)
+
+
 def cpu_baseline_c1(ctx, budget_s: float):
     """Torch-CPU restatement of the reference's dequantise-then-matmul path,
     timed on this host.  TEST INFRASTRUCTURE (oracle) used only as the baseline."""
@@ -281,7 +384,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4"])
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -301,6 +404,14 @@ def main():
     from hydranet_amd import _lib
     _lib.call("hn_set_decode_path", args.decode_path)
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
+    if args.workload == "c4":
+        c4 = bench_c4(args)
+        _log("c4", c4)
+        print(json.dumps({"metric": "INT4 expert-MLP prefill TFLOP/s (MoE layer, 1 GPU)",
+                          "value": c4["TFLOP_s"], "unit": "TFLOP/s", "n_gpus": 1,
+                          "ms_per_step": c4["ms_per_step"], "higher_is_better": True,
+                          "dtype": "fp16", "data": "synthetic", "config": c4}), flush=True)
+        return
     res, ctx = bench_c1(args)
     _log("c1 done", res["value"], res["unit"])
     c1 = {"GB_s": res["value"], "frac": res["roofline"]["expert_frac"],

@@ -36,9 +36,14 @@ SIGNATURES: dict[str, list] = {
     "hn_moe_unpermute": [P, L, P, P, P, L, L, P, L, P, L, L, P],
     "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],
     "hn_set_decode_path": [I],
+    "hn_grouped_expert_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, P, P, P],
 }
 
 RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long}
+
+# Tokens per weight matrix up to which the decode (skinny / streaming) kernels
+# run; above it the MFMA GEMM kernels do (kMaxRows in csrc/hn_gemv.hip).
+DECODE_MAX_ROWS = 64
 
 _lib = None
 

@@ -35,6 +35,11 @@ void hn_set_error(const char* fmt, ...);
     }                                        \
   } while (0)
 
+// Internal return code of the kernel-family dispatchers (hn_stream_*_impl,
+// hn_gemm_*_impl): the shape is not handled by that family, try another.
+// Never returned through the C ABI.
+#define HN_NOT_HANDLED (-1000)
+
 #define HN_LAUNCH_CHECK(what)                                              \
   do {                                                                     \
     hipError_t _e = hipGetLastError();                                     \

@@ -557,8 +557,8 @@ extern "C" long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long
   return (long)(ctr_bytes(ctr) + (a > b ? a : b));
 }
 
-// Persistent streaming kernels (hn_stream.hip): return 1 when a shape is not
-// theirs, 0 after a launch, < 0 on error.
+// Persistent streaming kernels (hn_stream.hip): return HN_NOT_HANDLED when a
+// shape is not theirs, 0 after a launch, a hipError_t if the launch failed.
 extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const void* q0,
                                      const void* s0, const void* q1, const void* s1, long ld_q,
                                      long ld_s, void* out, long ld_o, long M, long N, long K,
@@ -567,6 +567,16 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
                                       const int* active, const int* n_active, const int* offsets,
                                       long E, long max_rows, long H, long I, long group, void* out,
                                       long ld_o, void* stream, int dry_run);
+
+// Prefill GEMM kernels (hn_gemm.hip): same return convention.
+extern "C" int hn_gemm_linear_impl(int mats, const void* x, long ld_x, const void* q0,
+                                   const void* s0, const void* q1, const void* s1, long ld_q,
+                                   long ld_s, void* out, long ld_o, long M, long N, long K,
+                                   long group, void* stream);
+extern "C" int hn_gemm_grouped_impl(int phase, const void* x, long ld_x, const void* table,
+                                    const int* active, const int* n_active, const int* offsets,
+                                    long E, long rows, long H, long I, long group, void* out,
+                                    long ld_o, void* stream);
 
 // Decode kernel family: 0 = automatic (streaming kernels where they apply),
 // 1 = split-K kernels only.  Process-wide; for A/B measurement and tests.
@@ -599,10 +609,15 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
                "%s: one weight matrix must stay below 2 GiB", who);
   if (M == 0 || N == 0) return 0;
   const bool premul = (group % 128) != 0;
+  if (M > kMaxRows) {
+    const int rc = hn_gemm_linear_impl(mats, x, ld_x, w0.q, w0.s, w1.q, w1.s, w0.ld_q, w0.ld_s,
+                                       out, ld_o, M, N, K, group, s);
+    if (rc != HN_NOT_HANDLED) return rc;
+  }
   if (g_decode_path == 0 && !premul && M <= kStreamMaxRows) {
     const int rc = hn_stream_linear_impl(mats, x, ld_x, w0.q, w0.s, w1.q, w1.s, w0.ld_q, w0.ld_s,
                                          out, ld_o, M, N, K, group, s);
-    if (rc <= 0) return rc;
+    if (rc != HN_NOT_HANDLED) return rc;
   }
   const int tiles = hn_cdiv(N, kTileN);
   for (long m0 = 0; m0 < M; m0 += kMaxRows) {
@@ -704,8 +719,6 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
                                           void* stream) {
   const char* who = "hn_grouped_expert_mlp_int4";
   HN_ARG_CHECK(E > 0 && max_rows_per_expert >= 0 && rows >= 0, "%s: bad sizes", who);
-  HN_ARG_CHECK(max_rows_per_expert <= kMaxRows, "%s: at most %d rows per expert (got %ld); "
-               "use the grouped prefill GEMM", who, kMaxRows, max_rows_per_expert);
   HN_ARG_CHECK(H % 128 == 0 && I % 32 == 0, "%s: H=%ld must be a multiple of 128, I=%ld of 32",
                who, H, I);
   HN_ARG_CHECK(group >= 32 && group % 32 == 0 && H % group == 0 && I % group == 0,
@@ -714,6 +727,23 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
   HN_ARG_CHECK((I / 2) % 16 == 0, "%s: down rows (I/2=%ld bytes) must be 16-byte aligned", who,
                I / 2);
   if (max_rows_per_expert == 0 || rows == 0) return 0;
+  if (max_rows_per_expert > kMaxRows) {
+    // prefill: the grouped MFMA GEMM (no workspace)
+    HN_ARG_CHECK(I % 128 == 0 && E <= 256,
+                 "%s: more than %d rows per expert needs I %% 128 == 0 and E <= 256 "
+                 "(I=%ld, E=%ld)", who, kMaxRows, I, E);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = hn_gemm_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E, rows, H, I,
+                                  group, h_ws, I, s);
+    if (rc == 0)
+      rc = hn_gemm_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E, rows, H, I,
+                                group, y_perm, H, s);
+    if (rc == HN_NOT_HANDLED) {
+      hn_set_error("%s: shape not handled by the prefill GEMM (group=%ld)", who, group);
+      return -22;
+    }
+    return rc;
+  }
   const long need = hn_skinny_workspace_bytes(3, rows, H, I, E);
   HN_ARG_CHECK(work && work_bytes >= need, "%s: workspace too small (%ld < %ld)", who, work_bytes,
                need);
@@ -770,4 +800,32 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
     HN_LAUNCH_CHECK("hn_grouped_expert_mlp_int4(down)");
   }
   return 0;
+}
+
+// One phase of the grouped SwiGLU at prefill sizes (the MFMA GEMM kernels):
+// phase 0: h_ws[rows, I] = fp16(silu(x_perm Wg^T) * (x_perm Wu^T)) per expert;
+// phase 1: y_perm[rows, H] = h_ws Wd^T per expert.  Same operands as
+// hn_grouped_expert_mlp_int4; lets a caller time or schedule the phases apart.
+extern "C" int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const void* table,
+                                            const int* active, const int* n_active,
+                                            const int* offsets, long E, long rows, long H,
+                                            long I, long group, void* h_ws, void* y_perm,
+                                            void* stream) {
+  const char* who = "hn_grouped_expert_phase_int4";
+  HN_ARG_CHECK(phase == 0 || phase == 1, "%s: phase must be 0 or 1", who);
+  HN_ARG_CHECK(E > 0 && E <= 256 && rows >= 0, "%s: bad sizes (E=%ld, rows=%ld)", who, E, rows);
+  HN_ARG_CHECK(H % 128 == 0 && I % 128 == 0, "%s: H=%ld and I=%ld must be multiples of 128",
+               who, H, I);
+  HN_ARG_CHECK(aligned16(x_perm) && aligned16(h_ws) && aligned16(y_perm), "%s: misaligned", who);
+  if (rows == 0) return 0;
+  const int rc = phase == 0
+      ? hn_gemm_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E, rows, H, I, group,
+                             h_ws, I, stream)
+      : hn_gemm_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E, rows, H, I, group,
+                             y_perm, H, stream);
+  if (rc == HN_NOT_HANDLED) {
+    hn_set_error("%s: shape not handled by the GEMM kernels (group=%ld)", who, group);
+    return -22;
+  }
+  return rc;
 }

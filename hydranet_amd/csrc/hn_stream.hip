@@ -608,7 +608,7 @@ int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, h
                                kLdsPerCu - kStaticLds) == hipSuccess ? 1 : 0;
     if (!attr) (void)hipGetLastError();  // plans then stay within 64 KiB
   }
-  if (!attr && p.lds > 64 * 1024 - kStaticLds) return 1;
+  if (!attr && p.lds > 64 * 1024 - kStaticLds) return HN_NOT_HANDLED;
   hipLaunchKernelGGL(kern, dim3(num_cus()), dim3(p.kw * 64), (size_t)p.lds, s, A, g.table,
                      g.active, g.n_active, g.offsets);
   return 0;
@@ -627,7 +627,7 @@ int launch_stream(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p
     if (p.lpw == 8) return launch_one<GROUPED, MATS, EPI, 8, 3>(A, g, p, s);
     if (p.lpw == 16) return launch_one<GROUPED, MATS, EPI, 16, 2>(A, g, p, s);
   }
-  return 1;
+  return HN_NOT_HANDLED;
 }
 
 void fill_common(StreamArgs& A, const StreamPlan& p, long N, long K) {
@@ -644,18 +644,19 @@ void fill_common(StreamArgs& A, const StreamPlan& p, long N, long K) {
 }  // namespace
 
 // Streaming decode, single problem (the entry points of hn_gemv.hip call this
-// first).  Returns 1 when the shape is not handled here (the caller then uses
-// the split-K kernels), 0 after a launch, a HIP error code if the launch failed.
+// first).  Returns HN_NOT_HANDLED when the shape is not handled here (the
+// caller then uses the split-K kernels), 0 after a launch, a HIP error code if
+// the launch failed.
 extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const void* q0,
                                      const void* s0, const void* q1, const void* s1, long ld_q,
                                      long ld_s, void* out, long ld_o, long M, long N, long K,
                                      long group, void* stream) {
   const StreamPlan p = stream_plan(K, mats, M);
-  if (!p.ok || group != 128 || M > p.tc) return 1;
-  if (mats == 2 && p.lpw > 8) return 1;
+  if (!p.ok || group != 128 || M > p.tc) return HN_NOT_HANDLED;
+  if (mats == 2 && p.lpw > 8) return HN_NOT_HANDLED;
   if (N * ld_q >= (1L << 31) || N * ld_s * 2 >= (1L << 31) || ld_x >= (1L << 31) ||
       ld_o >= (1L << 31))
-    return 1;
+    return HN_NOT_HANDLED;
   StreamArgs A = {};
   A.x = (const h16*)x;
   A.ld_x = (int)ld_x;
@@ -686,9 +687,9 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
   const int mats = phase == 0 ? 2 : 1;
   const long K = phase == 0 ? H : I, N = phase == 0 ? I : H;
   const StreamPlan p = stream_plan(K, mats, max_rows);
-  if (!p.ok || group != 128 || E > kMaxActive) return 1;
-  if (mats == 2 && p.lpw > 8) return 1;
-  if (N * (K / 2) >= (1L << 31) || N * (K / group) * 2 >= (1L << 31)) return 1;
+  if (!p.ok || group != 128 || E > kMaxActive) return HN_NOT_HANDLED;
+  if (mats == 2 && p.lpw > 8) return HN_NOT_HANDLED;
+  if (N * (K / 2) >= (1L << 31) || N * (K / group) * 2 >= (1L << 31)) return HN_NOT_HANDLED;
   if (dry_run) return 0;
   StreamArgs A = {};
   A.x = (const h16*)x;

@@ -94,10 +94,13 @@ def moe_experts_forward(hidden: torch.Tensor, idx: torch.Tensor, w: torch.Tensor
               _lib.ptr(x_perm), H, n, H, st)
     h_ws = torch.empty((max(n, 1), I), dtype=torch.float16, device=dev)
     y_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
-    work = _lib.skinny_workspace(3, n, H, I, E, dev)
+    # above DECODE_MAX_ROWS tokens per expert the grouped prefill GEMM runs,
+    # which needs no workspace
+    work = _lib.skinny_workspace(3, n, H, I, E, dev) if T <= _lib.DECODE_MAX_ROWS else None
     _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(x_perm), _lib.ptr(table.dev),
               _lib.ptr(active), _lib.ptr(n_active), _lib.ptr(offsets), E, T, n, H, I, g,
-              _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work), work.numel(), st)
+              _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work),
+              0 if work is None else work.numel(), st)
     out = torch.empty((T, H), dtype=torch.float16, device=dev)
     sh = None
     if shared is not None:

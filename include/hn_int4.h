@@ -108,8 +108,9 @@ int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* i
                      long T, long k, const void* shared, long ld_sh, void* out, long ld_o, long H,
                      void* stream);
 
-/* Grouped SwiGLU over every active expert of one MoE layer in two launches
- * (<= 64 rows per expert).  x_perm [rows, H] sorted by expert; table: E x
+/* Grouped SwiGLU over every active expert of one MoE layer in two launches:
+ * the decode kernels up to 64 rows per expert, the MFMA GEMM kernels above
+ * (then the workspace may be NULL / 0 bytes).  x_perm [rows, H] sorted by expert; table: E x
  * {gate_q, gate_s, up_q, up_s, down_q, down_s} device pointers (u64); active /
  * n_active / offsets from hn_moe_permute; h_ws [rows, I] fp16 buffer;
  * y_perm [rows, H] fp16 out; work: hn_skinny_workspace_bytes(3, rows, H, I, E).
@@ -120,6 +121,18 @@ int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int*
                                long max_rows_per_expert, long rows, long H, long I, long group,
                                void* h_ws, void* y_perm, void* work, long work_bytes,
                                void* stream);
+
+/* One phase of hn_grouped_expert_mlp_int4's prefill path (the grouped MFMA GEMM):
+ * phase 0 writes h_ws [rows, I] = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T)) per expert,
+ * phase 1 writes y_perm [rows, H] = fp16(h_ws Wd^T) per expert.  Any rows per
+ * expert; E <= 256; H, I multiples of 128; group 32, 64 or a multiple of 128.
+ * No separate counterpart in the reference (its loop calls
+ * expert_mlp_int4_fused per expert, model/mixtral.py:342-354); lets a caller
+ * time or schedule the two phases apart. */
+int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const void* table,
+                                 const int* active, const int* n_active, const int* offsets,
+                                 long E, long rows, long H, long I, long group, void* h_ws,
+                                 void* y_perm, void* stream);
 
 /* Decode kernel family for hn_int4_linear, hn_int4_gate_up_silu,
  * hn_expert_mlp_int4 and hn_grouped_expert_mlp_int4 (process-wide):
