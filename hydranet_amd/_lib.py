@@ -94,6 +94,7 @@ def skinny_workspace(kind: int, M: int, N: int, K: int, E: int, device) -> torch
     return workspace(lib().hn_skinny_workspace_bytes(kind, M, N, K, E), device)
 
 
+
 def ptr(t) -> ctypes.c_void_p:
     if t is None:
         return ctypes.c_void_p(None)

@@ -9,33 +9,29 @@
 // (model/mixtral.py:327-368, model/glm4.py:421-466) at prefill sizes.
 //
 // This is the one place the path is a real dense contraction, so it is built
-// around the MFMA pipe (v_mfma_f32_16x16x32_f16):
-//  * Tile = 128 tokens x (4 waves x NB x 16) weight rows of each matrix; a wave
-//    owns NB 16-row blocks of every matrix (gate and up together for the SwiGLU
-//    form, so its epilogue has both values of an output in the same lane) for
-//    all 128 tokens.  Waves split N, never M, so each weight is dequantised by
-//    exactly one wave of the workgroup and never goes through LDS.
-//  * Weights: per 128-k group each lane issues one 16-byte buffer load per
-//    16-row block: row (block + lane % 16), bytes [16 * (lane / 16), +16) of the
-//    row's 64-byte group (one load instruction = 16 rows x 64 B).  Loads for
-//    group g + 1 are in flight while group g computes.  In registers, each
-//    packed dword becomes eight fp16 weights in k order: a byte broadcast
+// around the MFMA pipe (v_mfma_f32_32x32x16_f16, which one wave per SIMD can
+// keep busy back to back):
+//  * Tile = 128 tokens x 256 weight rows, one workgroup of four waves per CU;
+//    a wave owns 64 weight rows -- one 32-row block of gate and the same rows
+//    of up (so the SwiGLU epilogue has both values of an output in one lane),
+//    or two 32-row blocks of one matrix -- for all 128 tokens.  Waves split
+//    N, never M, so each weight is dequantised by exactly one wave.
+//  * Every load of the K loop goes HBM -> LDS directly (buffer_load ... lds,
+//    issued from inline asm with explicit waits), three stages of 128 k deep:
+//    activations (XOR-swizzled rows so A-fragment reads are conflict-free),
+//    packed weights and the dwords holding the scales.
+//  * Each k-step's A fragments and unpacked weights are double-buffered: step
+//    s + 1's LDS reads and unpack are issued ahead of / under step s's MFMAs.
+//    A packed dword becomes eight fp16 weights in k order: a byte broadcast
 //    (v_perm_b32) and one v_and_or_b32 put two nibbles in the mantissas of
 //    1024 (0x6400), one v_pk_fma_f16 gives the exact (n - 8) pair, and
 //    v_pk_mul_f16 by the fp16 scale rounds the exact product once: the
 //    reference's dequantised weight bit for bit.
-//  * Activations: the 128 x 128 group slice goes HBM -> LDS directly
-//    (global_load_lds_dwordx4, no registers), double-buffered with one barrier
-//    per group.  Its 16-byte chunks are XOR-swizzled by row (chunk c of row r
-//    sits at r * 16 + (c ^ (r & 15))), so the 16-byte A-fragment reads of the
-//    16 rows of an MFMA block hit distinct banks.
-//  * Row blocks of 16 tokens past the tile's valid rows skip their MFMAs, so a
-//    ragged last tile of an expert costs what its rows need.
-//  * Persistent grid (2 workgroups per CU).  Tiles are numbered per problem in
-//    super-blocks of up to 8 M-tiles x n-tiles (n-tile slowest inside a
-//    super-block), and workgroups on one XCD take consecutive tile numbers, so
-//    the tiles running together on an XCD share activation and weight slices in
-//    its L2.
+//  * Rows of a tile past the valid tokens read the last valid row (results
+//    never stored).  Persistent grid: tiles are numbered per problem in
+//    super-blocks of up to 8 M-tiles x n-tiles, and workgroups on one XCD
+//    take consecutive numbers, so tiles running together on an XCD share
+//    activation and weight slices in its L2.
 #include "hn_common.h"
 
 namespace {
@@ -63,12 +59,6 @@ struct GemmArgs {
   int ld_q;         // packed row stride (bytes)
   int ld_s;         // scale row stride (elements)
   uint32_t m_pair, magic;
-};
-
-template <int MATS, int NB>
-struct BBuf {
-  u32x4 w[MATS][NB];
-  uint32_t s[MATS][NB];  // fp16 scale bits, zero-extended
 };
 
 struct Prob {
@@ -108,63 +98,130 @@ __device__ __forceinline__ Prob resolve(const GemmArgs& A, const GExpert* __rest
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Per-tile load state: buffer descriptors and the loop-invariant per-lane
-// byte offsets; the group offset goes in soffset.  Rows past N get an offset
-// past the descriptor's range (the load returns 0 and touches no memory): the
-// range check covers voffset (+ immediate) only, so the per-row part must be
-// in voffset.
-// (Descriptors are rebuilt from these at each use: a few scalar moves that
-// the compiler hoists; buffer-descriptor types cannot be struct members in
-// the host pass.)
-template <int MATS, int NB>
-struct TileLoads {
-  const void* px; int nx;             // activation rows of the tile, bytes
-  const void* pq[MATS];               // packed weights
-  const void* ps[MATS];               // scales
-  int nq, ns;                         // bytes of one packed / scale matrix
-  uint32_t va[8];                     // activation chunk offsets (8 DMA loads)
-  uint32_t vq[NB], vs[NB];            // weight / scale offsets per 16-row block
-};
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, 0x00020000);
 }
 
-// Activation slice of group g -> LDS: 128 rows x 128 k = 2048 16-byte chunks.
-// Wave w issues 8 direct loads of 64 consecutive LDS chunks each; LDS chunk
-// L = (row r, slot c') receives global chunk c' ^ (r & 15) of row r.  Rows
-// past the valid ones repeat the last valid row (their results are never
-// stored).
+// ---------------------------------------------------------------------------
+// Loads.  Everything the K loop reads from memory goes HBM -> LDS directly
+// (buffer_load ... lds: lane i's bytes land at m0 + size * i), issued from
+// inline asm so that the compiler neither counts these loads nor assumes
+// they alias its LDS reads: every wait on them is explicit (s_waitcnt vmcnt
+// below), and loads return in issue order.  Offsets: the per-lane part is in
+// voffset (the buffer range check covers voffset only, so rows past N carry
+// an offset past the descriptor's range and read as 0 without touching
+// memory); the per-group part is in soffset.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                         uint32_t lds) {
+  // soffset and m0 are uniform by construction; readfirstlane keeps them in SGPRs
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)),
+                  "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Work decomposition.  A tile is 128 tokens x 256 weight rows; a workgroup of
+// four waves computes it, each wave 64 rows: one 32-row block of gate and the
+// same 32 rows of up (MATS 2, so the SwiGLU epilogue finds both values of an
+// output in one lane) or two 32-row blocks of one matrix (MATS 1).  Two
+// workgroups per CU (two waves per SIMD: one wave's unpack runs under the
+// other's MFMAs, and one workgroup's tile start and epilogue under the
+// other's K loop).  K advances in stages of 64: three LDS stages, the loads
+// of stages t + 1 and t + 2 in flight while stage t computes.
+// ---------------------------------------------------------------------------
+#ifndef HN_GEMM_KSM
+#define HN_GEMM_KSM 2         // k per stage = 64 * KSM
+#endif
+#ifndef HN_GEMM_OCC
+#define HN_GEMM_OCC 1         // workgroups per CU (waves per SIMD)
+#endif
+constexpr int kKSM = HN_GEMM_KSM;
+constexpr int kOccW = HN_GEMM_OCC;
+constexpr int kBlk = 2;            // 32-row weight blocks per wave
+constexpr int kKS = 64 * kKSM;     // k per stage
+constexpr int kSteps = 4 * kKSM;   // MFMA k-steps (16 k) per stage
+constexpr int kChunks = 8 * kKSM;  // 16-byte activation chunks per row per stage
+constexpr int kNST = 3;            // LDS stages
+
+// LDS stage (bytes): activations [128 rows][kChunks chunks of 16 B], chunk c of
+// row r at slot c ^ key(r), so the 8 or 16 rows an A-fragment read serves per
+// LDS cycle hit distinct banks; packed weights [wave][block][d][lane] 16 B;
+// scale dwords [wave][block][lane] 4 B.
+struct Stage {
+  static constexpr int kA = 0;
+  static constexpr int kB = kBM * kChunks * 16;
+  static constexpr int kS = kB + kWaves * kBlk * kKSM * 1024;
+  static constexpr int kSize = kS + kWaves * kBlk * 256;
+};
+constexpr int kALoads = kChunks * kBM / (kWaves * 64);         // activation loads per lane
+constexpr int kLoadsPerStage = kALoads + kBlk * kKSM + kBlk;   // + weights + scales
+
+__device__ __forceinline__ int akey(int r) {
+  return kChunks == 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
+}
+
+// Per-tile load state.  (Buffer descriptors are rebuilt from the pointers at
+// each use -- a few scalar moves the compiler hoists; descriptor types cannot
+// be struct members in the host pass.)  Block b of the wave: matrix pq[b],
+// rows row0[b] .. + 32.
+struct TileLoads {
+  const void* px; int nx;             // activation rows of the tile, bytes
+  const void* pq[kBlk];               // packed weights of each block's matrix
+  const void* ps[kBlk];               // scales
+  int nq, ns;                         // bytes of one packed / scale matrix
+  uint32_t va[kALoads];               // activation chunk offsets
+  uint32_t vq[kBlk];                  // weight byte offset of (lane's row, lane's 16 B)
+  uint32_t vs[kBlk];                  // scale byte offset of (lane's row, lane's k)
+  int group;
+};
+
+// Activation loads: wave w issues kALoads loads of 64 consecutive LDS chunks
+// (1 KiB each); LDS chunk L = (row r, slot c') holds global chunk c' ^ key(r)
+// of row r.  Rows past the valid ones repeat the last valid row (their
+// results are never stored).
 __device__ __forceinline__ uint32_t a_offset(int j, int wave, int lane, int rows, long ld_x) {
-  const int L = (wave * 8 + j) * 64 + lane;
-  const int r = L >> 4;
-  const int c = (L & 15) ^ (r & 15);
+  const int L = (wave * kALoads + j) * 64 + lane;
+  const int r = L / kChunks;
+  const int c = (L % kChunks) ^ akey(r);
   return (uint32_t)((min(r, rows - 1) * (int)ld_x + 8 * c) * 2);
 }
 
-// (Not a template: the host pass rejects this builtin in a dependent call.)
-__device__ __forceinline__ void dma_a(const void* px, int nx, const uint32_t (&va)[8], int g,
-                                      h16* xs, int wave) {
-  const __amdgpu_buffer_rsrc_t r = rsrc(px, nx);
+// Issue stage t's loads into the LDS stage at byte address st.  Weights: per
+// block kKSM loads; load d brings lane l's 16 bytes at 16 kKSM (l / 32) + 16 d
+// of row (l % 32)'s 32 kKSM bytes of the stage.  Scales: the dword holding the
+// lane's scale.
+__device__ __forceinline__ void issue_stage(const TileLoads& tl, int t, uint32_t st, int wave) {
+  using L = Stage;
+  {
+    const __amdgpu_buffer_rsrc_t r = rsrc(tl.px, tl.nx);
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(xs + (wave * 8 + j) * 512), 16,
-                                             va[j], 256 * g, 0, 0);
-}
-
-template <int MATS, int NB>
-__device__ __forceinline__ void issue_b(BBuf<MATS, NB>& b, const TileLoads<MATS, NB>& tl, int g,
-                                        int group) {
-  const int soff_s = 2 * ((128 * g) / group);
+    for (int j = 0; j < kALoads; ++j)
+      dma_b128(r, tl.va[j], 2 * kKS * t, st + L::kA + (wave * kALoads + j) * 1024);
+  }
 #pragma unroll
-  for (int bk = 0; bk < NB; ++bk)
+  for (int b = 0; b < kBlk; ++b) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(tl.pq[b], tl.nq);
 #pragma unroll
-    for (int mt = 0; mt < MATS; ++mt) {
-      b.w[mt][bk] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rsrc(tl.pq[mt], tl.nq), tl.vq[bk], 64 * g, 0));
-      b.s[mt][bk] = (uint32_t)__builtin_bit_cast(unsigned short, __builtin_amdgcn_raw_buffer_load_b16(
-                                                rsrc(tl.ps[mt], tl.ns), tl.vs[bk], soff_s, 0));
-    }
+    for (int d = 0; d < kKSM; ++d)
+      dma_b128(r, tl.vq[b] + 16 * d, kKS / 2 * t,
+               st + L::kB + ((wave * kBlk + b) * kKSM + d) * 1024);
+  }
+  const uint32_t soff = 2 * ((kKS * t) / tl.group);
+#pragma unroll
+  for (int b = 0; b < kBlk; ++b)
+    dma_b32(rsrc(tl.ps[b], tl.ns), (tl.vs[b] + soff) & ~3u, st + L::kS + (wave * kBlk + b) * 256);
 }
 
 // Unpack constants (gfx9 VOP3 takes no literals): mask in an SGPR, the rest
@@ -182,103 +239,162 @@ __device__ __forceinline__ half8_t deq8(uint32_t w, const DeqRegs& c, half2_t s2
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t t = __builtin_amdgcn_perm(w, w, 0x01010101u * j);  // byte j, 4 times
-    const half2_t v = hn_bits_h2(hn_and_or(t, c.m_pair, c.magic));    // (1024+n, 1024+16n')
+    const half2_t v = hn_bits_h2((t & c.m_pair) | c.magic);           // (1024+n, 1024+16n')
     const half2_t d = __builtin_elementwise_fma(v, hn_bits_h2(c.mul), hn_bits_h2(c.add));
     r[j] = __builtin_bit_cast(uint32_t, d * s2);
   }
   return __builtin_bit_cast(half8_t, r);
 }
 
-// One group (4 MFMA k-steps of 32) for this wave.  FULL: all 8 row blocks
-// valid (no per-block branches, so unpack and MFMA interleave freely).
-template <int MATS, int NB, bool FULL>
-__device__ __forceinline__ void compute(const BBuf<MATS, NB>& b, const h16* xs, int nrb, int col,
-                                        int q, const DeqRegs& dr, float4_t (&acc)[8][MATS][NB]) {
-  half2_t s2[MATS][NB];
+template <typename T>
+__device__ __forceinline__ T lds_read(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(
+      (__attribute__((address_space(3))) char*)nullptr + addr);
+}
+
+// MFMA v_mfma_f32_32x32x16_f16: lane l supplies A[row l % 32][k 8 (l / 32) + 0..7],
+// B[k 8 (l / 32) + 0..7][col l % 32] and holds D[8 (r / 4) + 4 (l / 32) + r % 4]
+// [l % 32], r = 0..15.  In a stage, step s (0..3) gives lane half h the 8 k of
+// chunk kSteps h + s: the 16 kKSM packed bytes a lane loaded are its steps.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Operand registers of one wave.  A fragments and unpacked weights are
+// double-buffered over steps: step s + 1's LDS reads and unpack are issued
+// ahead of step s's MFMAs into the other buffer.
+struct Ops {
+  uint32_t pk[kBlk][kSteps];  // packed weights of the current stage, one dword per step
+  half2_t s2[kBlk];       // scales, both halves
+  half8_t af[2][4];       // A fragments of the 4 row blocks
+  half8_t bw[2][kBlk];    // unpacked weights
+};
+
+__device__ __forceinline__ uint32_t a_addr(uint32_t st, int s, int row32, int h) {
+  return st + row32 * (kChunks * 16) + (((h * kSteps + s) ^ akey(row32)) << 4);
+}
+
+__device__ __forceinline__ void read_a(Ops& o, int buf, uint32_t st, int s, int row32, int h) {
+  const uint32_t base = a_addr(st, s, row32, h);
 #pragma unroll
-  for (int mt = 0; mt < MATS; ++mt)
+  for (int rb = 0; rb < 4; ++rb) o.af[buf][rb] = lds_read<half8_t>(base + rb * 32 * kChunks * 16);
+}
+
+// Weights + scales of the stage at st (stage number t); half-word of each
+// scale dword from the byte offset the dword was loaded for.
+__device__ __forceinline__ void read_b(Ops& o, const TileLoads& tl, uint32_t st, int t, int wave,
+                                       int lane) {
+  using L = Stage;
+  const uint32_t soff = 2 * ((kKS * t) / tl.group);
 #pragma unroll
-    for (int bk = 0; bk < NB; ++bk) s2[mt][bk] = hn_bits_h2(b.s[mt][bk] | (b.s[mt][bk] << 16));
+  for (int b = 0; b < kBlk; ++b) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    half8_t bw[MATS][NB];
+    for (int d = 0; d < kKSM; ++d) {
+      const u32x4 v =
+          lds_read<u32x4>(st + L::kB + ((wave * kBlk + b) * kKSM + d) * 1024 + lane * 16);
 #pragma unroll
-    for (int mt = 0; mt < MATS; ++mt)
-#pragma unroll
-      for (int bk = 0; bk < NB; ++bk) bw[mt][bk] = deq8(b.w[mt][bk][t], dr, s2[mt][bk]);
-    const int slot = ((4 * q + t) ^ col) * 8;
-#pragma unroll
-    for (int rb = 0; rb < 8; ++rb) {
-      if (FULL || rb < nrb) {  // uniform
-        const half8_t a = *reinterpret_cast<const half8_t*>(xs + (rb * 16 + col) * 128 + slot);
-#pragma unroll
-        for (int mt = 0; mt < MATS; ++mt)
-#pragma unroll
-          for (int bk = 0; bk < NB; ++bk)
-            acc[rb][mt][bk] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw[mt][bk], acc[rb][mt][bk], 0, 0, 0);
-      }
+      for (int i = 0; i < 4; ++i) o.pk[b][4 * d + i] = v[i];
     }
+    const uint32_t hsel = (tl.vs[b] + soff) & 2u;
+    const uint32_t sv =
+        lds_read<unsigned short>(st + L::kS + (wave * kBlk + b) * 256 + lane * 4 + hsel);
+    o.s2[b] = hn_bits_h2(sv | (sv << 16));
   }
 }
 
-// s_waitcnt with only vmcnt = n (expcnt and lgkmcnt at their maxima; gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+__device__ __forceinline__ void deq_step(Ops& o, int buf, int s, const DeqRegs& dr) {
+#pragma unroll
+  for (int b = 0; b < kBlk; ++b) o.bw[buf][b] = deq8(o.pk[b][s], dr, o.s2[b]);
 }
 
-template <int MATS, int NB, bool FULL>
-__device__ __forceinline__ void main_loop(const TileLoads<MATS, NB>& tl, int group, int G,
-                                          h16* xs0, h16* xs1, BBuf<MATS, NB>& b0,
-                                          BBuf<MATS, NB>& b1, int nrb, int col, int q, int wave,
-                                          const DeqRegs& dr, float4_t (&acc)[8][MATS][NB]) {
-  constexpr int kBLoads = 2 * MATS * NB;  // weight + scale loads per group
-  for (int g = 0; g < G; g += 2) {
-    {
-      const bool more = g + 1 < G;  // uniform
-      if (more) {
-        dma_a(tl.px, tl.nx, tl.va, g + 1, xs1, wave);
-        __builtin_amdgcn_sched_barrier(0);
-        issue_b(b1, tl, g + 1, group);
-      }
-      compute<MATS, NB, FULL>(b0, xs0, nrb, col, q, dr, acc);
-      if (more) wait_vmcnt<kBLoads>();
-      __syncthreads();
+__device__ __forceinline__ void mfma_step(const Ops& o, int buf, f32x16 (&acc)[4][kBlk]) {
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int b = 0; b < kBlk; ++b)
+      acc[rb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.af[buf][rb], o.bw[buf][b], acc[rb][b],
+                                                          0, 0, 0);
+}
+
+// Interleave hint for one step: LDS reads first, then 4 kBlk x (1 MFMA,
+// 4 VALU) -- the next step's unpack under this step's MFMAs.
+template <int NDS>
+__device__ __forceinline__ void sched_step() {
+  if (NDS) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // DS read
+#pragma unroll
+  for (int i = 0; i < 4 * kBlk; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+  }
+}
+
+// K loop of one tile over stages [tb, T) of kKS k each.  In a stage, step s's MFMAs
+// overlap the unpack and A-fragment reads of step s + 1; during the last
+// step the wave waits for its own loads of stage t + 1 (those of t + 2 stay in
+// flight), reads that stage's weights and unpacks its first step; the barrier
+// then makes every wave's activation loads of t + 1 visible.
+__device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int T, uint32_t lds0,
+                                       int row32, int h, int wave, int lane, const DeqRegs& dr,
+                                       f32x16 (&acc)[4][kBlk]) {
+  using L = Stage;
+  Ops o;
+  issue_stage(tl, tb, lds0, wave);
+  if (tb + 1 < T) {
+    issue_stage(tl, tb + 1, lds0 + L::kSize, wave);
+    wait_vmcnt<kLoadsPerStage>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
+  read_b(o, tl, lds0, tb, wave, lane);
+  deq_step(o, 0, 0, dr);
+  read_a(o, 0, lds0, 0, row32, h);
+  int sc = 0;  // LDS stage of stage t
+  for (int t = tb; t < T; ++t) {
+    const int s1 = sc + 1 == kNST ? 0 : sc + 1;
+    const int s2 = s1 + 1 == kNST ? 0 : s1 + 1;
+    const uint32_t cur = lds0 + sc * L::kSize;
+    const uint32_t nxt = lds0 + s1 * L::kSize;
+    const bool ahead = t + 2 < T;  // uniform
+    if (ahead) issue_stage(tl, t + 2, lds0 + s2 * L::kSize, wave);
+#pragma unroll
+    for (int s = 0; s < kSteps - 1; ++s) {
+      // step s + 1's A fragments are requested before step s's MFMAs (the
+      // scheduling fences keep them there); its unpack runs under them
+      read_a(o, (s + 1) & 1, cur, s + 1, row32, h);
+      __builtin_amdgcn_sched_barrier(0);
+      deq_step(o, (s + 1) & 1, s + 1, dr);
+      mfma_step(o, s & 1, acc);
+      sched_step<0>();
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (g + 1 < G) {
-      const bool more = g + 2 < G;
-      if (more) {
-        dma_a(tl.px, tl.nx, tl.va, g + 2, xs0, wave);
-        __builtin_amdgcn_sched_barrier(0);
-        issue_b(b0, tl, g + 2, group);
-      }
-      compute<MATS, NB, FULL>(b1, xs1, nrb, col, q, dr, acc);
-      if (more) wait_vmcnt<kBLoads>();
-      __syncthreads();
-    }
+    if (ahead) wait_vmcnt<kLoadsPerStage>();
+    else wait_vmcnt<0>();
+    read_b(o, tl, nxt, t + 1, wave, lane);
+    deq_step(o, 0, 0, dr);
+    mfma_step(o, 1, acc);
+    sched_step<kBlk * kKSM + kBlk>();
+    __syncthreads();
+    if (t + 1 < T) read_a(o, 0, nxt, 0, row32, h);
+    sc = s1;
   }
 }
 
 template <bool GROUPED, int MATS>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs A,
-                                                      const GExpert* __restrict__ table,
-                                                      const int* __restrict__ active,
-                                                      const int* __restrict__ n_active,
-                                                      const int* __restrict__ offsets) {
-  constexpr int NB = 4 / MATS;
-  constexpr int WROWS = kWaves * NB * 16;  // weight rows per matrix per tile
-  __shared__ __align__(16) h16 xs[2][kBM * 128];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOccW))) void gemm_kernel(
+    GemmArgs A, const GExpert* __restrict__ table, const int* __restrict__ active,
+    const int* __restrict__ n_active, const int* __restrict__ offsets) {
+  constexpr int WN = kWaves * 32 * kBlk / MATS;  // output columns per tile
+  using L = Stage;
+  __shared__ __align__(16) unsigned char lds[kNST * L::kSize];
   __shared__ int toff[kMaxProb + 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 15;
-  const int q = lane >> 4;
+  const int row32 = lane & 31;
+  const int h = lane >> 5;
   const int N = A.N;
-  const int G = A.K >> 7;
-  const int NT = (N + WROWS - 1) / WROWS;
+  const int T = A.K / kKS;
+  const int NT = (N + WN - 1) / WN;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
   DeqRegs dr;
   dr.m_pair = A.m_pair;
   dr.magic = hn_vgpr(A.magic);
@@ -321,9 +437,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs A,
         const int mid = (lo + hi + 1) >> 1;
         if (toff[mid] <= mg) lo = mid; else hi = mid - 1;
       }
-      p = lo;
+      p = __builtin_amdgcn_readfirstlane(lo);  // uniform: keep the tile state in SGPRs
     }
-    const int pt0 = toff[p], mtp = toff[p + 1] - pt0;
+    const int pt0 = __builtin_amdgcn_readfirstlane(toff[p]);
+    const int mtp = __builtin_amdgcn_readfirstlane(toff[p + 1]) - pt0;
     const int local = tile - pt0 * NT;
     const int sb = local / (kSuperM * NT);           // super-block
     const int sm0 = sb * kSuperM;
@@ -334,71 +451,59 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs A,
     const Prob pr = resolve<GROUPED>(A, table, active, offsets, p);
     const int m0 = mtile * kBM;
     const int rows = min(kBM, pr.rows - m0);
-    const int nrb = (rows + 15) >> 4;
-    const int rbase = ntile * WROWS + wave * NB * 16 + col;
+    // output column of this lane in block 0
+    const int n0 = ntile * WN + wave * 32 * kBlk / MATS + row32;
 
-    TileLoads<MATS, NB> tl;
+    TileLoads tl;
     tl.px = pr.x + (long)m0 * A.ld_x;
     tl.nx = (int)(rows * A.ld_x * 2);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) tl.va[j] = a_offset(j, wave, lane, rows, A.ld_x);
-#pragma unroll
-    for (int mt = 0; mt < MATS; ++mt) {
-      tl.pq[mt] = pr.q[mt];
-      tl.ps[mt] = pr.s[mt];
-    }
+    for (int j = 0; j < kALoads; ++j) tl.va[j] = a_offset(j, wave, lane, rows, A.ld_x);
     tl.nq = N * A.ld_q;
     tl.ns = N * A.ld_s * 2;
+    tl.group = A.group;
 #pragma unroll
-    for (int bk = 0; bk < NB; ++bk) {
-      const int row = rbase + 16 * bk;
+    for (int b = 0; b < kBlk; ++b) {
+      const int mt = MATS == 2 ? b : 0;
+      const int row = MATS == 2 ? n0 : n0 + 32 * b;
+      tl.pq[b] = pr.q[mt];
+      tl.ps[b] = pr.s[mt];
       const bool ok = row < N;
-      tl.vq[bk] = ok ? (uint32_t)(row * A.ld_q + 16 * q) : kOOB;
-      tl.vs[bk] = ok ? (uint32_t)(2 * (row * A.ld_s + (32 * q) / A.group)) : kOOB;
+      tl.vq[b] = ok ? (uint32_t)(row * A.ld_q + 16 * kKSM * h) : kOOB;
+      tl.vs[b] = ok ? (uint32_t)(2 * (row * A.ld_s + (A.group == 32 * kKSM ? h : 0))) : kOOB;
     }
-    float4_t acc[8][MATS][NB];
+    f32x16 acc[4][kBlk];
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb)
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int mt = 0; mt < MATS; ++mt)
+      for (int b = 0; b < kBlk; ++b)
 #pragma unroll
-        for (int bk = 0; bk < NB; ++bk) acc[rb][mt][bk] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < 16; ++r) acc[rb][b][r] = 0.f;
 
-    BBuf<MATS, NB> b0, b1;
-    constexpr int kBLoads = 2 * MATS * NB;
-    // the previous tile's last reads of xs[0] end before anyone restages it
+    // the previous tile's last reads of the stages end before anyone restages
     __syncthreads();
-    dma_a(tl.px, tl.nx, tl.va, 0, xs[0], wave);
-    __builtin_amdgcn_sched_barrier(0);
-    issue_b(b0, tl, 0, A.group);
-    wait_vmcnt<kBLoads>();
-    __syncthreads();
+    k_loop(tl, 0, T, lds0, row32, h, wave, lane, dr, acc);
 
-    // group g: restage g + 1 (activations first, then weights, so that the
-    // wait for the activations leaves the weight loads in flight), compute g
-    if (nrb == 8) main_loop<MATS, NB, true>(tl, A.group, G, xs[0], xs[1], b0, b1, nrb, col, q,
-                                            wave, dr, acc);
-    else main_loop<MATS, NB, false>(tl, A.group, G, xs[0], xs[1], b0, b1, nrb, col, q, wave,
-                                    dr, acc);
-
-    // ---- epilogue: lane (col, q) holds tokens rb*16 + 4q + i of row n
+    // ---- epilogue: lane holds column n, tokens 32 rb + 8 (r / 4) + 4 h + r % 4
 #pragma unroll
-    for (int bk = 0; bk < NB; ++bk) {
-      const int n = rbase + 16 * bk;
+    for (int ob = 0; ob < kBlk / MATS; ++ob) {
+      const int n = n0 + 32 * ob;
       if (n < N) {
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb) {
+        for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int m = rb * 16 + 4 * q + i;
+          for (int r = 0; r < 16; ++r) {
+            const int m = 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3);
             if (m < rows) {
               h16 o;
               if (MATS == 2) {
-                const float gv = (float)(h16)acc[rb][0][bk][i];
-                const float uv = (float)(h16)acc[rb][MATS - 1][bk][i];
-                o = (h16)(hn_silu(gv) * uv);
+                // silu(g) * u in fp32 from the fp16-rounded projections; the
+                // fast exp / reciprocal are well inside the fp16 rounding
+                const float gv = (float)(h16)acc[rb][0][r];
+                const float uv = (float)(h16)acc[rb][1][r];
+                o = (h16)(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
               } else {
-                o = (h16)acc[rb][0][bk][i];
+                o = (h16)acc[rb][ob][r];
               }
               pr.out[(long)(m0 + m) * A.ld_o + n] = o;
             }
@@ -430,21 +535,26 @@ void fill_consts(GemmArgs& A) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Workgroups: two per CU, fewer when there are fewer tiles.
+constexpr int kOcc = kOccW;  // workgroups per CU
+
+// Workgroups: OCC per CU, fewer when there are fewer tiles.
 int grid_for(long tiles_upper) {
-  const long cap = 2L * num_cus();
+  const long cap = (long)kOcc * num_cus();
   return (int)(tiles_upper < cap ? (tiles_upper < 1 ? 1 : tiles_upper) : cap);
 }
+
+
 
 }  // namespace
 
 // Shape checks shared by the entry points below: 1 when the GEMM kernels
 // handle the shape.
 static int gemm_shape_ok(long N, long K, long group, long ld_q, long ld_s) {
-  // the scale offset split (voffset: lane part, soffset: group part) needs
-  // group in {32, 64} or a multiple of 128
-  if (K <= 0 || K % 128 != 0 || K % group != 0) return 0;
-  if (group != 32 && group != 64 && (group <= 0 || group % 128 != 0)) return 0;
+  // a lane's 32 kKSM k of a stage share one scale, and the scale offset split
+  // (voffset: lane part, soffset: stage part) needs group 32 kKSM or a
+  // multiple of the stage
+  if (K <= 0 || K % kKS != 0 || group <= 0 || K % group != 0) return 0;
+  if (group != 32 * kKSM && group % kKS != 0) return 0;
   if (ld_q % 16 != 0) return 0;
   if (N * ld_q >= (long)kOOB || N * ld_s * 2 >= (long)kOOB) return 0;
   return 1;
@@ -475,15 +585,16 @@ extern "C" int hn_gemm_linear_impl(int mats, const void* x, long ld_x, const voi
   A.ld_q = (int)ld_q;
   A.ld_s = (int)ld_s;
   fill_consts(A);
-  const long wrows = mats == 2 ? 128 : 256;
-  const long tiles = ((M + kBM - 1) / kBM) * ((N + wrows - 1) / wrows);
+  const long wn = kWaves * 32 * kBlk / mats;
+  const long tiles = ((M + kBM - 1) / kBM) * ((N + wn - 1) / wn);
   hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(grid_for(tiles));
   if (mats == 2)
-    hipLaunchKernelGGL((gemm_kernel<false, 2>), dim3(grid_for(tiles)), dim3(256), 0, s, A,
-                       nullptr, nullptr, nullptr, nullptr);
+    hipLaunchKernelGGL((gemm_kernel<false, 2>), grid, dim3(256), 0, s, A, nullptr, nullptr,
+                       nullptr, nullptr);
   else
-    hipLaunchKernelGGL((gemm_kernel<false, 1>), dim3(grid_for(tiles)), dim3(256), 0, s, A,
-                       nullptr, nullptr, nullptr, nullptr);
+    hipLaunchKernelGGL((gemm_kernel<false, 1>), grid, dim3(256), 0, s, A, nullptr, nullptr,
+                       nullptr, nullptr);
   HN_LAUNCH_CHECK("hn_gemm_linear");
   return 0;
 }
@@ -511,16 +622,18 @@ extern "C" int hn_gemm_grouped_impl(int phase, const void* x, long ld_x, const v
   A.ld_q = (int)(K / 2);
   A.ld_s = (int)(K / group);
   fill_consts(A);
-  const long wrows = phase == 0 ? 128 : 256;
+  const long wn = kWaves * 32 * kBlk / (phase == 0 ? 2 : 1);
   const long mt_upper = (rows + kBM - 1) / kBM + (E < rows ? E : rows);
-  const long tiles = mt_upper * ((N + wrows - 1) / wrows);
+  const long tiles = mt_upper * ((N + wn - 1) / wn);
   hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(grid_for(tiles));
+  const GExpert* tb = (const GExpert*)table;
   if (phase == 0)
-    hipLaunchKernelGGL((gemm_kernel<true, 2>), dim3(grid_for(tiles)), dim3(256), 0, s, A,
-                       (const GExpert*)table, active, n_active, offsets);
+    hipLaunchKernelGGL((gemm_kernel<true, 2>), grid, dim3(256), 0, s, A, tb, active, n_active,
+                       offsets);
   else
-    hipLaunchKernelGGL((gemm_kernel<true, 1>), dim3(grid_for(tiles)), dim3(256), 0, s, A,
-                       (const GExpert*)table, active, n_active, offsets);
+    hipLaunchKernelGGL((gemm_kernel<true, 1>), grid, dim3(256), 0, s, A, tb, active, n_active,
+                       offsets);
   HN_LAUNCH_CHECK("hn_gemm_grouped");
   return 0;
 }

@@ -525,8 +525,14 @@ void launch_grouped(SkinnyArgs& A, const Plan& p, int E_max, hipStream_t s) {
 
 constexpr int kMaxRows = 64;  // tokens per weight matrix handled per launch
 
-// workspace layout: [counters: one region shared by every launch of a call][partials]
-size_t ctr_bytes(long counters) { return ((size_t)counters * 4 + 255) & ~(size_t)255; }
+// Workspace layout, the same for every call: [counters: a fixed 2 MiB region
+// at the start][partials].  One buffer serves calls of every kind and size
+// in turn; with the counter region fixed, no call's partials ever land on
+// another call's counters (which must read zero on entry; every launch
+// leaves its counters at zero).
+constexpr size_t kCtrRegion = 2u << 20;
+constexpr long kMaxCounters = (long)(kCtrRegion / 4);
+size_t ctr_bytes(long /*counters*/) { return kCtrRegion; }
 
 size_t part_bytes(int ks, int mats, long rows, long N) {
   return ks > 1 ? (size_t)ks * mats * rows * N * 4 : 0;
@@ -623,6 +629,8 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
   for (long m0 = 0; m0 < M; m0 += kMaxRows) {
     const int rows = (int)((M - m0) > kMaxRows ? kMaxRows : (M - m0));
     const Plan p = make_plan(rows, (int)K, mats);
+    HN_ARG_CHECK((n_counters < tiles ? tiles : n_counters) <= kMaxCounters,
+                 "%s: N=%ld needs more split-K counters than the workspace holds", who, N);
     const size_t cb = ctr_bytes(n_counters < tiles ? tiles : n_counters);
     const size_t need = cb + part_bytes(p.ks, mats, rows, N);
     HN_ARG_CHECK(p.ks == 1 || (ws && (size_t)ws_size >= need),
@@ -774,6 +782,8 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
   A.M = rmax;
   const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
                                                             : hn_cdiv(H, kTileN);
+  HN_ARG_CHECK(E * tmax <= kMaxCounters, "%s: E=%ld x %ld tiles exceed the counter region", who,
+               E, tmax);
   float* partial = (float*)((char*)work + ctr_bytes(E * tmax));
   {
     const Plan p = make_plan(rmax, (int)H, 2);

@@ -43,7 +43,9 @@ int hn_int4_quantize(const void* w, long ld_w, int dtype, int mode, void* packed
  * (M, N, K); 1: hn_int4_gate_up_silu (M, N=I, K=H); 2: hn_expert_mlp_int4
  * (M=T, N=H, K=I); 3: hn_grouped_expert_mlp_int4 (M=rows, N=H, K=I, E).  The
  * workspace must be zero-filled once when allocated; the kernels leave its
- * counters at zero.  Calls that run concurrently need distinct workspaces.
+ * counters at zero.  Its layout (counters in the first 2 MiB, partials after)
+ * is the same for every call, so one buffer may serve calls of every kind and
+ * size in turn.  Calls that run concurrently need distinct workspaces.
  * No counterpart in the reference (Triton needs no split-K workspace). */
 long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long E);
 
@@ -110,7 +112,7 @@ int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* i
 
 /* Grouped SwiGLU over every active expert of one MoE layer in two launches:
  * the decode kernels up to 64 rows per expert, the MFMA GEMM kernels above
- * (then the workspace may be NULL / 0 bytes).  x_perm [rows, H] sorted by expert; table: E x
+ * (which take no workspace: it may then be NULL / 0 bytes).  x_perm [rows, H] sorted by expert; table: E x
  * {gate_q, gate_s, up_q, up_s, down_q, down_s} device pointers (u64); active /
  * n_active / offsets from hn_moe_permute; h_ws [rows, I] fp16 buffer;
  * y_perm [rows, H] fp16 out; work: hn_skinny_workspace_bytes(3, rows, H, I, E).
@@ -125,7 +127,7 @@ int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int*
 /* One phase of hn_grouped_expert_mlp_int4's prefill path (the grouped MFMA GEMM):
  * phase 0 writes h_ws [rows, I] = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T)) per expert,
  * phase 1 writes y_perm [rows, H] = fp16(h_ws Wd^T) per expert.  Any rows per
- * expert; E <= 256; H, I multiples of 128; group 32, 64 or a multiple of 128.
+ * expert; E <= 256; H, I multiples of 128; group 64 or a multiple of 128.
  * No separate counterpart in the reference (its loop calls
  * expert_mlp_int4_fused per expert, model/mixtral.py:342-354); lets a caller
  * time or schedule the two phases apart. */

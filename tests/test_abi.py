@@ -40,12 +40,15 @@ def test_ctypes_table_matches_header():
 def test_workspace_query():
     from hydranet_amd import _lib
     h = _lib.lib()
+    ctr = 2 << 20  # fixed counter region at the start of every workspace
     # one token: every tile reduces K inside a workgroup -> counters only
-    assert h.hn_skinny_workspace_bytes(2, 1, 4096, 14336, 0) <= 4096
-    assert h.hn_skinny_workspace_bytes(0, 1, 64, 256, 0) == 256
+    assert h.hn_skinny_workspace_bytes(2, 1, 4096, 14336, 0) == ctr
+    assert h.hn_skinny_workspace_bytes(0, 1, 64, 256, 0) == ctr
     # 64 tokens x K=14336 do not fit one workgroup's LDS -> fp32 partials
     b = h.hn_skinny_workspace_bytes(0, 64, 4096, 14336, 0)
-    assert b >= 2 * 64 * 4096 * 4
+    assert b >= ctr + 2 * 64 * 4096 * 4
+    # the grouped query at decode sizes covers E x tiles counters + partials
+    assert h.hn_skinny_workspace_bytes(3, 32, 4096, 14336, 8) >= ctr
 
 
 def test_argument_errors_raise_without_gpu():
