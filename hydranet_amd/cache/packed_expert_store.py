@@ -33,9 +33,6 @@ import torch
 
 from .blob_layout import BlobLayout
 
-warnings.filterwarnings("ignore", message=r"The given buffer is not writable.*",
-                        category=UserWarning, module=r"torch\..*")
-
 __all__ = ["BlobLayout", "ExpertIndex", "GpuExpertSlot", "PinnedStagingRing", "PackedExpertStore"]
 
 
@@ -66,7 +63,7 @@ class GpuExpertSlot:
     """One expert's INT4 weights resident on the GPU (one slab, six views)."""
 
     def __init__(self, slot_idx: int, hidden_dim: int, intermediate_dim: int, group_size: int,
-                 device: torch.device):
+                 device: torch.device, slab: Optional[torch.Tensor] = None):
         self.slot_idx = slot_idx
         self.hidden_dim = hidden_dim
         self.intermediate_dim = intermediate_dim
@@ -75,7 +72,14 @@ class GpuExpertSlot:
         self.layer_idx: Optional[int] = None
         self.expert_idx: Optional[int] = None
         self.layout = BlobLayout.from_dims(hidden_dim, intermediate_dim, group_size)
-        self.slab = torch.empty(self.layout.total_size, dtype=torch.uint8, device=self.device)
+        if slab is None:
+            slab = torch.empty(self.layout.total_size, dtype=torch.uint8, device=self.device)
+        elif (slab.dtype != torch.uint8 or slab.numel() != self.layout.total_size
+              or not slab.is_contiguous() or slab.device != self.device):
+            raise ValueError("slab must be a contiguous uint8 tensor of the blob size on "
+                             f"{self.device} ({self.layout.total_size} bytes)")
+        # a caller-provided slab is a window of a larger arena (one allocation per layer)
+        self.slab = slab
         for name, view in _slab_views(self.slab, self.layout, hidden_dim, intermediate_dim,
                                       group_size).items():
             setattr(self, name, view)
@@ -263,7 +267,9 @@ class PackedExpertStore:
     def load_to_staging(self, layer_idx: int, expert_idx: int):
         blob, layout = self.get_expert_blob(layer_idx, expert_idx)
         slot_idx, staging = self.staging.acquire()
-        t = torch.frombuffer(blob, dtype=torch.uint8)
+        with warnings.catch_warnings():  # a read-only mmap window, only copied from
+            warnings.simplefilter("ignore", UserWarning)
+            t = torch.frombuffer(blob, dtype=torch.uint8)
         staging[: t.numel()].copy_(t)
         return slot_idx, staging, layout
 
@@ -273,6 +279,10 @@ class PackedExpertStore:
         staging_idx, staging, layout = self.load_to_staging(layer_idx, expert_idx)
         if stream is None:
             stream = self.memcpy_stream
+        if stream is not None and gpu_slot.device.type == "cuda":
+            # the slab may still be read by kernels already queued on the compute
+            # stream (an evicted expert): the overwrite waits for them
+            stream.wait_stream(torch.cuda.current_stream(gpu_slot.device))
         gpu_slot.load_from_pinned(staging, layout, layer_idx, expert_idx, stream=stream)
         if stream is not None and gpu_slot.ready_event is not None:
             gpu_slot.ready_event.record(stream)

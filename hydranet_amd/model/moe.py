@@ -13,10 +13,12 @@ MixtralMoELayer.forward (model/mixtral.py:290-370) and GLM4MoELayer.forward
                                             hn_moe_unpermute: fp16 index_add_ order
 
 Expert weights come from a device table of slab pointers, one row per expert
-(``ExpertTable``), built once when every expert is resident.  If a cache
-manager holds only some experts, the active experts are fetched to the host
-(one D2H), made resident through the manager (its get_int4_slot records
-hits/misses and loads misses), and the table is refreshed for that call.
+(``ExpertTable``), built once when every expert is resident (fixed slots, or
+a cache manager layer made resident in one HBM arena).  If a cache manager
+holds only some experts, the active experts are fetched to the host (one
+D2H), made resident through the manager (its get_int4_slot records
+hits/misses and loads misses, none of them evicting another), and the table
+is refreshed for that call.
 """
 from __future__ import annotations
 
@@ -119,6 +121,7 @@ class _ResidentExperts:
         self.layer_idx = layer_idx
         self.cache_manager = cache_manager
         self.table: Optional[ExpertTable] = None
+        self._resident_table: Optional[ExpertTable] = None
         if slots is not None:
             self.table = ExpertTable.from_slots(slots)
 
@@ -126,15 +129,25 @@ class _ResidentExperts:
         cm = self.cache_manager
         if cm is None:
             return self.table
+        if cm.is_resident(self.layer_idx):
+            # every expert sits in the layer's HBM arena: static table, no host sync
+            if self._resident_table is None:
+                self._resident_table = ExpertTable.from_slots(cm.resident_slots(self.layer_idx),
+                                                              idx.device)
+            return self._resident_table
         if self.table is None:
             self.table = ExpertTable(self.num_experts, idx.device)
         needed = torch.unique(idx).tolist()  # one D2H when experts may be missing
         hits = [e for e in needed if cm.is_cached(self.layer_idx, e)]
         misses = [e for e in needed if e not in hits]
-        for e in misses:  # start the loads of misses before touching hits
-            cm.prefetch_int4_slot(self.layer_idx, e)
-        for e in hits + misses:
-            self.table.set(e, cm.get_int4_slot(self.layer_idx, e))
+        # the experts of this call are used by one grouped launch: none may evict another
+        with cm.hold(self.layer_idx, needed):
+            for e in misses:  # start the loads of misses before touching hits
+                cm.prefetch_int4_slot(self.layer_idx, e)
+            for e in hits:
+                self.table.set(e, cm.get_int4_slot(self.layer_idx, e))
+            for e in misses:
+                self.table.set(e, cm.get_int4_slot(self.layer_idx, e, prefetched_miss=True))
         self.table.upload()
         return self.table
 

@@ -1,0 +1,160 @@
+"""GPU tests of the residency path: experts.bin on disk -> pinned staging ->
+HBM slots (PerLayerCache / ExpertCacheManager) -> the grouped MoE kernels.
+
+Bar: the MoE layer run through a cache manager (partial cache with
+evictions, or every expert resident in one arena) gives bit-identical output
+to the same layer over fixed slots loaded directly from the same blobs, and
+slot bytes equal the blob bytes after the async loads complete.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hydranet_amd.cache.expert_cache import ExpertCacheConfig, ExpertCacheManager, MoEModelConfig
+from hydranet_amd.cache.packed_expert_store import GpuExpertSlot, PackedExpertStore
+from hydranet_amd.preprocess import pack_store as ps
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+H, I, G, E, L = 512, 1024, 128, 8, 2
+
+
+@pytest.fixture(scope="module")
+def store(tmp_path_factory):
+    path = tmp_path_factory.mktemp("packed")
+    rng = np.random.default_rng(11)
+    experts = {}
+    for l in range(L):
+        for e in range(E):
+            t = {}
+            for pre, (n, k) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+                w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+                p, s = oracle.quantize(w, G, mode=0)
+                t[f"{pre}_packed"] = torch.from_numpy(p)
+                t[f"{pre}_scales"] = torch.from_numpy(s.copy())
+            experts[(l, e)] = t
+    ps.write_packed_store(path, ((l, e, t) for (l, e), t in experts.items()), L, E, H, I, G,
+                          model_type="test")
+    st = PackedExpertStore(path / "experts.idx", device=DEV)
+    yield st, experts
+    st.close()
+
+
+def _fixed_slots(experts, layer):
+    out = []
+    for e in range(E):
+        s = GpuExpertSlot(e, H, I, G, DEV)
+        s.load_from_tensors({n: v.to(DEV) for n, v in experts[(layer, e)].items()}, layer, e)
+        out.append(s)
+    return out
+
+
+def _layers(cm, experts, layer):
+    from hydranet_amd.model.moe import MixtralMoELayer
+    ref = MixtralMoELayer(H, E, 2, layer_idx=layer, slots=_fixed_slots(experts, layer)).to(DEV)
+    got = MixtralMoELayer(H, E, 2, layer_idx=layer, cache_manager=cm).to(DEV)
+    g = torch.Generator().manual_seed(5 + layer)
+    w = (torch.randn(E, H, generator=g) * 0.05).half()
+    for m in (ref, got):
+        m.eval()
+        m.router.gate.weight.data.copy_(w.to(DEV))
+    return ref, got
+
+
+def _manager(store, base):
+    cfg = MoEModelConfig(num_layers=L, num_experts=E, hidden_dim=H, intermediate_dim=I)
+    cm = ExpertCacheManager(cfg, ExpertCacheConfig(0, base // 2, base - base // 2,
+                                                   enable_dynamic_slots=False), device=DEV)
+    cm.set_packed_store(store)
+    return cm
+
+
+def test_slot_bytes_after_async_load(store):
+    st, experts = store
+    cm = _manager(st, 3)
+    try:
+        for e in range(E):
+            s = cm.get_int4_slot(1, e)  # 4 slots: later loads evict and reuse slabs
+            torch.cuda.current_stream().synchronize()
+            for n, v in experts[(1, e)].items():
+                assert torch.equal(getattr(s, n).cpu(), v), (e, n)
+        assert cm.get_stats()["total_evictions"] == E - 4
+    finally:
+        cm.shutdown()
+
+
+def test_decode_through_partial_cache_matches_fixed_slots(store):
+    """Decode steps through a 4-slot cache (Mixtral layers < 12 get base + 1)
+    with evictions between steps: outputs equal the fixed-slot layer's."""
+    st, experts = store
+    cm = _manager(st, 3)
+    try:
+        ref, got = _layers(cm, experts, 0)
+        g = torch.Generator().manual_seed(21)
+        outs = []
+        for step in range(12):
+            x = (torch.randn(1, 1, H, generator=g)).half().to(DEV)
+            a, b = ref(x), got(x)
+            outs.append((a, b))  # compare after all steps: later loads must not clobber
+        torch.cuda.synchronize()
+        for step, (a, b) in enumerate(outs):
+            assert torch.equal(a, b), step
+        stats = cm.get_stats()
+        assert stats["total_misses"] >= 4 and stats["total_hits"] > 0
+    finally:
+        cm.shutdown()
+
+
+def test_prefill_through_resident_arena_matches_fixed_slots(store):
+    st, experts = store
+    cm = _manager(st, 3)
+    try:
+        cm.make_resident()
+        for layer in range(L):
+            ref, got = _layers(cm, experts, layer)
+            for T in (1, 16, 130):
+                x = (torch.randn(1, T, H, generator=torch.Generator().manual_seed(T)) * 1.0
+                     ).half().to(DEV)
+                assert torch.equal(ref(x), got(x)), (layer, T)
+        assert cm.get_stats()["total_misses"] == 0
+    finally:
+        cm.shutdown()
+
+
+def test_packed_get_expert_weights_dequant(store):
+    """get_expert_weights in packed mode = bit-exact oracle dequant of the blob."""
+    st, experts = store
+    cm = _manager(st, 3)
+    try:
+        w = cm.get_expert_weights(0, 5)
+        t = experts[(0, 5)]
+        for proj, pre in (("gate_proj", "gate"), ("up_proj", "up"), ("down_proj", "down")):
+            want = oracle.dequant(t[f"{pre}_packed"].numpy(), t[f"{pre}_scales"].numpy(), G)
+            assert np.array_equal(w[proj].cpu().numpy().view(np.uint16), want.view(np.uint16))
+        assert cm.get_expert_weights(0, 5) is w  # cached fp16 copy on a hit
+        cm.clear_layer_fp16(0)
+        assert cm.get_expert_weights(0, 5) is not w
+    finally:
+        cm.shutdown()
+
+
+def test_pack_experts_gpu_quantizer_matches_oracle(tmp_path):
+    """fp16 experts -> GPU quantiser -> experts.bin: blob bytes equal the
+    oracle's quantisation (ExpertWeightPacker rule) of the same weights."""
+    rng = np.random.default_rng(4)
+    weights = {}
+    for e in range(2):
+        weights[e] = {n: torch.from_numpy((rng.standard_normal(shp) * 0.02).astype(np.float16))
+                      for n, shp in (("gate_proj", (I, H)), ("up_proj", (I, H)),
+                                     ("down_proj", (H, I)))}
+    idx = ps.pack_experts(((0, e, w) for e, w in weights.items()), tmp_path, 1, 2, H, I, G,
+                          model_type="mixtral")
+    raw = (tmp_path / "experts.bin").read_bytes()
+    size = idx["experts"][0]["size"]
+    for e, w in weights.items():
+        t = {}
+        for proj, pre in (("gate_proj", "gate"), ("up_proj", "up"), ("down_proj", "down")):
+            p, s = oracle.quantize(w[proj].numpy(), G, mode=0)
+            t[f"{pre}_packed"], t[f"{pre}_scales"] = torch.from_numpy(p), torch.from_numpy(s.copy())
+        assert raw[e * size:(e + 1) * size] == ps.expert_blob(t).tobytes(), e
