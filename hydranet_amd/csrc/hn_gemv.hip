@@ -611,8 +611,10 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
   if (int rc = check_common(who, M, N, K, group, x, ld_x)) return rc;
   HN_ARG_CHECK(aligned16(w0.q) && w0.ld_q % 16 == 0 && aligned16(w1.q) && w1.ld_q % 16 == 0,
                "%s: packed weight rows must be 16-byte aligned", who);
-  HN_ARG_CHECK(N * w0.ld_q < (1L << 31) && N * w0.ld_s * 2 < (1L << 31),
-               "%s: one weight matrix must stay below 2 GiB", who);
+  // buffer descriptors span one matrix; the out-of-range offset marker
+  // (0x7ffffff0) must lie past that extent
+  HN_ARG_CHECK(N * w0.ld_q < 0x7ffffff0L && N * w0.ld_s * 2 < 0x7ffffff0L,
+               "%s: one weight matrix must stay below 2 GiB - 16 B", who);
   if (M == 0 || N == 0) return 0;
   const bool premul = (group % 128) != 0;
   if (M > kMaxRows) {
@@ -734,6 +736,8 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
   HN_ARG_CHECK(aligned16(x_perm) && aligned16(h_ws) && aligned16(y_perm), "%s: misaligned", who);
   HN_ARG_CHECK((I / 2) % 16 == 0, "%s: down rows (I/2=%ld bytes) must be 16-byte aligned", who,
                I / 2);
+  HN_ARG_CHECK(I * (H / 2) < 0x7ffffff0L && I * (H / group) * 2 < 0x7ffffff0L,
+               "%s: one weight matrix must stay below 2 GiB - 16 B", who);
   if (max_rows_per_expert == 0 || rows == 0) return 0;
   if (max_rows_per_expert > kMaxRows) {
     // prefill: the grouped MFMA GEMM (no workspace)

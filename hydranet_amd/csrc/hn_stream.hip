@@ -75,10 +75,13 @@ struct StreamArgs {
   uint32_t m_lo, m_hi, magic;
 };
 
-template <int MATS, int PAIRS>
+// Weights and scales of one column for one wave.  Scales: with WIDE, dword
+// pi holds the scales of groups (g0 + 2 pi, g0 + 2 pi + 1) of the lane's row
+// (read as one vector per row); without, the lane's own scale per pair.
+template <int MATS, int PAIRS, bool WIDE>
 struct WBuf {
   u32x4 lo[MATS][PAIRS], hi[MATS][PAIRS];
-  h16 slo[MATS][PAIRS], shi[MATS][PAIRS];
+  uint32_t slo[MATS][PAIRS], shi[MATS][PAIRS];
 };
 
 struct Problem {
@@ -136,8 +139,13 @@ __device__ __forceinline__ Problem resolve(const StreamArgs& A, const Meta& mt, 
 // loads return 0 without touching memory.  Groups past K (the last wave of
 // a K that is not a multiple of 2 * LPW * 128) read the next row or nothing;
 // they meet zero activations and their products are skipped.
-template <int MATS, int PAIRS>
-__device__ __forceinline__ void issue(WBuf<MATS, PAIRS>& b, const Problem& pr,
+// WIDE scales: one load per (matrix, row) of the wave's LPW scales (LPW * 2
+// bytes: b32 / b64 / b128 / 2 x b128), instead of one 2-byte load per lane
+// and pair (which costs as much address work as a 1 KiB weight load).  The
+// host selects it when the wave's groups lie inside the row (K / 128 = KW *
+// LPW) and scale rows and pointers are 16-byte aligned.
+template <int MATS, int PAIRS, bool WIDE>
+__device__ __forceinline__ void issue(WBuf<MATS, PAIRS, WIDE>& b, const Problem& pr,
                                       const StreamArgs& A, int tile, int g0, bool valid,
                                       int col, int q) {
   const int N = A.N, ldq = A.ld_q, lds2 = 2 * A.ld_s;
@@ -147,27 +155,62 @@ __device__ __forceinline__ void issue(WBuf<MATS, PAIRS>& b, const Problem& pr,
   const bool vl = valid && rlo < N, vh = valid && rhi < N;
   const uint32_t vlo = vl ? (uint32_t)(rlo * ldq + 64 * g0 + 16 * ch) : kOOB;
   const uint32_t vhi = vh ? (uint32_t)(rhi * ldq + 64 * g0 + 16 * ch) : kOOB;
-  const uint32_t vslo = vl ? (uint32_t)(rlo * lds2 + 2 * (g0 + odd)) : kOOB;
-  const uint32_t vshi = vh ? (uint32_t)(rhi * lds2 + 2 * (g0 + odd)) : kOOB;
+  const int gs = WIDE ? g0 : g0 + odd;
+  const uint32_t vslo = vl ? (uint32_t)(rlo * lds2 + 2 * gs) : kOOB;
+  const uint32_t vshi = vh ? (uint32_t)(rhi * lds2 + 2 * gs) : kOOB;
   __amdgpu_buffer_rsrc_t rq[MATS], rs[MATS];
 #pragma unroll
   for (int mt = 0; mt < MATS; ++mt) {
     rq[mt] = __builtin_amdgcn_make_buffer_rsrc((void*)pr.q[mt], (short)0, N * ldq, 0x00020000);
     rs[mt] = __builtin_amdgcn_make_buffer_rsrc((void*)pr.s[mt], (short)0, N * lds2, 0x00020000);
   }
-  // issue order = use order (pair, matrix, lo/hi)
-#pragma unroll
-  for (int pi = 0; pi < PAIRS; ++pi) {
+  if constexpr (WIDE) {
 #pragma unroll
     for (int mt = 0; mt < MATS; ++mt) {
-      b.lo[mt][pi] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vlo + 128 * pi, 0, 2));
-      b.slo[mt][pi] = __builtin_bit_cast(
-          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vslo + 4 * pi, 0, 0));
-      b.hi[mt][pi] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vhi + 128 * pi, 0, 2));
-      b.shi[mt][pi] = __builtin_bit_cast(
-          h16, __builtin_amdgcn_raw_buffer_load_b16(rs[mt], vshi + 4 * pi, 0, 0));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t vo = h ? vshi : vslo;
+        uint32_t* dst = h ? b.shi[mt] : b.slo[mt];
+        if constexpr (PAIRS == 1) {
+          dst[0] = __builtin_amdgcn_raw_buffer_load_b32(rs[mt], vo, 0, 0);
+        } else if constexpr (PAIRS == 2) {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs[mt], vo, 0, 0);
+          dst[0] = v[0];
+          dst[1] = v[1];
+        } else {
+#pragma unroll
+          for (int j = 0; j < PAIRS / 4; ++j) {
+            const u32x4 v = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[mt], vo + 16 * j, 0, 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[4 * j + e] = v[e];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int pi = 0; pi < PAIRS; ++pi) {
+#pragma unroll
+      for (int mt = 0; mt < MATS; ++mt) {
+        b.lo[mt][pi] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vlo + 128 * pi, 0, 2));
+        b.hi[mt][pi] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vhi + 128 * pi, 0, 2));
+      }
+    }
+  } else {
+    // issue order = use order (pair, matrix, lo/hi)
+#pragma unroll
+    for (int pi = 0; pi < PAIRS; ++pi) {
+#pragma unroll
+      for (int mt = 0; mt < MATS; ++mt) {
+        b.lo[mt][pi] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vlo + 128 * pi, 0, 2));
+        b.slo[mt][pi] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs[mt], vslo + 4 * pi, 0, 0);
+        b.hi[mt][pi] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mt], vhi + 128 * pi, 0, 2));
+        b.shi[mt][pi] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs[mt], vshi + 4 * pi, 0, 0);
+      }
     }
   }
 }
@@ -183,11 +226,11 @@ __device__ __forceinline__ half8_t unpack_biased(uint32_t w, const HnUnpackRegs&
 
 // Unpack + MFMA of one column for this wave.  acc_lo / acc_hi: D rows 4q + r
 // (token 2q + r/2, group parity r%2) of the lo / hi chains.
-template <int MATS, int PAIRS>
-__device__ __forceinline__ void compute(const WBuf<MATS, PAIRS>& b, const h16* xs,
+template <int MATS, int PAIRS, bool WIDE>
+__device__ __forceinline__ void compute(const WBuf<MATS, PAIRS, WIDE>& b, const h16* xs,
                                         const float* cs, int ldx, int pb0, int gw, int arow_i,
-                                        int q, const HnUnpackRegs& ur, float4_t acc_lo[MATS],
-                                        float4_t acc_hi[MATS]) {
+                                        int q, int sshift, const HnUnpackRegs& ur,
+                                        float4_t acc_lo[MATS], float4_t acc_hi[MATS]) {
 #pragma unroll
   for (int mt = 0; mt < MATS; ++mt) {
     acc_lo[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -212,7 +255,10 @@ __device__ __forceinline__ void compute(const WBuf<MATS, PAIRS>& b, const h16* x
         for (int t = 0; t < 4; ++t)
           ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], unpack_biased(b.hi[mt][pi][t], ur),
                                                       ch, 0, 0, 0);
-        const float sl = (float)b.slo[mt][pi], sh = (float)b.shi[mt][pi];
+        // WIDE: the lane's group parity picks the half of the pair's dword
+        const int sft = WIDE ? sshift : 0;
+        const float sl = (float)__builtin_bit_cast(h16, (uint16_t)(b.slo[mt][pi] >> sft));
+        const float sh = (float)__builtin_bit_cast(h16, (uint16_t)(b.shi[mt][pi] >> sft));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           acc_lo[mt][r] = __builtin_fmaf(sl, cl[r], acc_lo[mt][r]);
@@ -324,7 +370,7 @@ __device__ __forceinline__ void locate(Cursor& cu, const int* chunk_off, int npr
 
 // At most 8 waves per workgroup and one workgroup per CU: 2 waves per SIMD,
 // 256 VGPRs each.
-template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF>
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE>
 __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
                                                      const SExpert* __restrict__ table,
                                                      const int* __restrict__ active,
@@ -397,7 +443,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
   int parity = 0;
   const int blk_per_tok = A.npair * 2 * 16;
 
-  auto issue_next = [&](WBuf<MATS, PAIRS>& b) {
+  auto issue_next = [&](WBuf<MATS, PAIRS, WIDE>& b) {
     const bool more = ci < ce;
     int p = 0, ch = 0, t = 0;
     if (more) {
@@ -407,7 +453,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
         pi_last = p;
       }
     }
-    issue<MATS, PAIRS>(b, pi_pr, A, t, g0, more, col, q);
+    issue<MATS, PAIRS, WIDE>(b, pi_pr, A, t, g0, more, col, q);
     ++ci;
   };
   auto geom = [&](int ch) {
@@ -419,7 +465,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     return g;
   };
 
-  WBuf<MATS, PAIRS> b0, b1, b2;
+  WBuf<MATS, PAIRS, WIDE> b0, b1, b2;
   // ---- prologue: the first chunk's activations are requested before the
   //      first columns' weights and waited for alone
   {
@@ -448,7 +494,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
   // One column: restage if its chunk changes (before the next column's loads
   // go out, so waiting for the activations never waits for those), issue
   // column c + NBUF - 1, unpack/MFMA column c, reduce over the waves.
-  auto step = [&](int c, const WBuf<MATS, PAIRS>& cur, WBuf<MATS, PAIRS>& nxt) {
+  auto step = [&](int c, const WBuf<MATS, PAIRS, WIDE>& cur, WBuf<MATS, PAIRS, WIDE>& nxt) {
     int t = 0;
     if (c < ce) {  // uniform
       int p, ch;
@@ -466,7 +512,8 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
       const int Mc = sg.Mc;
       const int arow_i = 2 * min(col >> 1, Mc - 1) + (col & 1);
       float4_t acc_lo[MATS], acc_hi[MATS];
-      compute<MATS, PAIRS>(cur, xs, cs, A.ldx, pb0, gw, arow_i, q, ur, acc_lo, acc_hi);
+      compute<MATS, PAIRS, WIDE>(cur, xs, cs, A.ldx, pb0, gw, arow_i, q, col >= 8 ? 16 : 0, ur,
+                                 acc_lo, acc_hi);
       // lane (col, q): row n0 + col, tokens 2q, 2q + 1 (both group parities)
       float2 v[MATS];
       const bool low = col < 8;
@@ -553,6 +600,7 @@ struct GroupedPtrs {
 
 struct StreamPlan {
   bool ok;
+  bool wide;  // vector scale loads (set by the caller after its alignment checks)
   int lpw, nbuf, kw, tc, ldx, npair;
   int lds;  // dynamic LDS bytes per workgroup
 };
@@ -599,9 +647,9 @@ int num_cus() {
   return n;
 }
 
-template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF>
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE>
 int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
-  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF>;
+  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE>;
   static int attr = -1;  // per instantiation
   if (attr < 0) {
     attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -614,20 +662,32 @@ int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, h
   return 0;
 }
 
+template <bool GROUPED, int MATS, int EPI, bool WIDE>
+int launch_lpw(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
+  if constexpr (MATS == 2) {
+    if (p.lpw == 2) return launch_one<GROUPED, MATS, EPI, 2, 3, WIDE>(A, g, p, s);
+    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 3, WIDE>(A, g, p, s);
+    if (p.lpw == 8) return launch_one<GROUPED, MATS, EPI, 8, 2, WIDE>(A, g, p, s);
+  } else {
+    if (p.lpw == 2) return launch_one<GROUPED, MATS, EPI, 2, 3, WIDE>(A, g, p, s);
+    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 3, WIDE>(A, g, p, s);
+    if (p.lpw == 8) return launch_one<GROUPED, MATS, EPI, 8, 3, WIDE>(A, g, p, s);
+    if (p.lpw == 16) return launch_one<GROUPED, MATS, EPI, 16, 2, WIDE>(A, g, p, s);
+  }
+  return HN_NOT_HANDLED;
+}
+
 template <bool GROUPED, int MATS, int EPI>
 int launch_stream(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p,
                   hipStream_t s) {
-  if constexpr (MATS == 2) {
-    if (p.lpw == 2) return launch_one<GROUPED, MATS, EPI, 2, 3>(A, g, p, s);
-    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 3>(A, g, p, s);
-    if (p.lpw == 8) return launch_one<GROUPED, MATS, EPI, 8, 2>(A, g, p, s);
-  } else {
-    if (p.lpw == 2) return launch_one<GROUPED, MATS, EPI, 2, 3>(A, g, p, s);
-    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 3>(A, g, p, s);
-    if (p.lpw == 8) return launch_one<GROUPED, MATS, EPI, 8, 3>(A, g, p, s);
-    if (p.lpw == 16) return launch_one<GROUPED, MATS, EPI, 16, 2>(A, g, p, s);
-  }
-  return HN_NOT_HANDLED;
+  return p.wide ? launch_lpw<GROUPED, MATS, EPI, true>(A, g, p, s)
+                : launch_lpw<GROUPED, MATS, EPI, false>(A, g, p, s);
+}
+
+// Vector scale loads need the wave's LPW groups inside the scale row and
+// 16-byte aligned scale rows.
+bool wide_scales_ok(const StreamPlan& p, long K, long ld_s) {
+  return K / 128 == (long)p.kw * p.lpw && (ld_s * 2) % 16 == 0;
 }
 
 void fill_common(StreamArgs& A, const StreamPlan& p, long N, long K) {
@@ -654,9 +714,11 @@ extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const v
   const StreamPlan p = stream_plan(K, mats, M);
   if (!p.ok || group != 128 || M > p.tc) return HN_NOT_HANDLED;
   if (mats == 2 && p.lpw > 8) return HN_NOT_HANDLED;
-  if (N * ld_q >= (1L << 31) || N * ld_s * 2 >= (1L << 31) || ld_x >= (1L << 31) ||
+  if (N * ld_q >= (long)kOOB || N * ld_s * 2 >= (long)kOOB || ld_x >= (1L << 31) ||
       ld_o >= (1L << 31))
     return HN_NOT_HANDLED;
+  StreamPlan pw = p;
+  pw.wide = wide_scales_ok(p, K, ld_s) && ((uintptr_t)s0 & 15) == 0 && ((uintptr_t)s1 & 15) == 0;
   StreamArgs A = {};
   A.x = (const h16*)x;
   A.ld_x = (int)ld_x;
@@ -670,8 +732,8 @@ extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const v
   fill_common(A, p, N, K);
   hipStream_t s = (hipStream_t)stream;
   const GroupedPtrs g = {};
-  const int rc = mats == 2 ? launch_stream<false, 2, 1>(A, g, p, s)
-                           : launch_stream<false, 1, 0>(A, g, p, s);
+  const int rc = mats == 2 ? launch_stream<false, 2, 1>(A, g, pw, s)
+                           : launch_stream<false, 1, 0>(A, g, pw, s);
   if (rc) return rc;
   HN_LAUNCH_CHECK("hn_stream_linear");
   return 0;
@@ -689,8 +751,11 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
   const StreamPlan p = stream_plan(K, mats, max_rows);
   if (!p.ok || group != 128 || E > kMaxActive) return HN_NOT_HANDLED;
   if (mats == 2 && p.lpw > 8) return HN_NOT_HANDLED;
-  if (N * (K / 2) >= (1L << 31) || N * (K / group) * 2 >= (1L << 31)) return HN_NOT_HANDLED;
+  if (N * (K / 2) >= (long)kOOB || N * (K / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
   if (dry_run) return 0;
+  // table pointers are 16-byte aligned (the grouped entry point's contract)
+  StreamPlan pw = p;
+  pw.wide = wide_scales_ok(p, K, K / group);
   StreamArgs A = {};
   A.x = (const h16*)x;
   A.ld_x = (int)ld_x;
@@ -702,8 +767,8 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
   fill_common(A, p, N, K);
   const GroupedPtrs g = {(const SExpert*)table, active, n_active, offsets};
   hipStream_t s = (hipStream_t)stream;
-  const int rc = mats == 2 ? launch_stream<true, 2, 1>(A, g, p, s)
-                           : launch_stream<true, 1, 0>(A, g, p, s);
+  const int rc = mats == 2 ? launch_stream<true, 2, 1>(A, g, pw, s)
+                           : launch_stream<true, 1, 0>(A, g, pw, s);
   if (rc) return rc;
   HN_LAUNCH_CHECK("hn_stream_grouped");
   return 0;

@@ -49,8 +49,11 @@ class ExpertTable:
             self.dims = dims
         elif self.dims != dims:
             raise ValueError(f"expert {e} dims {dims} != table dims {self.dims}")
+        ptrs = slot.data_ptrs()
+        if any(p % 16 for p in ptrs):
+            raise ValueError(f"expert {e}: weight and scale tensors must start 16-byte aligned")
         self.slots[e] = slot
-        self.host[e] = torch.tensor(slot.data_ptrs(), dtype=torch.int64)
+        self.host[e] = torch.tensor(ptrs, dtype=torch.int64)
 
     def upload(self) -> None:
         self.dev.copy_(self.host)

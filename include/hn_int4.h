@@ -113,7 +113,8 @@ int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* i
 /* Grouped SwiGLU over every active expert of one MoE layer in two launches:
  * the decode kernels up to 64 rows per expert, the MFMA GEMM kernels above
  * (which take no workspace: it may then be NULL / 0 bytes).  x_perm [rows, H] sorted by expert; table: E x
- * {gate_q, gate_s, up_q, up_s, down_q, down_s} device pointers (u64); active /
+ * {gate_q, gate_s, up_q, up_s, down_q, down_s} device pointers (u64), each
+ * 16-byte aligned (GpuExpertSlot slabs are); active /
  * n_active / offsets from hn_moe_permute; h_ws [rows, I] fp16 buffer;
  * y_perm [rows, H] fp16 out; work: hn_skinny_workspace_bytes(3, rows, H, I, E).
  * Replaces the per-expert loop calling expert_mlp_int4_fused
