@@ -37,7 +37,14 @@ SIGNATURES: dict[str, list] = {
     "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],
     "hn_set_decode_path": [I],
     "hn_grouped_expert_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, P, P, P],
+    "hn_moe_route": [P, L, P, L, I, P, P, L, L, L, L, I, F, F, P, P, P, P, P, P, P, P, P, L,
+                     P],
 }
+
+# Sizes up to which hn_moe_route (one launch: logits, top-k, permutation,
+# gather) applies; larger batches use the separate kernels.
+ROUTE_MAX_LOGITS = 8192   # T * E
+ROUTE_MAX_ASSIGN = 1024   # T * k
 
 RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long}
 

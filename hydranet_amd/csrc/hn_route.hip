@@ -24,6 +24,8 @@
 //                      addend as in GLM4MoELayer (model/glm4.py:473).
 #include "hn_common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int kPermThreads = 1024;
@@ -47,6 +49,24 @@ __device__ __forceinline__ void load8f<float>(const float* p, float out[8]) {
   for (int j = 0; j < 4; ++j) { out[j] = a[j]; out[4 + j] = b[j]; }
 }
 
+// One wave's dot product of length H (fp32 accumulation, lane-strided, then a
+// butterfly over the wave; every lane returns the sum).
+template <typename TW, bool ROUND16>
+__device__ __forceinline__ float logit_dot(const h16* hr, const TW* wr, int H, int lane) {
+  float acc = 0.f;
+#pragma unroll 4
+  for (int k = lane * 8; k < H; k += 512) {
+    float a[8], b[8];
+    load8f<h16>(hr + k, a);
+    load8f<TW>(wr + k, b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(a[j], b[j], acc);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  return ROUND16 ? (float)(h16)acc : acc;
+}
+
 // One wave per (token, expert) dot product of length H; fp32 accumulation.
 template <typename TW, bool ROUND16>
 __global__ __launch_bounds__(256) void router_logits_kernel(const h16* __restrict__ h, long ld_h,
@@ -58,80 +78,159 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const h16* __restric
   if (wid >= (long)T * E) return;
   const int t = (int)(wid / E);
   const int e = (int)(wid - (long)t * E);
-  const h16* hr = h + (long)t * ld_h;
-  const TW* wr = w + (long)e * ld_w;
-  float acc = 0.f;
-  for (int k = lane * 8; k < H; k += 512) {
-    float a[8], b[8];
-    load8f<h16>(hr + k, a);
-    load8f<TW>(wr + k, b);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(a[j], b[j], acc);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (lane == 0) logits[(long)t * E + e] = ROUND16 ? (float)(h16)acc : acc;
+  const float acc = logit_dot<TW, ROUND16>(h + (long)t * ld_h, w + (long)e * ld_w, H, lane);
+  if (lane == 0) logits[(long)t * E + e] = acc;
 }
 
 __device__ __forceinline__ float sigmoid_f32(float l) {
   return (float)(1.0 / (1.0 + exp(-(double)l)));
 }
 
-// One thread per token.
-__global__ __launch_bounds__(256) void router_topk_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int k,
-    int mode, float eps, float scaling, int* __restrict__ idx_out, h16* __restrict__ w_out) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  const float* l = logits + (long)t * E;
-  float key[kMaxTopK];
+// Selection order of top-k: larger value first, equal values lower expert
+// first (a strict total order on (value, expert) for non-NaN values).
+__device__ __forceinline__ bool topk_beats(float bv, int be, float av, int ae) {
+  return bv > av || (bv == av && be < ae);
+}
+
+// Routing weights of the k selected experts sel[0..k) (already written) from
+// the token's raw logits l: mode 0 softmax over the selected logits (exp in
+// double, one rounding to fp32 per element) and renormalisation by the fp32
+// sum (model/router.py:114-117); mode 1 sigmoid, / (sum + eps) * scaling
+// (model/glm4.py:282-307).  Compact loops: each element's value is recomputed
+// where it is needed (same arithmetic each time) instead of kept in arrays.
+__device__ __noinline__ void topk_weights(const float* l, const int* sel, int k, int mode,
+                                          float eps, float scaling, h16* w_o) {
+  if (mode == 0) {
+    const double mx = (double)l[sel[0]];
+    double z = 0.0;
+#pragma unroll 1
+    for (int i = 0; i < k; ++i) z += exp((double)l[sel[i]] - mx);
+    float s = 0.f;
+#pragma unroll 1
+    for (int i = 0; i < k; ++i) s += (float)(exp((double)l[sel[i]] - mx) / z);
+#pragma unroll 1
+    for (int i = 0; i < k; ++i) w_o[i] = (h16)((float)(exp((double)l[sel[i]] - mx) / z) / s);
+  } else {
+    float s = 0.f;
+#pragma unroll 1
+    for (int i = 0; i < k; ++i) s += sigmoid_f32(l[sel[i]]);
+    const float d = s + eps;
+#pragma unroll 1
+    for (int i = 0; i < k; ++i) w_o[i] = (h16)((sigmoid_f32(l[sel[i]]) / d) * scaling);
+  }
+}
+
+// Top-k of one token's logits row by one wave: lanes hold experts lane +
+// 64 j (E <= 256), k rounds of a wave-wide maximum.  Same selection and the
+// same weight arithmetic (on lane 0, in the same order) as topk_row, without
+// per-thread arrays indexed at run time.
+__device__ __forceinline__ void topk_wave(const float* l, const float* bias, int E, int k,
+                                          int mode, float eps, float scaling, int lane,
+                                          int* idx_o, h16* w_o) {
+  constexpr int kNone = 0x7fffffff;
+  float cv[4];
+  int ce[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    cv[j] = -__builtin_inff();
+    ce[j] = kNone;
+    if (e < E) {
+      float v = l[e];
+      if (mode == 1) {
+        v = sigmoid_f32(v);
+        if (bias) v = v + bias[e];
+      }
+      cv[j] = v;
+      ce[j] = e;
+    }
+  }
   int sel[kMaxTopK];
-  int n = 0;
-  for (int e = 0; e < E; ++e) {
-    float v = l[e];
-    if (mode == 1) {
+#pragma unroll
+  for (int i = 0; i < kMaxTopK; ++i) {
+    sel[i] = -1;
+    if (i < k) {
+      float bv = cv[0];
+      int be = ce[0];
+#pragma unroll
+      for (int j = 1; j < 4; ++j)
+        if (topk_beats(cv[j], ce[j], bv, be)) { bv = cv[j]; be = ce[j]; }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oe = __shfl_xor(be, off, 64);
+        if (topk_beats(ov, oe, bv, be)) { bv = ov; be = oe; }
+      }
+      sel[i] = be < E ? be : -1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (ce[j] == be) { cv[j] = -__builtin_inff(); ce[j] = kNone; }
+    }
+  }
+  if (lane != 0) return;
+#pragma unroll
+  for (int i = 0; i < kMaxTopK; ++i)
+    if (i < k) idx_o[i] = sel[i];
+  topk_weights(l, idx_o, k, mode, eps, scaling, w_o);
+}
+
+// Top-k of one token's row by one thread for E <= EB experts: every loop is
+// unrolled over compile-time bounds, so the candidates and the selection
+// stay in registers.  Same selection and weight arithmetic as topk_wave.
+template <int EB, int KB = kMaxTopK, int MODE = -1>
+__device__ __forceinline__ void topk_small(const float* l, const float* bias, int E, int k,
+                                           int mode_rt, float eps, float scaling, int* idx_o,
+                                           h16* w_o) {
+  const int mode = MODE >= 0 ? MODE : mode_rt;
+  float cv[EB];
+  bool ok[EB];
+#pragma unroll
+  for (int e = 0; e < EB; ++e) {
+    ok[e] = e < E;
+    float v = ok[e] ? l[e] : 0.f;
+    if (mode == 1 && ok[e]) {
       v = sigmoid_f32(v);
       if (bias) v = v + bias[e];
     }
-    // insert if strictly greater than the current k-th (ties keep lower index)
-    if (n < k || v > key[n - 1]) {
-      int p = (n < k) ? n : k - 1;
-      while (p > 0 && v > key[p - 1]) {
-        key[p] = key[p - 1];
-        sel[p] = sel[p - 1];
-        --p;
-      }
-      key[p] = v;
-      sel[p] = e;
-      if (n < k) ++n;
+    cv[e] = v;
+  }
+  int sel[KB];
+#pragma unroll
+  for (int i = 0; i < KB; ++i) {
+    sel[i] = -1;
+    if (i < k) {
+      float bv = -__builtin_inff();
+      int be = 0x7fffffff;
+#pragma unroll
+      for (int e = 0; e < EB; ++e)
+        if (ok[e] && topk_beats(cv[e], e, bv, be)) { bv = cv[e]; be = e; }
+      sel[i] = be < E ? be : -1;
+#pragma unroll
+      for (int e = 0; e < EB; ++e)
+        if (e == be) ok[e] = false;
     }
   }
-  float wt[kMaxTopK];
-  if (mode == 0) {
-    // softmax over the selected logits (fp32 result per element), then
-    // divide by the fp32 sum (model/router.py:114-117)
-    const double mx = (double)l[sel[0]];
-    double z = 0.0;
-    for (int i = 0; i < n; ++i) z += exp((double)l[sel[i]] - mx);
-    float s = 0.f;
-    for (int i = 0; i < n; ++i) {
-      wt[i] = (float)(exp((double)l[sel[i]] - mx) / z);
-      s += wt[i];
-    }
-    for (int i = 0; i < n; ++i) wt[i] = wt[i] / s;
-  } else {
-    float s = 0.f;
-    for (int i = 0; i < n; ++i) {
-      wt[i] = sigmoid_f32(l[sel[i]]);
-      s += wt[i];
-    }
-    const float d = s + eps;
-    for (int i = 0; i < n; ++i) wt[i] = (wt[i] / d) * scaling;
+#pragma unroll
+  for (int i = 0; i < KB; ++i)
+    if (i < k) idx_o[i] = sel[i];
+  topk_weights(l, idx_o, k, mode, eps, scaling, w_o);
+}
+
+// One wave per token (more than 16 experts) or one thread per token.
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int k,
+    int mode, float eps, float scaling, int* __restrict__ idx_out, h16* __restrict__ w_out) {
+  if (E <= 16) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    topk_small<16>(logits + (long)t * E, bias, E, k, mode, eps, scaling, idx_out + (long)t * k,
+                   w_out + (long)t * k);
+    return;
   }
-  for (int i = 0; i < k; ++i) {
-    idx_out[(long)t * k + i] = (i < n) ? sel[i] : -1;
-    w_out[(long)t * k + i] = (i < n) ? (h16)wt[i] : (h16)0.0f;
-  }
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  topk_wave(logits + (long)t * E, bias, E, k, mode, eps, scaling, threadIdx.x & 63,
+            idx_out + (long)t * k, w_out + (long)t * k);
 }
 
 // Single-workgroup stable counting sort.  Entries outside [0, E) are ignored
@@ -266,6 +365,205 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
   }
 }
 
+// Decode routing in one launch.  Every workgroup computes the routing of all
+// T tokens into LDS (logits unless given, top-k, the stable order by expert),
+// then copies its share of the permuted rows x_perm[p] = h[perm[p] / k];
+// workgroup 0 also writes the routing outputs.  Top-k and the order are those
+// of router_topk_kernel / moe_permute_kernel.  Logits (LG):
+//  * 1, 2: MFMA (fp16 gate, T <= 16 / 32 tokens, E <= 16, H % 512 == 0):
+//    each of the 16 waves multiplies one 1/16 slice of H (all its loads in
+//    flight together), the 16 partial 16x16 tiles are summed in wave order,
+//    then rounded to fp16 (the fp16 Linear of the reference);
+//  * 0: one wave per (token, expert) dot product, as router_logits_kernel.
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / 64;
+constexpr int kRouteMaxLogits = 8192;  // T * E
+constexpr int kRouteMaxAssign = 1024;  // T * k (one thread per assignment)
+
+template <typename TW, bool ROUND16, int LG, int TK>
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
+    const h16* __restrict__ h, long ld_h, const TW* __restrict__ w, long ld_w,
+    const float* __restrict__ logits_in, const float* __restrict__ bias, int T, int E, int H,
+    int k, int mode, float eps, float scaling, float* __restrict__ logits_out,
+    int* __restrict__ idx_out, h16* __restrict__ w_out, int* __restrict__ offsets,
+    int* __restrict__ perm, int* __restrict__ inv, int* __restrict__ active,
+    int* __restrict__ n_active, h16* __restrict__ x_perm, long ld_p) {
+  __shared__ float s_buf[kRouteMaxLogits];  // logits, or the MFMA partial tiles
+  __shared__ float s_lg[512];               // MFMA logits (T <= 32, E <= 16)
+  __shared__ int s_sel[kRouteMaxAssign];
+  __shared__ h16 s_w[kRouteMaxAssign];
+  __shared__ int s_perm[kRouteMaxAssign];
+  __shared__ int s_wcnt[kRouteWaves][kMaxExperts];  // per wave, per expert
+  __shared__ int s_off[kMaxExperts + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = blockDim.x >> 6;
+  const bool lead = blockIdx.x == 0;
+  const int n = T * k;
+
+  for (int i = tid; i < kRouteWaves * kMaxExperts; i += blockDim.x) (&s_wcnt[0][0])[i] = 0;
+
+  // 1. logits
+  const float* lg = s_buf;
+  if (logits_in) {
+    for (int i = tid; i < T * E; i += blockDim.x) s_buf[i] = logits_in[i];
+  } else if constexpr (LG > 0) {
+    const int ksl = H >> 4, kb0 = wave * ksl, steps = ksl >> 5;
+    const int tl = lane & 15, kq = (lane >> 4) * 8;
+    const h16* ap[LG];
+#pragma unroll
+    for (int u = 0; u < LG; ++u) ap[u] = h + (long)min(16 * u + tl, T - 1) * ld_h + kb0 + kq;
+    const h16* bp = reinterpret_cast<const h16*>(w) + (long)min(tl, E - 1) * ld_w + kb0 + kq;
+    float4_t acc[LG];
+#pragma unroll
+    for (int u = 0; u < LG; ++u) acc[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int st = 0; st < steps; ++st) {
+      const half8_t b = *reinterpret_cast<const half8_t*>(bp + 32 * st);
+#pragma unroll
+      for (int u = 0; u < LG; ++u) {
+        const half8_t a = *reinterpret_cast<const half8_t*>(ap[u] + 32 * st);
+        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[u], 0, 0, 0);
+      }
+    }
+    // lane: expert tl, tokens 16 u + 4 (lane >> 4) + r
+#pragma unroll
+    for (int u = 0; u < LG; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        s_buf[(wave * 32 + 16 * u + 4 * (lane >> 4) + r) * 16 + tl] = acc[u][r];
+    __syncthreads();
+    for (int i = tid; i < T * E; i += blockDim.x) {
+      const int t = i / E, e = i - t * E;
+      float v = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < kRouteWaves; ++w2) v += s_buf[(w2 * 32 + t) * 16 + e];
+      s_lg[i] = ROUND16 ? (float)(h16)v : v;
+    }
+    lg = s_lg;
+  } else {
+    for (int pr = wave; pr < T * E; pr += nw) {
+      const int t = pr / E, e = pr - t * E;
+      const float v = logit_dot<TW, ROUND16>(h + (long)t * ld_h, w + (long)e * ld_w, H, lane);
+      if (lane == 0) s_buf[pr] = v;
+    }
+  }
+  __syncthreads();
+  if (lead && logits_out)
+    for (int i = tid; i < T * E; i += blockDim.x) logits_out[i] = lg[i];
+
+  // 2. top-k: one thread per token up to 16 experts, else one wave per token
+  if constexpr (TK == 1) {  // E <= 8, k == 2, softmax (Mixtral)
+    for (int t = tid; t < T; t += blockDim.x)
+      topk_small<8, 2, 0>(lg + t * E, bias, E, 2, 0, eps, scaling, s_sel + t * 2, s_w + t * 2);
+  } else if (E <= 16) {
+    for (int t = tid; t < T; t += blockDim.x)
+      topk_small<16>(lg + t * E, bias, E, k, mode, eps, scaling, s_sel + t * k, s_w + t * k);
+  } else {
+    for (int t = wave; t < T; t += nw)
+      topk_wave(lg + t * E, bias, E, k, mode, eps, scaling, lane, s_sel + t * k, s_w + t * k);
+  }
+  __syncthreads();
+  if (lead)
+    for (int j = tid; j < n; j += blockDim.x) {
+      idx_out[j] = s_sel[j];
+      w_out[j] = s_w[j];
+    }
+
+  // 3. stable order by expert: one thread per assignment j (n <= blockDim);
+  //    rank among equal experts in the wave from nine ballots over the bits
+  //    of e (-1 for none), then the per-wave counts before this wave
+  const int j = tid;
+  int e = j < n ? s_sel[j] : -1;
+  if (e < 0 || e >= E) e = -1;
+  uint64_t same = ~0ull;
+#pragma unroll
+  for (int b = 0; b < 9; ++b) {
+    const uint64_t bal = __ballot((e >> b) & 1);
+    same &= ((e >> b) & 1) ? bal : ~bal;
+  }
+  const int rank = __popcll(same & ((1ull << lane) - 1));
+  if (e >= 0 && rank == 0) s_wcnt[wave][e] = __popcll(same);
+  __syncthreads();
+  if (wave == 0) {  // counts, offsets and the active list: 4 experts per lane, wave scans
+    int c[4], f[4], cs = 0, fs = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ex = 4 * lane + q;
+      c[q] = 0;
+      if (ex < E)
+        for (int w2 = 0; w2 < kRouteWaves; ++w2) c[q] += s_wcnt[w2][ex];
+      f[q] = c[q] > 0 ? 1 : 0;
+      cs += c[q];
+      fs += f[q];
+    }
+    int ci = cs, fi = fs;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int oc = __shfl_up(ci, off, 64), of = __shfl_up(fi, off, 64);
+      if (lane >= off) { ci += oc; fi += of; }
+    }
+    int co = ci - cs, fo = fi - fs;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ex = 4 * lane + q;
+      if (ex < E) {
+        s_off[ex] = co;
+        if (lead) {
+          offsets[ex] = co;
+          if (f[q]) active[fo] = ex;
+        }
+      }
+      co += c[q];
+      fo += f[q];
+    }
+    if (lane == 63) {
+      s_off[E] = ci;
+      if (lead) {
+        offsets[E] = ci;
+        *n_active = fi;
+      }
+    }
+  }
+  __syncthreads();
+  if (j < n) {
+    if (e >= 0) {
+      int pos = s_off[e] + rank;
+      for (int w2 = 0; w2 < wave; ++w2) pos += s_wcnt[w2][e];
+      s_perm[pos] = j;
+      if (lead) {
+        perm[pos] = j;
+        inv[j] = pos;
+      }
+    } else if (lead) {
+      inv[j] = -1;
+    }
+  }
+  __syncthreads();
+
+  // 4. this workgroup's rows of x_perm (16-byte pieces, 4 in flight per thread)
+  const int rows = s_off[E];
+  const int per_row = H >> 3;
+  const int pieces = rows * per_row;  // < 2^31: T*k <= 1024 rows, checked H
+  for (int base = blockIdx.x * blockDim.x * 4 + tid; base < pieces;
+       base += gridDim.x * blockDim.x * 4) {
+    half8_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(base + u * (int)blockDim.x, pieces - 1);
+      const int p = i / per_row, c = i - p * per_row;
+      v[u] = *reinterpret_cast<const half8_t*>(h + (long)(s_perm[p] / k) * ld_h + c * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + u * (int)blockDim.x;
+      if (i < pieces) {
+        const int p = i / per_row, c = i - p * per_row;
+        *reinterpret_cast<half8_t*>(x_perm + (long)p * ld_p + c * 8) = v[u];
+      }
+    }
+  }
+}
+
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
@@ -301,7 +599,8 @@ extern "C" int hn_router_topk(const void* logits, const void* bias, long T, long
                "hn_router_topk: need 0 < k <= min(E, %d)", kMaxTopK);
   HN_ARG_CHECK(mode == 0 || mode == 1, "hn_router_topk: mode must be 0 or 1");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(router_topk_kernel, dim3(hn_cdiv(T, 256)), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(router_topk_kernel, dim3(E <= 16 ? hn_cdiv(T, 256) : hn_cdiv(T, 4)), dim3(256),
+                     0, (hipStream_t)stream,
                      (const float*)logits, (const float*)bias, (int)T, (int)E, (int)k, mode, eps,
                      scaling, idx_out, (h16*)w_out);
   HN_LAUNCH_CHECK("hn_router_topk");
@@ -345,5 +644,52 @@ extern "C" int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, c
                      (const h16*)y_perm, ld_y, inv, idx, (const h16*)w, (int)k,
                      (const h16*)shared, ld_sh, (h16*)out, ld_o, (int)H);
   HN_LAUNCH_CHECK("hn_moe_unpermute");
+  return 0;
+}
+
+// Decode routing in one launch (logits unless logits_in is given, top-k,
+// permutation, gather).  See include/hn_int4.h.
+extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, int w_dtype,
+                            const void* logits_in, const void* bias, long T, long E, long H,
+                            long k, int mode, float eps, float scaling, void* logits_out,
+                            int* idx_out, void* w_out, int* offsets, int* perm, int* inv,
+                            int* active, int* n_active, void* x_perm, long ld_p, void* stream) {
+  const char* who = "hn_moe_route";
+  HN_ARG_CHECK(T >= 0 && E > 0 && E <= kMaxExperts && H > 0,
+               "%s: need 0 < E <= %d", who, kMaxExperts);
+  HN_ARG_CHECK(k > 0 && k <= kMaxTopK && k <= E, "%s: need 0 < k <= min(E, %d)", who, kMaxTopK);
+  HN_ARG_CHECK(mode == 0 || mode == 1, "%s: mode must be 0 or 1", who);
+  HN_ARG_CHECK(T * E <= kRouteMaxLogits && T * k <= kRouteMaxAssign,
+               "%s: T*E <= %d and T*k <= %d (decode sizes; use the separate kernels above)",
+               who, kRouteMaxLogits, kRouteMaxAssign);
+  HN_ARG_CHECK(H % 8 == 0 && ld_h % 8 == 0 && al16(h) && al16(x_perm) && ld_p % 8 == 0,
+               "%s: h and x_perm rows must be 16-byte aligned with H %% 8 == 0", who);
+  HN_ARG_CHECK(logits_in || (w && al16(w) && (w_dtype == 0 ? ld_w % 8 == 0 : ld_w % 4 == 0)),
+               "%s: weight rows must be 16-byte aligned (or pass logits_in)", who);
+  if (T == 0) return 0;
+  // about 64 KiB of rows per workgroup; every workgroup repeats the routing
+  const long bytes = T * k * H * 2;
+  const int grid = (int)std::min(128L, std::max(1L, (bytes + 65535) / 65536));
+  hipStream_t s = (hipStream_t)stream;
+  // logits by MFMA for an fp16 gate with T <= 32, E <= 16, H % 512 == 0
+  const int lgv = (logits_in || w_dtype != 0 || E > 16 || H % 512 != 0) ? 0 : (T <= 16 ? 1 : (T <= 32 ? 2 : 0));
+  const bool mix = E <= 8 && k == 2 && mode == 0;
+#define HN_ROUTE_LAUNCH(TW, R16, LGV, TKV)                                                          \
+  hipLaunchKernelGGL((moe_route_kernel<TW, R16, LGV, TKV>), dim3(grid), dim3(kRouteThreads), 0, s, \
+                     (const h16*)h, ld_h, (const TW*)w, ld_w, (const float*)logits_in,           \
+                     (const float*)bias, (int)T, (int)E, (int)H, (int)k, mode, eps, scaling,      \
+                     (float*)logits_out, idx_out, (h16*)w_out, offsets, perm, inv, active,        \
+                     n_active, (h16*)x_perm, ld_p)
+  if (w_dtype == 0) {
+    if (lgv == 1 && mix) HN_ROUTE_LAUNCH(h16, true, 1, 1);
+    else if (lgv == 2 && mix) HN_ROUTE_LAUNCH(h16, true, 2, 1);
+    else if (lgv == 1) HN_ROUTE_LAUNCH(h16, true, 1, 0);
+    else if (lgv == 2) HN_ROUTE_LAUNCH(h16, true, 2, 0);
+    else HN_ROUTE_LAUNCH(h16, true, 0, 0);
+  } else {
+    HN_ROUTE_LAUNCH(float, false, 0, 0);
+  }
+#undef HN_ROUTE_LAUNCH
+  HN_LAUNCH_CHECK(who);
   return 0;
 }

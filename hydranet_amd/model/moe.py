@@ -29,7 +29,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .. import _lib
-from .router import GLM4SigmoidRouter, TopKRouter
+from .router import GLM4SigmoidRouter, TopKRouter, router_logits
 
 
 class ExpertTable:
@@ -65,6 +65,93 @@ class ExpertTable:
             t.set(e, s)
         t.upload()
         return t
+
+
+class Routed:
+    """Routing of one MoE layer call: idx [T,k] i32, w [T,k] fp16, logits [T,E] f32
+    (or None), the permutation metadata and the permuted rows x_perm [T*k, H]."""
+
+    def __init__(self, T, k, E, H, device):
+        n = max(T * k, 1)
+        self.T, self.k, self.E = T, k, E
+        self.meta = torch.empty(3 * E + 2 + 2 * n, dtype=torch.int32, device=device)
+        self.offsets = self.meta[: E + 1]
+        self.active = self.meta[E + 1: 2 * E + 1]
+        self.n_active = self.meta[2 * E + 1: 2 * E + 2]
+        self.perm = self.meta[2 * E + 2: 2 * E + 2 + n]
+        self.inv = self.meta[2 * E + 2 + n: 2 * E + 2 + 2 * n]
+        self.idx = torch.empty((T, k), dtype=torch.int32, device=device)
+        self.w = torch.empty((T, k), dtype=torch.float16, device=device)
+        self.logits = None
+        self.x_perm = torch.empty((n, H), dtype=torch.float16, device=device)
+
+
+def route_fits(T: int, E: int, k: int) -> bool:
+    """Whether hn_moe_route (one launch) covers this batch."""
+    return 0 < T * E <= _lib.ROUTE_MAX_LOGITS and T * k <= _lib.ROUTE_MAX_ASSIGN and E <= 256
+
+
+def moe_route(hidden: torch.Tensor, k: int, mode: int, gate_w: Optional[torch.Tensor] = None,
+              logits: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+              eps: float = 1e-9, scaling: float = 1.0, want_logits: bool = True) -> Routed:
+    """Logits (from gate_w, unless ``logits`` is given), top-k, permutation and
+    gather in one launch (hn_moe_route).  mode 0: Mixtral softmax top-k over
+    fp16-rounded logits of an fp16 gate; mode 1: GLM sigmoid top-k (fp32 gate)."""
+    T, H = hidden.shape
+    _lib.require_gpu(hidden)
+    dev = hidden.device
+    x = _lib.aligned_rows(hidden.to(torch.float16))
+    E = (logits.shape[1] if logits is not None else gate_w.shape[0])
+    r = Routed(T, k, E, H, dev)
+    wptr, ldw, wdt = None, 0, 0
+    lg_in = None
+    if logits is not None:
+        lg_in = logits.to(torch.float32).contiguous()
+        r.logits = lg_in
+    else:
+        wdt = 0 if mode == 0 else 1
+        ww = gate_w.to(torch.float16 if wdt == 0 else torch.float32)
+        ww = _lib.aligned_rows(ww)
+        wptr, ldw = ww, ww.stride(0)
+        if want_logits:
+            r.logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
+    out_logits = r.logits if lg_in is None else None
+    _lib.call("hn_moe_route", _lib.ptr(x), x.stride(0), _lib.ptr(wptr), ldw, wdt,
+              _lib.ptr(lg_in), _lib.ptr(b), T, E, H, k, mode, eps, scaling,
+              _lib.ptr(out_logits), _lib.ptr(r.idx), _lib.ptr(r.w), _lib.ptr(r.offsets),
+              _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active), _lib.ptr(r.n_active),
+              _lib.ptr(r.x_perm), H, _lib.stream(dev))
+    return r
+
+
+def moe_dispatch(r: Routed, table: ExpertTable,
+                 shared: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Grouped SwiGLU over the routed rows and the weighted, ordered sum back
+    per token (the compute and unpermute halves of moe_experts_forward)."""
+    T, k, E = r.T, r.k, r.E
+    H = r.x_perm.shape[1]
+    Ht, I, g = table.dims
+    assert Ht == H, f"hidden {H} != expert hidden {Ht}"
+    assert table.num_experts == E, f"routing over {E} experts, table has {table.num_experts}"
+    dev = r.x_perm.device
+    st = _lib.stream(dev)
+    n = T * k
+    h_ws = torch.empty((max(n, 1), I), dtype=torch.float16, device=dev)
+    y_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
+    work = _lib.skinny_workspace(3, n, H, I, E, dev) if T <= _lib.DECODE_MAX_ROWS else None
+    _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(r.x_perm), _lib.ptr(table.dev),
+              _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I, g,
+              _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work),
+              0 if work is None else work.numel(), st)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    sh = None
+    if shared is not None:
+        sh = _lib.aligned_rows(shared.reshape(T, H).to(torch.float16))
+    _lib.call("hn_moe_unpermute", _lib.ptr(y_perm), H, _lib.ptr(r.inv), _lib.ptr(r.idx),
+              _lib.ptr(r.w), T, k, _lib.ptr(sh), H if sh is None else sh.stride(0), _lib.ptr(out),
+              H, H, st)
+    return out
 
 
 def moe_experts_forward(hidden: torch.Tensor, idx: torch.Tensor, w: torch.Tensor,
@@ -172,11 +259,24 @@ class MixtralMoELayer(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor, top_k: int = 2) -> torch.Tensor:
         B, S, H = hidden_states.shape
-        ro = self.router(hidden_states, top_k_override=top_k)
-        flat = hidden_states.reshape(B * S, H)
-        idx = ro.expert_indices.reshape(B * S, top_k)
+        T = B * S
+        flat = hidden_states.reshape(T, H)
+        rt = self.router
+        if route_fits(T, self.num_experts, top_k):
+            # decode: routing, permutation and gather in one launch
+            logits = None
+            if rt.enable_affinity_bonus and rt._is_cached_fn is not None:
+                logits = rt._affinity(router_logits(flat, rt.gate.weight.to(torch.float16)))
+            r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits)
+            if not rt.training:
+                rt.usage_counts += torch.bincount(r.idx.view(-1).long(),
+                                                  minlength=self.num_experts)
+            out = moe_dispatch(r, self.experts.table_for(r.idx))
+            return out.view(B, S, H)
+        ro = rt(hidden_states, top_k_override=top_k)
+        idx = ro.expert_indices.reshape(T, top_k)
         table = self.experts.table_for(idx)
-        out = moe_experts_forward(flat, idx, ro.expert_weights.reshape(B * S, top_k), table)
+        out = moe_experts_forward(flat, idx, ro.expert_weights.reshape(T, top_k), table)
         return out.view(B, S, H)
 
 
@@ -216,8 +316,18 @@ class GLM4MoELayer(nn.Module):
         shared = self.shared_expert(hidden_states)
         if skip_routed:
             return shared
-        idx, w = self.router(hidden_states)
+        T = B * S
+        flat = hidden_states.reshape(T, H)
+        rt = self.router
+        if route_fits(T, rt.num_experts, rt.top_k):
+            # fp32 logits by the multi-workgroup kernel, the rest in one launch
+            logits = router_logits(flat, rt.weight.float() if rt.weight.dtype != torch.float32
+                                   else rt.weight)
+            r = moe_route(flat, rt.top_k, 1, logits=logits, bias=rt.selection_bias,
+                          scaling=rt.routed_scaling_factor)
+            out = moe_dispatch(r, self.experts.table_for(r.idx), shared=shared.reshape(T, H))
+            return out.view(B, S, H)
+        idx, w = rt(hidden_states)
         table = self.experts.table_for(idx)
-        out = moe_experts_forward(hidden_states.reshape(B * S, H), idx, w, table,
-                                  shared=shared.reshape(B * S, H))
+        out = moe_experts_forward(flat, idx, w, table, shared=shared.reshape(T, H))
         return out.view(B, S, H)

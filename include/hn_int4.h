@@ -103,6 +103,22 @@ int hn_moe_permute(const int* idx, long T, long k, long E, int* offsets, int* pe
 int hn_moe_gather(const void* x, long ld_x, const int* perm, long k, const int* offsets, long E,
                   void* x_perm, long ld_p, long rows, long H, void* stream);
 
+/* Decode routing in one launch: logits (w_dtype as hn_router_logits; skipped
+ * when logits_in [T, E] fp32 is given), top-k (mode, bias, eps, scaling as
+ * hn_router_topk), the stable permutation (as hn_moe_permute) and the gather
+ * x_perm [T*k, H] (as hn_moe_gather); logits_out may be NULL.  Every
+ * workgroup repeats the routing of all T tokens and copies a share of the
+ * rows, so the outputs equal those of the four separate kernels.
+ * T*E <= 8192, T*k <= 1024, E <= 256.  Replaces TopKRouter.forward
+ * (model/router.py:96-120) or GLM4SigmoidRouter.forward (model/glm4.py:275-309)
+ * plus the unique()/where()/gather steps of MixtralMoELayer.forward
+ * (model/mixtral.py:296-338) at decode sizes. */
+int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, int w_dtype,
+                 const void* logits_in, const void* bias, long T, long E, long H, long k,
+                 int mode, float eps, float scaling, void* logits_out, int* idx_out,
+                 void* w_out, int* offsets, int* perm, int* inv, int* active, int* n_active,
+                 void* x_perm, long ld_p, void* stream);
+
 /* out[T, H] = (shared +) sum over the token's experts (ascending id) of
  * fp16(y_perm[inv[t*k+s]] * w[t, s]) with fp16 accumulation: output.index_add_
  * (model/mixtral.py:365-368) and shared + routed (model/glm4.py:473). */

@@ -242,3 +242,87 @@ def test_glm_moe_layer_c3(T, decode_path):
     ref = torch_ref.glm_moe(h.view(T, 4096), None, cpu, shared,
                             routing=(idx.long().cpu(), w.cpu()))
     _close(out.view(T, 4096), ref)
+
+
+# --------------------------------------------------------------------------- fused routing
+def _separate_route(h, gate_w, k, mode, bias=None, scaling=1.0, logits=None):
+    """Routing through the four separate kernels (logits, top-k, permute, gather)."""
+    from hydranet_amd import _lib
+    from hydranet_amd.model.router import router_logits, topk_from_logits
+    T, H = h.shape
+    if logits is None:
+        logits = router_logits(h, gate_w)
+    E = logits.shape[1]
+    idx, w = topk_from_logits(logits, k, mode, bias=bias, scaling=scaling)
+    n = T * k
+    offs = torch.empty(E + 1, dtype=torch.int32, device=DEV)
+    act = torch.empty(E, dtype=torch.int32, device=DEV)
+    na = torch.empty(1, dtype=torch.int32, device=DEV)
+    perm = torch.empty(n, dtype=torch.int32, device=DEV)
+    inv = torch.empty(n, dtype=torch.int32, device=DEV)
+    st = _lib.stream()
+    _lib.call("hn_moe_permute", _lib.ptr(idx), T, k, E, _lib.ptr(offs), _lib.ptr(perm),
+              _lib.ptr(inv), _lib.ptr(act), _lib.ptr(na), st)
+    xp = torch.empty(n, H, dtype=torch.float16, device=DEV)
+    _lib.call("hn_moe_gather", _lib.ptr(h), H, _lib.ptr(perm), k, _lib.ptr(offs), E,
+              _lib.ptr(xp), H, n, H, st)
+    return dict(idx=idx, w=w, logits=logits, offsets=offs, perm=perm, inv=inv,
+                n_active=na, x_perm=xp, active=act)
+
+
+@pytest.mark.parametrize("T,E,k,mode", [(1, 8, 2, 0), (4, 8, 2, 0), (16, 8, 2, 0), (64, 8, 2, 0),
+                                        (32, 128, 8, 1), (64, 128, 8, 1), (3, 16, 4, 0)])
+def test_fused_route_matches_separate_kernels(T, E, k, mode):
+    """hn_moe_route (one launch) = router logits + top-k + permute + gather,
+    bit for bit (indices, weights, logits, permutation, gathered rows)."""
+    from hydranet_amd.model.moe import moe_route
+    H = 4096
+    g = torch.Generator().manual_seed(T * 100 + E)
+    h = (torch.randn(T, H, generator=g)).half().to(DEV)
+    if mode == 0:
+        gw = (torch.randn(E, H, generator=g) * 0.02).half().to(DEV)
+        r = moe_route(h, k, 0, gate_w=gw)
+        # logits: the fp16 rounding of an fp32 dot product in another summation
+        # order (MFMA tiles) -> within one fp16 ulp of the separate kernel's
+        sep = _separate_route(h, gw, k, 0)["logits"]
+        ulp = torch.pow(2.0, torch.floor(torch.log2(sep.abs().clamp_min(2.0 ** -14))) - 10)
+        assert bool(((r.logits - sep).abs() <= ulp).all())
+        # and vs the CPU oracle's fp32 dot products rounded to fp16
+        ref_lg = torch.from_numpy(oracle.router_logits(h.cpu().numpy(), gw.cpu().numpy()))
+        assert bool(((r.logits.cpu() - ref_lg).abs() <= ulp.cpu()).all())
+        # top-k, permutation and gather bit for bit from the fused logits
+        ref = _separate_route(h, gw, k, 0, logits=r.logits)
+    else:
+        gw = (torch.randn(E, H, generator=g) * 0.02).float().to(DEV)
+        bias = (torch.rand(E, generator=g) * 0.1).to(DEV)
+        from hydranet_amd.model.router import router_logits
+        logits = router_logits(h, gw)
+        r = moe_route(h, k, 1, logits=logits, bias=bias, scaling=2.5)
+        ref = _separate_route(h, gw, k, 1, bias=bias, scaling=2.5, logits=logits)
+    n = T * k
+    na = int(ref["n_active"].item())
+    assert int(r.n_active.item()) == na
+    assert torch.equal(r.idx, ref["idx"]) and torch.equal(r.w, ref["w"])
+    assert torch.equal(r.offsets, ref["offsets"])
+    assert torch.equal(r.active[:na], ref["active"][:na])
+    assert torch.equal(r.perm[:n], ref["perm"]) and torch.equal(r.inv[:n], ref["inv"])
+    assert torch.equal(r.x_perm[:n], ref["x_perm"])
+
+
+def test_fused_route_layer_matches_separate_path(mixtral_experts):
+    """MixtralMoELayer through the fused routing equals moe_experts_forward
+    (separate permute / gather / unpermute kernels) on the same routing, bit
+    for bit."""
+    from hydranet_amd.model.moe import MixtralMoELayer, moe_experts_forward
+    from hydranet_amd.model.router import mixtral_route
+    slots, _ = mixtral_experts
+    layer = MixtralMoELayer(4096, 8, 2, slots=slots).to(DEV)
+    layer.router.gate.weight.data = (torch.randn(8, 4096, generator=torch.Generator()
+                                                 .manual_seed(3)) * 0.02).half().to(DEV)
+    from hydranet_amd.model.moe import moe_route
+    for T in (1, 5, 16):
+        x = torch.randn(1, T, 4096, generator=torch.Generator().manual_seed(T)).half().to(DEV)
+        got = layer(x)
+        r = moe_route(x.view(T, 4096), 2, 0, gate_w=layer.router.gate.weight)
+        ref = moe_experts_forward(x.view(T, 4096), r.idx, r.w, layer.experts.table)
+        assert torch.equal(got.view(T, 4096), ref), T
