@@ -39,6 +39,8 @@ SIGNATURES: dict[str, list] = {
     "hn_grouped_expert_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, P, P, P],
     "hn_moe_route": [P, L, P, L, I, P, P, L, L, L, L, I, F, F, P, P, P, P, P, P, P, P, P, L,
                      P],
+    "hn_moe_experts_decode": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, P, P, L, L, P, L, P, L,
+                              P, L, P],
 }
 
 # Sizes up to which hn_moe_route (one launch: logits, top-k, permutation,

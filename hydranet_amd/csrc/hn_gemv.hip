@@ -560,7 +560,12 @@ extern "C" long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long
   const Plan pd = make_plan(r, (int)I, 1);
   const size_t a = part_bytes(pg.ks, 2, prow, I);
   const size_t b = part_bytes(pd.ks, 1, prow, H);
-  return (long)(ctr_bytes(ctr) + (a > b ? a : b));
+  size_t m = a > b ? a : b;
+  if (kind == 3) {  // hn_moe_experts_decode: 4 fp32 K-slice partials of the down projection
+    const size_t c = (size_t)4 * prow * H * 4;
+    m = m > c ? m : c;
+  }
+  return (long)(ctr_bytes(ctr) + m);
 }
 
 // Persistent streaming kernels (hn_stream.hip): return HN_NOT_HANDLED when a
@@ -573,6 +578,18 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
                                       const int* active, const int* n_active, const int* offsets,
                                       long E, long max_rows, long H, long I, long group, void* out,
                                       long ld_o, void* stream, int dry_run);
+extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const int* active,
+                                         const int* n_active, const int* offsets, long E,
+                                         long max_rows, long rows_cap, long H, long I,
+                                         long group, float* part, void* stream, int dry_run);
+extern "C" int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* idx,
+                                const void* w, long T, long k, const void* shared, long ld_sh,
+                                void* out, long ld_o, long H, void* stream);
+// Unpermute (hn_route.hip) from the four fp32 slices of the split down projection.
+extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, const int* inv,
+                                            const int* idx, const void* w, long T, long k,
+                                            const void* shared, long ld_sh, void* out,
+                                            long ld_o, long H, void* stream);
 
 // Prefill GEMM kernels (hn_gemm.hip): same return convention.
 extern "C" int hn_gemm_linear_impl(int mats, const void* x, long ld_x, const void* q0,
@@ -841,5 +858,55 @@ extern "C" int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const
     hn_set_error("%s: shape not handled by the GEMM kernels (group=%ld)", who, group);
     return -22;
   }
+  return rc;
+}
+
+// The experts half of a decode MoE layer: grouped SwiGLU over the routed rows
+// and the ordered, weighted sum back per token.  Where the streaming kernels
+// apply, the down projection runs in four K slices whose fp32 partials (in
+// the workspace) the unpermute sums in slice order; otherwise this is
+// hn_grouped_expert_mlp_int4 into y_ws followed by hn_moe_unpermute.
+extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, const int* active,
+                                     const int* n_active, const int* offsets, long E,
+                                     long max_rows_per_expert, long rows, long H, long I,
+                                     long group, void* h_ws, void* y_ws, const int* inv,
+                                     const int* idx, const void* w, long T, long k,
+                                     const void* shared, long ld_sh, void* out, long ld_o,
+                                     void* work, long work_bytes, void* stream) {
+  const char* who = "hn_moe_experts_decode";
+  HN_ARG_CHECK(E > 0 && E <= 256 && max_rows_per_expert >= 0 && rows >= 0 && T >= 0 && k > 0,
+               "%s: bad sizes", who);
+  HN_ARG_CHECK(aligned16(out) && ld_o % 8 == 0 && H % 8 == 0, "%s: out rows must be 16-byte "
+               "aligned", who);
+  hipStream_t s = (hipStream_t)stream;
+  const bool premul = (group % 128) != 0;
+  if (rows > 0 && max_rows_per_expert > 0 && max_rows_per_expert <= kStreamMaxRows &&
+      g_decode_path == 0 && !premul && H % 128 == 0 && I % 128 == 0 && aligned16(x_perm) &&
+      aligned16(h_ws) &&
+      hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
+                             max_rows_per_expert, H, I, group, h_ws, I, s, 1) == 0 &&
+      hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, max_rows_per_expert,
+                                rows, H, I, group, nullptr, s, 1) == 0) {
+    const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
+                                                              : hn_cdiv(H, kTileN);
+    const long need = hn_skinny_workspace_bytes(3, rows, H, I, E);
+    HN_ARG_CHECK(work && work_bytes >= need, "%s: workspace too small (%ld < %ld)", who,
+                 work_bytes, need);
+    float* part = (float*)((char*)work + ctr_bytes(E * tmax));
+    int rc = hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
+                                    max_rows_per_expert, H, I, group, h_ws, I, s, 0);
+    if (rc == 0)
+      rc = hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E,
+                                     max_rows_per_expert, rows, H, I, group, part, s, 0);
+    if (rc == 0)
+      rc = hn_moe_unpermute_split4_impl(part, rows * H, inv, idx, w, T, k, shared, ld_sh, out,
+                                        ld_o, H, stream);
+    return rc;
+  }
+  int rc = hn_grouped_expert_mlp_int4(x_perm, table, active, n_active, offsets, E,
+                                      max_rows_per_expert, rows, H, I, group, h_ws, y_ws, work,
+                                      work_bytes, stream);
+  if (rc == 0)
+    rc = hn_moe_unpermute(y_ws, H, inv, idx, w, T, k, shared, ld_sh, out, ld_o, H, stream);
   return rc;
 }

@@ -317,11 +317,16 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const h16* __restrict__
     *reinterpret_cast<half8_t*>(dst + c) = *reinterpret_cast<const half8_t*>(src + c);
 }
 
-// One workgroup per token; each thread owns 8 consecutive columns.
+// One workgroup per token; each thread owns 8 consecutive columns.  KS = 0:
+// y is fp16 [rows, ld_y]; KS > 0: y is given as KS fp32 partial sums
+// part[j * ks_stride + row * ld_y] (a K-split down projection), added in
+// slice order and rounded to fp16 once: the expert output the unsplit kernel
+// would write, up to fp32 summation order.
+template <int KS>
 __global__ __launch_bounds__(256) void moe_unpermute_kernel(
-    const h16* __restrict__ y, long ld_y, const int* __restrict__ inv,
-    const int* __restrict__ idx, const h16* __restrict__ w, int k, const h16* __restrict__ shared,
-    long ld_sh, h16* __restrict__ out, long ld_o, int H) {
+    const h16* __restrict__ y, const float* __restrict__ part, long ks_stride, long ld_y,
+    const int* __restrict__ inv, const int* __restrict__ idx, const h16* __restrict__ w, int k,
+    const h16* __restrict__ shared, long ld_sh, h16* __restrict__ out, long ld_o, int H) {
   const int t = blockIdx.x;
   int pos[kMaxTopK];
   int ex[kMaxTopK];
@@ -349,7 +354,27 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
   for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
     half8_t acc = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int s = 0; s < n; ++s) {
-      const half8_t v = *reinterpret_cast<const half8_t*>(y + (long)pos[s] * ld_y + c);
+      half8_t v;
+      if constexpr (KS == 0) {
+        v = *reinterpret_cast<const half8_t*>(y + (long)pos[s] * ld_y + c);
+      } else {
+        float f[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) f[q] = 0.f;
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+          const float* pp = part + j * ks_stride + (long)pos[s] * ld_y + c;
+          const float4_t a = *reinterpret_cast<const float4_t*>(pp);
+          const float4_t b = *reinterpret_cast<const float4_t*>(pp + 4);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            f[q] += a[q];
+            f[4 + q] += b[q];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = (h16)f[q];
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const h16 prod = (h16)((float)v[j] * wt[s]);
@@ -640,9 +665,10 @@ extern "C" int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, c
                    (!shared || (al16(shared) && ld_sh % 8 == 0)),
                "hn_moe_unpermute: rows must be 16-byte aligned");
   if (T <= 0) return 0;
-  hipLaunchKernelGGL(moe_unpermute_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
-                     (const h16*)y_perm, ld_y, inv, idx, (const h16*)w, (int)k,
-                     (const h16*)shared, ld_sh, (h16*)out, ld_o, (int)H);
+  hipLaunchKernelGGL(moe_unpermute_kernel<0>, dim3((unsigned)T), dim3(256), 0,
+                     (hipStream_t)stream, (const h16*)y_perm, (const float*)nullptr, 0L, ld_y,
+                     inv, idx, (const h16*)w, (int)k, (const h16*)shared, ld_sh, (h16*)out, ld_o,
+                     (int)H);
   HN_LAUNCH_CHECK("hn_moe_unpermute");
   return 0;
 }
@@ -691,5 +717,23 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
   }
 #undef HN_ROUTE_LAUNCH
   HN_LAUNCH_CHECK(who);
+  return 0;
+}
+
+// Unpermute from 4 fp32 K-slice partials of the down projection
+// (hn_stream_down_split_impl): part[j * ks_stride + row * H], j < 4.
+extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, const int* inv,
+                                            const int* idx, const void* w, long T, long k,
+                                            const void* shared, long ld_sh, void* out,
+                                            long ld_o, long H, void* stream) {
+  HN_ARG_CHECK(k > 0 && k <= kMaxTopK, "hn_moe_unpermute: k must be in (0, %d]", kMaxTopK);
+  HN_ARG_CHECK(H % 8 == 0 && al16(part) && al16(out) && ks_stride % 4 == 0 && ld_o % 8 == 0 &&
+                   (!shared || (al16(shared) && ld_sh % 8 == 0)),
+               "hn_moe_unpermute: rows must be 16-byte aligned");
+  if (T <= 0) return 0;
+  hipLaunchKernelGGL(moe_unpermute_kernel<4>, dim3((unsigned)T), dim3(256), 0,
+                     (hipStream_t)stream, (const h16*)nullptr, part, ks_stride, H, inv, idx,
+                     (const h16*)w, (int)k, (const h16*)shared, ld_sh, (h16*)out, ld_o, (int)H);
+  HN_LAUNCH_CHECK("hn_moe_unpermute");
   return 0;
 }

@@ -73,6 +73,10 @@ struct StreamArgs {
   int ldx;    // LDS row stride of the staged activations (halves)
   int npair;  // group pairs per staged row (KW * LPW / 2)
   uint32_t m_lo, m_hi, magic;
+  // K split (KS > 1, down phase only): K above is one slice; slice j of
+  // row r goes to out32[j * ks_stride + r * N + n] in fp32
+  float* out32;
+  long ks_stride;
 };
 
 // Weights and scales of one column for one wave.  Scales: with WIDE, dword
@@ -87,6 +91,7 @@ struct WBuf {
 struct Problem {
   const h16* x;
   h16* out;
+  int t0;    // first row of this problem in the launch
   int rows;  // tokens of this problem
   const uint8_t* q[2];
   const h16* s[2];
@@ -108,12 +113,14 @@ __device__ __forceinline__ Problem resolve(const StreamArgs& A, const Meta& mt, 
   if (!GROUPED) {
     p.x = A.x;
     p.out = A.out;
+    p.t0 = 0;
     p.rows = A.M;
     p.q[0] = A.q[0]; p.s[0] = A.s[0];
     p.q[1] = A.q[1]; p.s[1] = A.s[1];
   } else {
     const int e = mt.active[a];
     const int t0 = mt.offsets[e];
+    p.t0 = t0;
     p.rows = mt.offsets[e + 1] - t0;
     const SExpert& ew = mt.table[e];
     if (A.phase == 0) {
@@ -370,7 +377,12 @@ __device__ __forceinline__ void locate(Cursor& cu, const int* chunk_off, int npr
 
 // At most 8 waves per workgroup and one workgroup per CU: 2 waves per SIMD,
 // 256 VGPRs each.
-template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE>
+// KS > 1: the columns of a chunk are (k slice, tile), the slices one after
+// the other, so that a workgroup's contiguous range mostly stays on one
+// slice (one staging); each column's wave-reduced partial is written in fp32
+// and the caller sums the KS slices in order.  A slice keeps the workgroup's
+// activations and the pipeline short where K is long (the down projection).
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS>
 __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
                                                      const SExpert* __restrict__ table,
                                                      const int* __restrict__ active,
@@ -389,7 +401,8 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
   const int q = lane >> 4;
   const int N = A.N, TC = A.tc;
   const int G = A.K >> 7;
-  const int tiles = (N + kTileN - 1) / kTileN;
+  const int tiles_n = (N + kTileN - 1) / kTileN;
+  const int tiles = tiles_n * KS;              // columns per chunk
   const int g0 = wave * LPW;                   // this wave's first group
   const int gw = max(0, min(LPW, G - g0));     // its groups (uniform)
   const int pb0 = g0 >> 1;                     // its first group pair
@@ -437,6 +450,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
   int pi_last;        // problem of the last issued column
   Problem pi_pr;      // its weights
   int st_p, st_ch;    // staged (problem, chunk)
+  int st_kj = 0;      // and k slice
   Problem st_pr;      // its activations / output
   StageGeom sg;
   int ci = cb;        // next column to issue
@@ -453,7 +467,8 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
         pi_last = p;
       }
     }
-    issue<MATS, PAIRS, WIDE>(b, pi_pr, A, t, g0, more, col, q);
+    const int kj = KS > 1 ? t / tiles_n : 0;
+    issue<MATS, PAIRS, WIDE>(b, pi_pr, A, t - kj * tiles_n, g0 + kj * G, more, col, q);
     ++ci;
   };
   auto geom = [&](int ch) {
@@ -473,17 +488,19 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     locate(cu_c, chunk_off, nprob, tiles, cb, p, ch, t);
     st_p = p;
     st_ch = ch;
+    if constexpr (KS > 1) st_kj = t / tiles_n;
     st_pr = resolve<GROUPED>(A, meta, p);
     pi_pr = st_pr;
     pi_last = p;
     sg = geom(ch);
+    const h16* xsl = st_pr.x + st_kj * A.K;
     half8_t v[4];
-    stage_load(A, st_pr.x, sg, 0, v);
+    stage_load(A, xsl, sg, 0, v);
     issue_next(b0);
     if (NBUF == 3) issue_next(b1);
     stage_store(A, sg, 0, v, xs);
     for (int base = 4 * (int)blockDim.x; base < sg.nblk; base += 4 * blockDim.x) {
-      stage_load(A, st_pr.x, sg, base, v);
+      stage_load(A, xsl, sg, base, v);
       stage_store(A, sg, base, v, xs);
     }
     __syncthreads();
@@ -499,12 +516,14 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     if (c < ce) {  // uniform
       int p, ch;
       locate(cu_c, chunk_off, nprob, tiles, c, p, ch, t);
-      if (p != st_p || ch != st_ch) {
+      const int kj = KS > 1 ? t / tiles_n : 0;
+      if (p != st_p || ch != st_ch || kj != st_kj) {
         if (p != st_p) st_pr = resolve<GROUPED>(A, meta, p);
         st_p = p;
         st_ch = ch;
+        st_kj = kj;
         sg = geom(ch);
-        stage(A, st_pr.x, sg, xs, cs);
+        stage(A, st_pr.x + st_kj * A.K, sg, xs, cs);
       }
     }
     issue_next(nxt);
@@ -546,8 +565,18 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
             v[mt].x += o[w2][mt].x;
             v[mt].y += o[w2][mt].y;
           }
-        const int row = t * kTileN + col;
-        if (row < N) {
+        const int row = (t - st_kj * tiles_n) * kTileN + col;
+        if (KS > 1) {
+          if (row < N) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const int m = 2 * q + j;
+              if (m < Mc)
+                A.out32[st_kj * A.ks_stride + (long)(st_pr.t0 + sg.m0 + m) * N + row] =
+                    j ? v[0].y : v[0].x;
+            }
+          }
+        } else if (row < N) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             const int m = 2 * q + j;
@@ -647,9 +676,9 @@ int num_cus() {
   return n;
 }
 
-template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE>
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS = 1>
 int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
-  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE>;
+  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS>;
   static int attr = -1;  // per instantiation
   if (attr < 0) {
     attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -683,6 +712,10 @@ int launch_stream(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p
   return p.wide ? launch_lpw<GROUPED, MATS, EPI, true>(A, g, p, s)
                 : launch_lpw<GROUPED, MATS, EPI, false>(A, g, p, s);
 }
+
+// Down projection in kDownSplit K slices: one slice of I = 14336 is 28
+// groups, 7 waves x 4 groups with three column buffers.
+constexpr int kDownSplit = 4;
 
 // Vector scale loads need the wave's LPW groups inside the scale row and
 // 16-byte aligned scale rows.
@@ -741,7 +774,7 @@ extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const v
 
 // Streaming decode, grouped over the active experts of one MoE layer; phase 0
 // is gate/up + SiLU into h, phase 1 the down projection.  dry_run: only say
-// whether the shape is handled (0) or not (1).
+// whether the shape is handled (0) or not (HN_NOT_HANDLED).
 extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const void* table,
                                       const int* active, const int* n_active, const int* offsets,
                                       long E, long max_rows, long H, long I, long group, void* out,
@@ -771,5 +804,38 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
                            : launch_stream<true, 1, 0>(A, g, pw, s);
   if (rc) return rc;
   HN_LAUNCH_CHECK("hn_stream_grouped");
+  return 0;
+}
+
+// Down projection of the grouped decode in kDownSplit K slices: fp32 partials
+// part[j][row][H] (j < kDownSplit, ks_stride = rows_cap * H floats), summed
+// in slice order by the caller.  Returns HN_NOT_HANDLED when the shape does
+// not split (then the caller runs hn_stream_grouped_impl's phase 1).
+extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const int* active,
+                                         const int* n_active, const int* offsets, long E,
+                                         long max_rows, long rows_cap, long H, long I,
+                                         long group, float* part, void* stream,
+                                         int dry_run) {
+  const long K = I / kDownSplit, N = H;
+  if (I % (kDownSplit * 128) != 0 || group != 128 || E > kMaxActive) return HN_NOT_HANDLED;
+  const StreamPlan p = stream_plan(K, 1, max_rows);
+  if (!p.ok || p.lpw != 4 || !wide_scales_ok(p, K, I / group)) return HN_NOT_HANDLED;
+  if (N * (I / 2) >= (long)kOOB || N * (I / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
+  if (dry_run) return 0;
+  StreamArgs A = {};
+  A.x = (const h16*)h;
+  A.ld_x = (int)I;
+  A.phase = 1;
+  A.ld_q = (int)(I / 2);
+  A.ld_s = (int)(I / group);
+  A.out32 = part;
+  A.ks_stride = rows_cap * H;
+  fill_common(A, p, N, K);
+  StreamPlan pw = p;
+  pw.wide = true;
+  const GroupedPtrs g = {(const SExpert*)table, active, n_active, offsets};
+  const int rc = launch_one<true, 1, 0, 4, 3, true, kDownSplit>(A, g, pw, (hipStream_t)stream);
+  if (rc) return rc;
+  HN_LAUNCH_CHECK("hn_stream_down_split");
   return 0;
 }

@@ -139,15 +139,24 @@ def moe_dispatch(r: Routed, table: ExpertTable,
     n = T * k
     h_ws = torch.empty((max(n, 1), I), dtype=torch.float16, device=dev)
     y_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
-    work = _lib.skinny_workspace(3, n, H, I, E, dev) if T <= _lib.DECODE_MAX_ROWS else None
+    sh = None
+    if shared is not None:
+        sh = _lib.aligned_rows(shared.reshape(T, H).to(torch.float16))
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    if T <= _lib.DECODE_MAX_ROWS:
+        # decode: both expert phases and the unpermute (split down projection)
+        work = _lib.skinny_workspace(3, n, H, I, E, dev)
+        _lib.call("hn_moe_experts_decode", _lib.ptr(r.x_perm), _lib.ptr(table.dev),
+                  _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I,
+                  g, _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(r.inv), _lib.ptr(r.idx),
+                  _lib.ptr(r.w), T, k, _lib.ptr(sh), H if sh is None else sh.stride(0),
+                  _lib.ptr(out), H, _lib.ptr(work), work.numel(), st)
+        return out
+    work = None
     _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(r.x_perm), _lib.ptr(table.dev),
               _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I, g,
               _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work),
               0 if work is None else work.numel(), st)
-    out = torch.empty((T, H), dtype=torch.float16, device=dev)
-    sh = None
-    if shared is not None:
-        sh = _lib.aligned_rows(shared.reshape(T, H).to(torch.float16))
     _lib.call("hn_moe_unpermute", _lib.ptr(y_perm), H, _lib.ptr(r.inv), _lib.ptr(r.idx),
               _lib.ptr(r.w), T, k, _lib.ptr(sh), H if sh is None else sh.stride(0), _lib.ptr(out),
               H, H, st)

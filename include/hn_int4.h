@@ -141,6 +141,21 @@ int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int*
                                void* h_ws, void* y_perm, void* work, long work_bytes,
                                void* stream);
 
+/* The experts half of a MoE layer at decode: hn_grouped_expert_mlp_int4 plus
+ * hn_moe_unpermute (same arguments; inv / idx / w / shared as for
+ * hn_moe_unpermute, out [T, H]).  Where the streaming kernels apply, the down
+ * projection runs in four K slices whose fp32 partials (kept in work) the
+ * unpermute adds in slice order before the fp16 rounding; y_ws [rows, H] fp16
+ * is then unused.  work: hn_skinny_workspace_bytes(3, rows, H, I, E).
+ * Replaces the per-expert loop and index_add_ of MixtralMoELayer.forward
+ * (model/mixtral.py:327-368) / GLM4MoELayer.forward (model/glm4.py:421-473). */
+int hn_moe_experts_decode(const void* x_perm, const void* table, const int* active,
+                          const int* n_active, const int* offsets, long E,
+                          long max_rows_per_expert, long rows, long H, long I, long group,
+                          void* h_ws, void* y_ws, const int* inv, const int* idx, const void* w,
+                          long T, long k, const void* shared, long ld_sh, void* out, long ld_o,
+                          void* work, long work_bytes, void* stream);
+
 /* One phase of hn_grouped_expert_mlp_int4's prefill path (the grouped MFMA GEMM):
  * phase 0 writes h_ws [rows, I] = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T)) per expert,
  * phase 1 writes y_perm [rows, H] = fp16(h_ws Wd^T) per expert.  Any rows per
