@@ -65,6 +65,7 @@ struct StreamArgs {
   const h16* s[2];
   h16* out; int ld_o;
   int phase;  // grouped: 0 gate/up + SiLU (N = I, K = H); 1 down (N = H, K = I)
+  int E;      // grouped: experts in the table
   // shape, shared by every problem of the launch
   int N, K;
   int ld_q;   // packed row stride (bytes)
@@ -97,15 +98,21 @@ struct Problem {
   const h16* s[2];
 };
 
-// Grouped-launch metadata.  The kernel takes these as separate __restrict__
-// arguments: it never writes them, which lets the compiler read them with
-// scalar loads (a vector load here would make the next wait on the weight
-// loads count it, in order, behind them).
+// Grouped-launch metadata: the active list, the row offsets and this
+// phase's four weight pointers per expert, copied into LDS at the start in
+// one round of independent loads (reading them on demand costs a chain of
+// dependent memory round trips before the first weight load can go out).
 struct Meta {
-  const SExpert* __restrict__ table;
-  const int* __restrict__ active;
-  const int* __restrict__ offsets;
+  const int* s_act;       // [E]
+  const int* s_off;       // [E + 1]
+  const uint64_t* s_ptr;  // [E][4]: q0, s0, q1, s1
 };
+
+__device__ __forceinline__ const void* rfl_ptr(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(((uint64_t)hi << 32) | lo);
+}
 
 template <bool GROUPED>
 __device__ __forceinline__ Problem resolve(const StreamArgs& A, const Meta& mt, int a) {
@@ -118,18 +125,14 @@ __device__ __forceinline__ Problem resolve(const StreamArgs& A, const Meta& mt, 
     p.q[0] = A.q[0]; p.s[0] = A.s[0];
     p.q[1] = A.q[1]; p.s[1] = A.s[1];
   } else {
-    const int e = mt.active[a];
-    const int t0 = mt.offsets[e];
+    const int e = __builtin_amdgcn_readfirstlane(mt.s_act[a]);
+    const int t0 = __builtin_amdgcn_readfirstlane(mt.s_off[e]);
     p.t0 = t0;
-    p.rows = mt.offsets[e + 1] - t0;
-    const SExpert& ew = mt.table[e];
-    if (A.phase == 0) {
-      p.q[0] = ew.gate_q; p.s[0] = ew.gate_s;
-      p.q[1] = ew.up_q;   p.s[1] = ew.up_s;
-    } else {
-      p.q[0] = ew.down_q; p.s[0] = ew.down_s;
-      p.q[1] = ew.down_q; p.s[1] = ew.down_s;
-    }
+    p.rows = __builtin_amdgcn_readfirstlane(mt.s_off[e + 1]) - t0;
+    p.q[0] = (const uint8_t*)rfl_ptr(mt.s_ptr[4 * e + 0]);
+    p.s[0] = (const h16*)rfl_ptr(mt.s_ptr[4 * e + 1]);
+    p.q[1] = (const uint8_t*)rfl_ptr(mt.s_ptr[4 * e + 2]);
+    p.s[1] = (const h16*)rfl_ptr(mt.s_ptr[4 * e + 3]);
     p.x = A.x + (long)t0 * A.ld_x;
     p.out = A.out + (long)t0 * A.ld_o;
   }
@@ -390,8 +393,8 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
                                                      const int* __restrict__ offsets) {
   constexpr int PAIRS = LPW / 2;
   static_assert(NBUF == 2 || NBUF == 3, "two or three column buffers");
-  const Meta meta = {table, active, offsets};
   extern __shared__ __align__(16) unsigned char smem[];
+  Meta meta = {nullptr, nullptr, nullptr};
   __shared__ int chunk_off[kMaxActive + 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -418,16 +421,50 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
   // ---- token chunks per problem -> prefix (chunk_off); columns = chunks * tiles
   int nprob = 1;
   if (GROUPED) {
-    nprob = min(*n_active, kMaxActive);
+    // one round of independent loads: active list, offsets, weight pointers
+    const int E = A.E;
+    int* s_act = reinterpret_cast<int*>(red + 2 * kRedSlots);
+    int* s_off = s_act + ((E + 1) & ~1);
+    uint64_t* s_ptr = reinterpret_cast<uint64_t*>(s_off + ((E + 2) & ~1));
+    const int na = *n_active;
+    const uint64_t* tw = reinterpret_cast<const uint64_t*>(table);
+    for (int i = tid; i < E; i += blockDim.x) s_act[i] = active[i];
+    for (int i = tid; i <= E; i += blockDim.x) s_off[i] = offsets[i];
+    for (int i = tid; i < 4 * E; i += blockDim.x) {
+      const int e = i >> 2, j = i & 3;
+      const int f = A.phase == 0 ? j : 4 + (j & 1);  // gate_q gate_s up_q up_s | down_q down_s
+      s_ptr[i] = tw[6 * e + f];
+    }
+    meta = {s_act, s_off, s_ptr};
+    nprob = min(na, min(E, kMaxActive));
+    __syncthreads();
     for (int i = tid; i < nprob; i += blockDim.x) {
-      const int e = active[i];
-      const int rows = offsets[e + 1] - offsets[e];
-      chunk_off[i + 1] = (rows + TC - 1) / TC;
+      const int e = s_act[i];
+      chunk_off[i + 1] = (s_off[e + 1] - s_off[e] + TC - 1) / TC;
     }
     __syncthreads();
-    if (tid == 0) {
-      chunk_off[0] = 0;
-      for (int i = 1; i <= nprob; ++i) chunk_off[i] += chunk_off[i - 1];
+    if (tid < 64) {  // prefix over <= 256 entries: 4 per lane, then a wave scan
+      int v[4], sum = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * tid + j;
+        v[j] = i < nprob ? chunk_off[i + 1] : 0;
+        sum += v[j];
+      }
+      int incl = sum;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (tid >= off) incl += o;
+      }
+      int run = incl - sum;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 4 * tid + j;
+        run += v[j];
+        if (i < nprob) chunk_off[i + 1] = run;
+      }
+      if (tid == 0) chunk_off[0] = 0;
     }
   } else if (tid == 0) {
     chunk_off[0] = 0;
@@ -638,7 +675,7 @@ struct StreamPlan {
 // per column, the smallest that covers K with 8 waves; three column buffers
 // when they fit the register budget, else two.  tc <= 8 tokens per chunk,
 // limited by the LDS left after the corrections and the reduction buffers.
-StreamPlan stream_plan(long K, int mats, long rows) {
+StreamPlan stream_plan(long K, int mats, long rows, long E = 0) {
   StreamPlan p{};
   const long G = K / 128;
   int lpw = 2;
@@ -654,10 +691,12 @@ StreamPlan stream_plan(long K, int mats, long rows) {
   const int cs = p.npair * 16 * 4;
   const int per_tok = 2 * p.ldx * 2;
   const int want = (int)(rows < kMaxTc ? rows : kMaxTc);
-  const int tcmax = (kLdsPerCu - kStaticLds - red - cs) / per_tok;
+  // grouped metadata copy: active [E], offsets [E + 1] (each padded to even), pointers [E][4]
+  const int meta = (int)(((E + 1) & ~1L) * 4 + ((E + 2) & ~1L) * 4 + E * 32);
+  const int tcmax = (kLdsPerCu - kStaticLds - red - cs - meta) / per_tok;
   p.tc = tcmax < want ? tcmax : want;
   if (p.tc < 1) return p;
-  p.lds = p.tc * per_tok + cs + red;
+  p.lds = p.tc * per_tok + cs + red + meta;
   p.ok = true;
   return p;
 }
@@ -781,8 +820,9 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
                                       long ld_o, void* stream, int dry_run) {
   const int mats = phase == 0 ? 2 : 1;
   const long K = phase == 0 ? H : I, N = phase == 0 ? I : H;
-  const StreamPlan p = stream_plan(K, mats, max_rows);
-  if (!p.ok || group != 128 || E > kMaxActive) return HN_NOT_HANDLED;
+  if (E > kMaxActive) return HN_NOT_HANDLED;
+  const StreamPlan p = stream_plan(K, mats, max_rows, E);
+  if (!p.ok || group != 128) return HN_NOT_HANDLED;
   if (mats == 2 && p.lpw > 8) return HN_NOT_HANDLED;
   if (N * (K / 2) >= (long)kOOB || N * (K / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
   if (dry_run) return 0;
@@ -793,6 +833,7 @@ extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const
   A.x = (const h16*)x;
   A.ld_x = (int)ld_x;
   A.phase = phase;
+  A.E = (int)E;
   A.ld_q = (int)(K / 2);
   A.ld_s = (int)(K / group);
   A.out = (h16*)out;
@@ -818,7 +859,7 @@ extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const
                                          int dry_run) {
   const long K = I / kDownSplit, N = H;
   if (I % (kDownSplit * 128) != 0 || group != 128 || E > kMaxActive) return HN_NOT_HANDLED;
-  const StreamPlan p = stream_plan(K, 1, max_rows);
+  const StreamPlan p = stream_plan(K, 1, max_rows, E);
   if (!p.ok || p.lpw != 4 || !wide_scales_ok(p, K, I / group)) return HN_NOT_HANDLED;
   if (N * (I / 2) >= (long)kOOB || N * (I / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
   if (dry_run) return 0;
@@ -826,6 +867,7 @@ extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const
   A.x = (const h16*)h;
   A.ld_x = (int)I;
   A.phase = 1;
+  A.E = (int)E;
   A.ld_q = (int)(I / 2);
   A.ld_s = (int)(I / group);
   A.out32 = part;
