@@ -93,23 +93,24 @@ __device__ __forceinline__ bool topk_beats(float bv, int be, float av, int ae) {
 }
 
 // Routing weights of the k selected experts sel[0..k) (already written) from
-// the token's raw logits l: mode 0 softmax over the selected logits (exp in
-// double, one rounding to fp32 per element) and renormalisation by the fp32
-// sum (model/router.py:114-117); mode 1 sigmoid, / (sum + eps) * scaling
+// the token's raw logits l: mode 0 fp32 softmax over the selected logits and
+// renormalisation by the fp32 sum (model/router.py:114-117); mode 1 sigmoid
+// (exp in double, rounded once: it also ranks the experts), / (sum + eps) * scaling
 // (model/glm4.py:282-307).  Compact loops: each element's value is recomputed
 // where it is needed (same arithmetic each time) instead of kept in arrays.
 __device__ __noinline__ void topk_weights(const float* l, const int* sel, int k, int mode,
                                           float eps, float scaling, h16* w_o) {
   if (mode == 0) {
-    const double mx = (double)l[sel[0]];
-    double z = 0.0;
+    // fp32 softmax as F.softmax(topk_logits.float()) (exp of x - max)
+    const float mx = l[sel[0]];
+    float z = 0.f;
 #pragma unroll 1
-    for (int i = 0; i < k; ++i) z += exp((double)l[sel[i]] - mx);
+    for (int i = 0; i < k; ++i) z += expf(l[sel[i]] - mx);
     float s = 0.f;
 #pragma unroll 1
-    for (int i = 0; i < k; ++i) s += (float)(exp((double)l[sel[i]] - mx) / z);
+    for (int i = 0; i < k; ++i) s += expf(l[sel[i]] - mx) / z;
 #pragma unroll 1
-    for (int i = 0; i < k; ++i) w_o[i] = (h16)((float)(exp((double)l[sel[i]] - mx) / z) / s);
+    for (int i = 0; i < k; ++i) w_o[i] = (h16)((expf(l[sel[i]] - mx) / z) / s);
   } else {
     float s = 0.f;
 #pragma unroll 1

@@ -304,12 +304,19 @@ __device__ __forceinline__ void stage_load(const StreamArgs& A, const h16* x,
   }
 }
 
+// Also the bias corrections: the 16 blocks of one (token, group) sit in 16
+// consecutive lanes (block index = base + tid + j * nthr, blk_per_tok a
+// multiple of 16), so each lane's 8-term dot product is summed across its
+// 16-lane DPP row and the row's first lane writes cs[pair * 16 + 2 t + parity]
+// = -C.  Lanes whose block is a repeat of the last one (past the chunk) skip
+// the write; so does the whole row, as the chunk ends on a group boundary.
 __device__ __forceinline__ void stage_store(const StreamArgs& A, const StageGeom& sg, int base,
-                                            const half8_t v[4], h16* xs) {
+                                            const half8_t v[4], h16* xs, float* cs) {
   const int tid = threadIdx.x, nthr = blockDim.x, K = A.K;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int i = min(base + tid + j * nthr, sg.nblk - 1);
+    const int ir = base + tid + j * nthr;
+    const int i = min(ir, sg.nblk - 1);
     const int t = i / sg.blk_per_tok;
     const int b = i - t * sg.blk_per_tok;
     const int g = b >> 4;
@@ -321,27 +328,25 @@ __device__ __forceinline__ void stage_store(const StreamArgs& A, const StageGeom
       p[e] = in_k ? ((e & 2) ? s * (h16)0.0625f : s) : (h16)0.0f;
     }
     *reinterpret_cast<half8_t*>(xs + (2 * t + (g & 1)) * A.ldx + (g >> 1) * 128 + (b & 15) * 8) = p;
+    // correction: sum over k of x * bias, bias 1032 (even k) / 1152 (odd k, x / 16 stored).
+    // (fp32 fma per term: v_dot2c_f32_f16 with these operands was miscompiled here,
+    // every dot product reading the first dword)
+    float c = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c = __builtin_fmaf((float)p[e], (e & 2) ? 1152.f : 1032.f, c);
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x128, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x124, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x122, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x121, 0xf, 0xf, false));
+    if ((tid & 15) == 0 && ir < sg.nblk) cs[(g >> 1) * 16 + 2 * t + (g & 1)] = -c;
   }
 }
 
-// Bias corrections of the staged chunk: cs[pair * 16 + R] = -C for MFMA row
-// R = 2t + p (token t, group 2 * pair + p); 0 for rows past the chunk.
-__device__ __forceinline__ void stage_corrections(const StreamArgs& A, int Mc, const h16* xs,
-                                                  float* cs) {
-  const int n = A.npair * 16;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int pb = i >> 4, R = i & 15;
-    float c = 0.f;
-    if ((R >> 1) < Mc) {
-      const h16* src = xs + R * A.ldx + pb * 128;
-      for (int j = 0; j < 16; ++j) {
-        const half8_t v = *reinterpret_cast<const half8_t*>(src + 8 * j);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) c = __builtin_fmaf((float)v[e], (e & 2) ? 1152.f : 1032.f, c);
-      }
-    }
-    cs[i] = -c;
-  }
+// Corrections of MFMA rows past the chunk's tokens are zero (their outputs
+// are never stored; the rows read a clamped token).
+__device__ __forceinline__ void stage_zero_rows(const StreamArgs& A, int Mc, float* cs) {
+  for (int i = threadIdx.x; i < A.npair * 16; i += blockDim.x)
+    if (((i & 15) >> 1) >= Mc) cs[i] = 0.f;
 }
 
 // Whole staging of one chunk (used when the staged chunk changes mid-stream).
@@ -349,13 +354,12 @@ __device__ __forceinline__ void stage(const StreamArgs& A, const h16* x, const S
                                       h16* xs, float* cs) {
   const int nthr = blockDim.x;
   __syncthreads();  // the previous chunk is no longer read
+  stage_zero_rows(A, sg.Mc, cs);
   for (int base = 0; base < sg.nblk; base += 4 * nthr) {
     half8_t v[4];
     stage_load(A, x, sg, base, v);
-    stage_store(A, sg, base, v, xs);
+    stage_store(A, sg, base, v, xs, cs);
   }
-  __syncthreads();
-  stage_corrections(A, sg.Mc, xs, cs);
   __syncthreads();
 }
 
@@ -535,13 +539,12 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     stage_load(A, xsl, sg, 0, v);
     issue_next(b0);
     if (NBUF == 3) issue_next(b1);
-    stage_store(A, sg, 0, v, xs);
+    stage_zero_rows(A, sg.Mc, cs);
+    stage_store(A, sg, 0, v, xs, cs);
     for (int base = 4 * (int)blockDim.x; base < sg.nblk; base += 4 * blockDim.x) {
       stage_load(A, xsl, sg, base, v);
-      stage_store(A, sg, base, v, xs);
+      stage_store(A, sg, base, v, xs, cs);
     }
-    __syncthreads();
-    stage_corrections(A, sg.Mc, xs, cs);
     __syncthreads();
   }
 
