@@ -181,7 +181,7 @@ def bench_c1(args):
 
 
 # ----------------------------------------------------------------------------- C2
-def bench_c2(args, T: int, n_layers: int = 4):
+def bench_c2(args, T: int, n_layers: int = 4, phases: bool = False):
     """One Mixtral MoE layer at decode: router + permute + grouped SwiGLU + unpermute.
     Steps rotate over n_layers layers of 8 experts (2.9 GB for 4 layers)."""
     from hydranet_amd import _lib
@@ -229,10 +229,85 @@ def bench_c2(args, T: int, n_layers: int = 4):
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     total_bytes = sum(step_bytes[i % n_layers] for i in range(args.steps))
     gbs = total_bytes / (ms * 1e-3 * args.steps) / 1e9
-    return {"tokens": T, "ms_per_step": round(ms, 5), "GB_s": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
-            "avg_unique_experts": sum((b - E * H * 2 - 4 * T * H) // blob for b in step_bytes)
-            / n_layers, "graph": gr is not None}
+    res = {"tokens": T, "ms_per_step": round(ms, 5), "GB_s": round(gbs, 1),
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+           "avg_unique_experts": sum((b - E * H * 2 - 4 * T * H) // blob for b in step_bytes)
+           / n_layers, "graph": gr is not None}
+    if phases and args.decode_path == 0:
+        res["phases"] = time_decode_phases(layers, x.view(T, H), T, H, I, g, E)
+    return res
+
+
+def time_decode_phases(layers, x, T, H, I, g, E, reps: int = 12):
+    """The two expert phases of the decode layer timed inside the layer's own
+    sequence (routing -> gate/up -> down -> unpermute over the rotating layers,
+    the kernels of hn_moe_route / hn_grouped_decode_phase_int4 /
+    hn_moe_unpermute), an event on the launch stream before and after each
+    expert phase.  Bytes per launch: the active experts' packed weights and scales
+    plus activations in and out (phase 1 writes four fp32 K-slice partials)."""
+    from hydranet_amd import _lib
+    from hydranet_amd.model.moe import moe_route
+    k = 2
+    n = T * k
+    routes = [moe_route(x, k, 0, gate_w=l.router.gate.weight) for l in layers]
+    torch.cuda.synchronize()
+    nact = [int(r.n_active.item()) for r in routes]
+    h_ws = torch.empty(n, I, dtype=torch.float16, device="cuda")
+    out = torch.empty(T, H, dtype=torch.float16, device="cuda")
+    work = _lib.skinny_workspace(3, n, H, I, E, "cuda")
+    lay = layers[0].experts.table.slots[0].layout
+    gu = 2 * (lay.gate_packed_size + lay.gate_scales_size)
+    dn = lay.down_packed_size + lay.down_scales_size
+    xx = _lib.aligned_rows(x)
+    sp = _lib.stream()
+    part = _lib.ptr(work)  # partials start after the counter region (set by the library)
+
+    def route(li):
+        r, lw = routes[li], layers[li].router.gate.weight
+        _lib.call("hn_moe_route", _lib.ptr(xx), H, _lib.ptr(lw), H, 0, None, None, T, E, H, k, 0,
+                  1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w), _lib.ptr(r.offsets),
+                  _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active), _lib.ptr(r.n_active),
+                  _lib.ptr(r.x_perm), H, sp)
+
+    def phase(li, ph):
+        r, tb = routes[li], layers[li].experts.table
+        xin = r.x_perm if ph == 0 else h_ws
+        _lib.call("hn_grouped_decode_phase_int4", ph, _lib.ptr(xin), _lib.ptr(tb.dev),
+                  _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I, g,
+                  _lib.ptr(h_ws), _lib.ptr(work), work.numel(), sp)
+
+    def unpermute(li):
+        # stand-in for the unpermute of hn_moe_experts_decode: same kernel, fp16 y path
+        r = routes[li]
+        _lib.call("hn_moe_unpermute", _lib.ptr(h_ws), I, _lib.ptr(r.inv), _lib.ptr(r.idx),
+                  _lib.ptr(r.w), T, k, None, H, _lib.ptr(out), H, H, sp)
+
+    n_it = 4 * reps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4 * n_it)]
+    for it in range(4):  # warm-up
+        route(it % 4); phase(it % 4, 0); phase(it % 4, 1); unpermute(it % 4)
+    torch.cuda.synchronize()
+    for it in range(n_it):
+        li = it % len(layers)
+        route(li)
+        ev[4 * it].record()
+        phase(li, 0)
+        ev[4 * it + 1].record()
+        ev[4 * it + 2].record()
+        phase(li, 1)
+        ev[4 * it + 3].record()
+        unpermute(li)
+    torch.cuda.synchronize()
+    t_gu = sum(ev[4 * it].elapsed_time(ev[4 * it + 1]) for it in range(n_it)) / n_it * 1e3
+    t_dn = sum(ev[4 * it + 2].elapsed_time(ev[4 * it + 3]) for it in range(n_it)) / n_it * 1e3
+    res = {}
+    avg_act = sum(nact) / len(nact)
+    for name, us, nbytes in (("gate_up_silu", t_gu, avg_act * gu + n * H * 2 + n * I * 2),
+                             ("down_4slices", t_dn, avg_act * dn + n * I * 2 + 4 * n * H * 4)):
+        res[name] = {"avg_us": round(us, 3), "bytes_per_launch": int(nbytes),
+                     "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    res["active_experts"] = avg_act
+    return res
 
 
 # ----------------------------------------------------------------------------- C4
@@ -379,12 +454,63 @@ def cpu_baseline_c1(ctx, budget_s: float):
                                                      "ok": ok}
 
 
+def c2phase(args):
+    """Counter run: 20 launches of the C2 T=16 grouped gate/up stream kernel, then 20
+    copies of 512 MiB (the copy calibrates FETCH_SIZE / WRITE_SIZE in bytes)."""
+    from hydranet_amd import _lib
+    from hydranet_amd.model.moe import MixtralMoELayer, moe_route
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
+    H, I, g, E, T, k = 4096, 14336, 128, 8, 16, 2
+    slots = [make_expert_slot(expert_seed(0, e), H, I, g, slot_idx=e) for e in range(E)]
+    layer = MixtralMoELayer(H, E, k, slots=slots).cuda()
+    layer.router.gate.weight.data = normal_f16((E, H), 7000)
+    x = normal_f16((T, H), 1234 + T, std=1.0)
+    r = moe_route(x, k, 0, gate_w=layer.router.gate.weight)
+    torch.cuda.synchronize()
+    maxr = int((r.offsets[1:] - r.offsets[:-1]).max().item())
+    n = T * k
+    h_ws = torch.empty(n, I, dtype=torch.float16, device="cuda")
+    work = _lib.skinny_workspace(3, n, H, I, E, "cuda")
+    for _ in range(20):
+        _lib.call("hn_grouped_decode_phase_int4", 0, _lib.ptr(r.x_perm),
+                  _lib.ptr(layer.experts.table.dev), _lib.ptr(r.active), _lib.ptr(r.n_active),
+                  _lib.ptr(r.offsets), E, maxr, n, H, I, g, _lib.ptr(h_ws), _lib.ptr(work),
+                  work.numel(), _lib.stream())
+    src = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    lay = slots[0].layout
+    print(json.dumps({"workload": "c2phase", "active_experts": int(r.n_active.item()),
+                      "gate_up_bytes_per_launch": int(r.n_active.item()) * 2 * (
+                          lay.gate_packed_size + lay.gate_scales_size) + n * H * 2 + n * I * 2,
+                      "copy_bytes": src.numel() * 2}), flush=True)
+
+
+def committed_traffic():
+    """HBM bytes per launch of the roofline kernel as measured by rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel), from the committed summary."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "stream_gate_up_c2_t16_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return {"bytes": int(float(line.split(":", 1)[1])), "source": os.path.relpath(
+                    path, os.path.dirname(os.path.abspath(__file__)))}
+    except OSError:
+        return None
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c2phase"],
+                    help="c2phase: only the C2 T=16 gate/up phase kernel and a 512 MiB copy "
+                         "(the two kernels whose rocprofv3 counters give roofline.traffic)")
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -404,6 +530,9 @@ def main():
     from hydranet_amd import _lib
     _lib.call("hn_set_decode_path", args.decode_path)
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
+    if args.workload == "c2phase":
+        c2phase(args)
+        return
     if args.workload == "c4":
         c4 = bench_c4(args)
         _log("c4", c4)
@@ -423,9 +552,25 @@ def main():
     if args.workload == "c2":
         sweep = {}
         for T in (1, 4, 16):
-            sweep[f"T{T}"] = bench_c2(args, T)
+            sweep[f"T{T}"] = bench_c2(args, T, phases=(T == 16))
             _log("c2", T, sweep[f"T{T}"])
         head = sweep["T16"]
+        ph = head.pop("phases", None)
+        if ph is not None:
+            # roofline of the dominant kernel of the headline workload: the grouped
+            # gate/up + SiLU stream kernel over the active experts at T = 16
+            gu = ph["gate_up_silu"]
+            res["c1_roofline"] = res.pop("roofline")
+            res["roofline"] = {
+                "bound": "hbm", "kernel": "stream_kernel<grouped, gate+up+SiLU> (C2, T=16)",
+                "achieved": gu["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": gu["bytes_per_launch"], "avg_us": gu["avg_us"],
+                "down": ph["down_4slices"], "active_experts": ph["active_experts"]}
+            tr = committed_traffic()
+            if tr is not None:
+                res["roofline"]["traffic"] = tr["bytes"]
+                res["roofline"]["traffic_source"] = tr["source"]
         res["metric"] = METRIC
         res["value"] = head["GB_s"]
         res["ms_per_step"] = head["ms_per_step"]

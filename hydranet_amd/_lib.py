@@ -41,6 +41,7 @@ SIGNATURES: dict[str, list] = {
                      P],
     "hn_moe_experts_decode": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, P, P, L, L, P, L, P, L,
                               P, L, P],
+    "hn_grouped_decode_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, L, P, P, L, P],
 }
 
 # Sizes up to which hn_moe_route (one launch: logits, top-k, permutation,

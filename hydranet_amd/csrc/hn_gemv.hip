@@ -910,3 +910,46 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
     rc = hn_moe_unpermute(y_ws, H, inv, idx, w, T, k, shared, ld_sh, out, ld_o, H, stream);
   return rc;
 }
+
+// One phase of hn_moe_experts_decode's streaming path on its own: phase 0
+// h_ws = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T)) per expert; phase 1 the
+// down projection in four K slices into fp32 partials part[4][rows][H]
+// (work after its counter region, as hn_moe_experts_decode keeps them).
+// Returns an error when the streaming kernels do not cover the shape.
+extern "C" int hn_grouped_decode_phase_int4(int phase, const void* x, const void* table,
+                                            const int* active, const int* n_active,
+                                            const int* offsets, long E,
+                                            long max_rows_per_expert, long rows, long H, long I,
+                                            long group, void* h_ws, void* work,
+                                            long work_bytes, void* stream) {
+  const char* who = "hn_grouped_decode_phase_int4";
+  HN_ARG_CHECK(phase == 0 || phase == 1, "%s: phase must be 0 or 1", who);
+  HN_ARG_CHECK(E > 0 && E <= 256 && rows >= 0 && max_rows_per_expert >= 0,
+               "%s: bad sizes (E=%ld, rows=%ld)", who, E, rows);
+  HN_ARG_CHECK(H % 128 == 0 && I % 128 == 0 && aligned16(x) && aligned16(h_ws),
+               "%s: H, I multiples of 128 and 16-byte aligned buffers", who);
+  HN_ARG_CHECK(max_rows_per_expert <= kStreamMaxRows && group == 128,
+               "%s: the streaming kernels take <= %ld rows per expert and group 128", who,
+               kStreamMaxRows);
+  if (rows == 0 || max_rows_per_expert == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+  if (phase == 0) {
+    rc = hn_stream_grouped_impl(0, x, H, table, active, n_active, offsets, E,
+                                max_rows_per_expert, H, I, group, h_ws, I, s, 0);
+  } else {
+    const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
+                                                              : hn_cdiv(H, kTileN);
+    const long need = hn_skinny_workspace_bytes(3, rows, H, I, E);
+    HN_ARG_CHECK(work && work_bytes >= need, "%s: workspace too small (%ld < %ld)", who,
+                 work_bytes, need);
+    rc = hn_stream_down_split_impl(x, table, active, n_active, offsets, E, max_rows_per_expert,
+                                   rows, H, I, group, (float*)((char*)work + ctr_bytes(E * tmax)),
+                                   s, 0);
+  }
+  if (rc == HN_NOT_HANDLED) {
+    hn_set_error("%s: shape not handled by the streaming kernels", who);
+    return -22;
+  }
+  return rc;
+}

@@ -156,6 +156,17 @@ int hn_moe_experts_decode(const void* x_perm, const void* table, const int* acti
                           long T, long k, const void* shared, long ld_sh, void* out, long ld_o,
                           void* work, long work_bytes, void* stream);
 
+/* One phase of hn_moe_experts_decode's streaming path on its own (<= 16 rows per
+ * expert, group 128): phase 0 reads x [rows, H] (sorted by expert) and writes
+ * h_ws [rows, I]; phase 1 reads h_ws-shaped x [rows, I] and writes the four
+ * fp32 K-slice partials of the down projection into work (after its counter
+ * region, part[j][row][H]).  No separate counterpart in the reference; lets a
+ * caller time the two decode phases apart (the benchmark's roofline). */
+int hn_grouped_decode_phase_int4(int phase, const void* x, const void* table, const int* active,
+                                 const int* n_active, const int* offsets, long E,
+                                 long max_rows_per_expert, long rows, long H, long I, long group,
+                                 void* h_ws, void* work, long work_bytes, void* stream);
+
 /* One phase of hn_grouped_expert_mlp_int4's prefill path (the grouped MFMA GEMM):
  * phase 0 writes h_ws [rows, I] = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T)) per expert,
  * phase 1 writes y_perm [rows, H] = fp16(h_ws Wd^T) per expert.  Any rows per
