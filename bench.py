@@ -1,21 +1,25 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X INT4 expert-MLP hot path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c3|c4] [--tokens T]
+    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c4|c2phase] [--tokens T]
 
 Prints ONE JSON line.  A "step" is one pass of the hot path over one batch of
 synthetic input already resident in HBM:
 
+  c2  (default, the headline) one Mixtral MoE layer at decode, T = 1, 4, 16
+      (value: T = 16): route + grouped gate/up + down + unpermute
   c1  one Mixtral expert SwiGLU (H 4096, I 14336, INT4 g128), T tokens (default 1)
+  c4  one Mixtral MoE layer at prefill (2048 tokens, Zipf-skewed routing)
 
 Weights are seeded N(0, 0.02) fp16 packed to INT4 by the GPU packer.  Steps
 rotate over enough distinct experts (>= 0.7 GB) that weights stream from HBM,
 not from the 256 MB Infinity Cache.  Steps are replayed from a HIP graph.
 
-roofline: the dominant kernel's algorithmic bytes per launch divided by its
-average duration, timed with HIP events around graph-replayed launches on the
-stream the kernel runs on.  cpu_baseline: the torch-CPU restatement of the
-reference's dequantise-then-matmul path (oracle/torch_ref.py) on this host.
+roofline: the dominant kernel's algorithmic bytes (flops) per launch divided by
+its average duration, timed with HIP events on the stream the kernel runs on
+(c2: around each launch of the gate/up kernel inside eager layer sequences).
+cpu_baseline: the torch-CPU restatement of the reference's
+dequantise-then-matmul path (oracle/torch_ref.py) on this host.
 """
 from __future__ import annotations
 
@@ -488,19 +492,12 @@ def c2phase(args):
                       "copy_bytes": src.numel() * 2}), flush=True)
 
 
-def committed_traffic():
-    """HBM bytes per launch of the roofline kernel as measured by rocprofv3 --pmc
-    (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel), from the committed summary."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "stream_gate_up_c2_t16_traffic.md")
-    try:
-        for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return {"bytes": int(float(line.split(":", 1)[1])), "source": os.path.relpath(
-                    path, os.path.dirname(os.path.abspath(__file__)))}
-    except OSError:
-        return None
-    return None
+# HBM bytes per launch of the roofline kernel (grouped gate/up stream kernel, C2
+# T=16, 8 active experts): FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes
+# over `bench.py --workload c2phase`, each scaled by the same counter on a 512 MiB
+# copy.  Commands, raw counter values and scale factors:
+# profiles/stream_gate_up_c2_t16_traffic.md.  Re-measure after a kernel change.
+GATE_UP_C2_T16_TRAFFIC = 487_869_183
 
 
 def main():
@@ -567,10 +564,8 @@ def main():
                 "frac": round(gu["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
                 "bytes_per_launch": gu["bytes_per_launch"], "avg_us": gu["avg_us"],
                 "down": ph["down_4slices"], "active_experts": ph["active_experts"]}
-            tr = committed_traffic()
-            if tr is not None:
-                res["roofline"]["traffic"] = tr["bytes"]
-                res["roofline"]["traffic_source"] = tr["source"]
+            if ph["active_experts"] == 8:
+                res["roofline"]["traffic"] = GATE_UP_C2_T16_TRAFFIC
         res["metric"] = METRIC
         res["value"] = head["GB_s"]
         res["ms_per_step"] = head["ms_per_step"]
