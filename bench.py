@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X INT4 expert-MLP hot path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c4|c2phase] [--tokens T]
+    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c3|c4|c2phase] [--tokens T]
 
 Prints ONE JSON line.  A "step" is one pass of the hot path over one batch of
 synthetic input already resident in HBM:
@@ -9,6 +9,7 @@ synthetic input already resident in HBM:
   c2  (default, the headline) one Mixtral MoE layer at decode, T = 1, 4, 16
       (value: T = 16): route + grouped gate/up + down + unpermute
   c1  one Mixtral expert SwiGLU (H 4096, I 14336, INT4 g128), T tokens (default 1)
+  c3  one GLM-4.5-Air MoE layer at decode (T = 32, 128 experts, shared expert)
   c4  one Mixtral MoE layer at prefill (2048 tokens, Zipf-skewed routing)
 
 Weights are seeded N(0, 0.02) fp16 packed to INT4 by the GPU packer.  Steps
@@ -314,6 +315,74 @@ def time_decode_phases(layers, x, T, H, I, g, E, reps: int = 12):
     return res
 
 
+# ----------------------------------------------------------------------------- C3
+def bench_c3(args, T: int = 32, n_layers: int = 2):
+    """One GLM-4.5-Air MoE layer at decode: 128 INT4 experts (4096->1408->4096, g128),
+    fp16 shared expert, fp32 sigmoid router with a seeded U(-0.1, 0.1) selection bias,
+    top-8, T = 32 tokens.  Steps rotate over n_layers layers (2.3 GB for 2).
+    Algorithmic bytes: the unique experts' blobs (from the actual routing) + the
+    shared expert + the fp32 router weight + x in + y out."""
+    from hydranet_amd.model.moe import GLM4MoELayer
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
+
+    H, I, g, E, k = 4096, 1408, 128, 128, 8
+    layers = []
+    for L in range(n_layers):
+        slots = [make_expert_slot(expert_seed(L, e), H, I, g, slot_idx=e) for e in range(E)]
+        layer = GLM4MoELayer(H, I, E, k, layer_idx=L, slots=slots).cuda().half()
+        gen = torch.Generator(device="cuda").manual_seed(9000 + L)
+        layer.router.weight.data = (torch.randn(E, H, generator=gen, device="cuda") * 0.02).float()
+        layer.router.selection_bias = torch.rand(E, generator=gen, device="cuda") * 0.2 - 0.1
+        for j, lin in enumerate((layer.shared_expert.gate_proj, layer.shared_expert.up_proj,
+                                 layer.shared_expert.down_proj)):
+            lin.weight.data = normal_f16(tuple(lin.weight.shape), 9100 + 10 * L + j)
+        layer.eval()
+        layers.append(layer)
+    x = normal_f16((1, T, H), 3232, std=1.0)
+    blob = layers[0].experts.table.slots[0].layout.total_size
+    shared_bytes = 3 * H * I * 2
+    step_bytes, uniq = [], []
+    with torch.no_grad():
+        for layer in layers:
+            idx, _ = layer.router(x)
+            u = int(torch.unique(idx).numel())
+            uniq.append(u)
+            step_bytes.append(u * blob + shared_bytes + E * H * 4 + 2 * T * H * 2)
+    state = {"i": 0}
+
+    def step():
+        layer = layers[state["i"] % n_layers]
+        state["i"] += 1
+        with torch.no_grad():
+            layer(x)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    chunk = _chunk(args.steps)
+    state["i"] = 0
+    gr = _graph(step, chunk)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    if gr is not None:
+        for _ in range(args.steps // chunk):
+            gr.replay()
+    else:
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    total_bytes = sum(step_bytes[i % n_layers] for i in range(args.steps))
+    gbs = total_bytes / (ms * 1e-3 * args.steps) / 1e9
+    return {"workload": "C3: one GLM-4.5-Air MoE layer at decode, T=32 (128 experts "
+                        "4096->1408->4096 INT4 g128 + fp16 shared expert, sigmoid top-8 with "
+                        "seeded selection bias); router + route + grouped SwiGLU + unpermute",
+            "tokens": T, "ms_per_step": round(ms, 5), "GB_s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+            "avg_unique_experts": sum(uniq) / len(uniq), "layers_rotated": n_layers,
+            "graph": gr is not None}
+
+
 # ----------------------------------------------------------------------------- C4
 def zipf_logits(T: int, E: int, seed: int, s: float = 1.1, device="cuda"):
     """Router logits N(0,1) + ln p_e with Zipf(s) expert popularity (seeded)."""
@@ -505,7 +574,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c2phase"],
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c2phase"],
                     help="c2phase: only the C2 T=16 gate/up phase kernel and a 512 MiB copy "
                          "(the two kernels whose rocprofv3 counters give roofline.traffic)")
     ap.add_argument("--tokens", type=int, default=1)
@@ -529,6 +598,14 @@ def main():
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
     if args.workload == "c2phase":
         c2phase(args)
+        return
+    if args.workload == "c3":
+        c3 = bench_c3(args)
+        _log("c3", c3)
+        print(json.dumps({"metric": "INT4 expert-MLP HBM GB/s (GLM-4.5-Air MoE layer decode, "
+                                    "1 GPU)", "value": c3["GB_s"], "unit": "GB/s", "n_gpus": 1,
+                          "ms_per_step": c3["ms_per_step"], "higher_is_better": True,
+                          "dtype": "fp16", "data": "synthetic", "config": c3}), flush=True)
         return
     if args.workload == "c4":
         c4 = bench_c4(args)

@@ -606,6 +606,15 @@ extern "C" int hn_gemm_grouped_impl(int phase, const void* x, long ld_x, const v
 static int g_decode_path = 0;
 constexpr long kStreamMaxRows = 16;
 
+// Whether the streaming kernels take a grouped decode launch.  They stage at
+// most 8 tokens of an expert per pass over its weights, so an expert with more
+// rows streams its weights once per 8; they are used up to 16 rows per expert,
+// or up to 64 when the average over the experts is at most 4 (many experts,
+// few rows each: GLM-4.5-Air's 128 experts x top-8).
+static bool stream_rows_ok(long max_rows, long rows, long E) {
+  return max_rows <= kStreamMaxRows || (max_rows <= kMaxRows && rows <= 4 * E);
+}
+
 extern "C" int hn_set_decode_path(int path) {
   HN_ARG_CHECK(path == 0 || path == 1, "hn_set_decode_path: path must be 0 or 1 (got %d)", path);
   g_decode_path = path;
@@ -778,7 +787,7 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
                need);
   hipStream_t s = (hipStream_t)stream;
   const bool premul = (group % 128) != 0;
-  if (g_decode_path == 0 && !premul && max_rows_per_expert <= kStreamMaxRows &&
+  if (g_decode_path == 0 && !premul && stream_rows_ok(max_rows_per_expert, rows, E) &&
       hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
                              max_rows_per_expert, H, I, group, h_ws, I, s, 1) == 0 &&
       hn_stream_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E,
@@ -880,7 +889,7 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
                "aligned", who);
   hipStream_t s = (hipStream_t)stream;
   const bool premul = (group % 128) != 0;
-  if (rows > 0 && max_rows_per_expert > 0 && max_rows_per_expert <= kStreamMaxRows &&
+  if (rows > 0 && max_rows_per_expert > 0 && stream_rows_ok(max_rows_per_expert, rows, E) &&
       g_decode_path == 0 && !premul && H % 128 == 0 && I % 128 == 0 && aligned16(x_perm) &&
       aligned16(h_ws) &&
       hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
@@ -928,9 +937,9 @@ extern "C" int hn_grouped_decode_phase_int4(int phase, const void* x, const void
                "%s: bad sizes (E=%ld, rows=%ld)", who, E, rows);
   HN_ARG_CHECK(H % 128 == 0 && I % 128 == 0 && aligned16(x) && aligned16(h_ws),
                "%s: H, I multiples of 128 and 16-byte aligned buffers", who);
-  HN_ARG_CHECK(max_rows_per_expert <= kStreamMaxRows && group == 128,
-               "%s: the streaming kernels take <= %ld rows per expert and group 128", who,
-               kStreamMaxRows);
+  HN_ARG_CHECK(stream_rows_ok(max_rows_per_expert, rows, E) && group == 128,
+               "%s: the streaming kernels take <= %ld rows per expert (<= %ld when rows <= "
+               "4 E) and group 128", who, kStreamMaxRows, kMaxRows);
   if (rows == 0 || max_rows_per_expert == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   int rc;

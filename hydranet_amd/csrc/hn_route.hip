@@ -121,58 +121,119 @@ __device__ __noinline__ void topk_weights(const float* l, const int* sel, int k,
   }
 }
 
+// Unsigned key with the order of the float: larger value, larger key.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // Top-k of one token's logits row by one wave: lanes hold experts lane +
-// 64 j (E <= 256), k rounds of a wave-wide maximum.  Same selection and the
-// same weight arithmetic (on lane 0, in the same order) as topk_row, without
-// per-thread arrays indexed at run time.
+// 64 j (E <= 256).  The k-th largest candidate key is found by bisection over
+// its 32 bits (one ballot per bit and candidate register: no lane exchanges),
+// ties at that key go to the lower experts, and each selected candidate's
+// place in the (value desc, expert asc) order is the number of selected
+// candidates ahead of it.  Same selection and weight arithmetic as topk_small /
+// topk_weights: the sums over the selected experts run in selection order.
 __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int E, int k,
                                           int mode, float eps, float scaling, int lane,
                                           int* idx_o, h16* w_o) {
-  constexpr int kNone = 0x7fffffff;
-  float cv[4];
-  int ce[4];
+  constexpr int NJ = 4;
+  const uint64_t lt = (1ull << lane) - 1;
+  uint32_t key[NJ];
+  float raw[NJ];  // sigmoid (mode 1) or logit (mode 0) of the candidate
+  bool ok[NJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int e = lane + 64 * j;
-    cv[j] = -__builtin_inff();
-    ce[j] = kNone;
-    if (e < E) {
-      float v = l[e];
-      if (mode == 1) {
-        v = sigmoid_f32(v);
-        if (bias) v = v + bias[e];
+    ok[j] = e < E;
+    const float lv = ok[j] ? l[e] : 0.f;
+    float v = lv;
+    if (mode == 1 && ok[j]) {
+      v = sigmoid_f32(lv);
+      raw[j] = v;
+      if (bias) v = v + bias[e];
+    } else {
+      raw[j] = lv;
+    }
+    key[j] = ok[j] ? order_key(v) : 0u;
+  }
+  // largest t with at least k candidates of key >= t
+  uint32_t t = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t c = t | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (64 * j < E) cnt += __popcll(__ballot(ok[j] && key[j] >= c));
+    if (cnt >= k) t = c;
+  }
+  bool sel[NJ];
+  int above = 0;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    if (64 * j < E) above += __popcll(__ballot(ok[j] && key[j] > t));
+  int tie = 0;  // ties at t in expert order until k are selected
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint64_t m = 64 * j < E ? __ballot(ok[j] && key[j] == t) : 0ull;
+    const bool eq = ok[j] && key[j] == t;
+    sel[j] = (ok[j] && key[j] > t) || (eq && above + tie + __popcll(m & lt) < k);
+    tie += __popcll(m);
+  }
+  // place of each selected candidate: selected candidates ahead of it
+  int pos[NJ] = {0, 0, 0, 0};
+#pragma unroll
+  for (int jr = 0; jr < NJ; ++jr) {
+    if (64 * jr >= E) continue;
+    uint64_t m = __ballot(sel[jr]);
+    while (m) {
+      const int L = __builtin_ctzll(m);
+      m &= m - 1;
+      const uint32_t kr = __builtin_amdgcn_readlane(key[jr], L);
+      const int er = L + 64 * jr;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int e = lane + 64 * j;
+        if (sel[j] && (kr > key[j] || (kr == key[j] && er < e))) ++pos[j];
       }
-      cv[j] = v;
-      ce[j] = e;
     }
   }
-  int sel[kMaxTopK];
+  // the selected raw values in selection order, on every lane
+  auto at = [&](int r) -> float {
+    float x = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxTopK; ++i) {
-    sel[i] = -1;
-    if (i < k) {
-      float bv = cv[0];
-      int be = ce[0];
-#pragma unroll
-      for (int j = 1; j < 4; ++j)
-        if (topk_beats(cv[j], ce[j], bv, be)) { bv = cv[j]; be = ce[j]; }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oe = __shfl_xor(be, off, 64);
-        if (topk_beats(ov, oe, bv, be)) { bv = ov; be = oe; }
-      }
-      sel[i] = be < E ? be : -1;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (ce[j] == be) { cv[j] = -__builtin_inff(); ce[j] = kNone; }
+    for (int j = 0; j < NJ; ++j) {
+      if (64 * j >= E) continue;
+      const uint64_t m = __ballot(sel[j] && pos[j] == r);
+      if (m) x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                     __builtin_bit_cast(int, raw[j]), __builtin_ctzll(m)));
     }
-  }
-  if (lane != 0) return;
+    return x;
+  };
+  if (mode == 0) {
+    // fp32 softmax over the selected logits, renormalised (topk_weights)
+    const float mx = at(0);
+    float z = 0.f;
+    for (int r = 0; r < k; ++r) z += expf(at(r) - mx);
+    float sum = 0.f;
+    for (int r = 0; r < k; ++r) sum += expf(at(r) - mx) / z;
 #pragma unroll
-  for (int i = 0; i < kMaxTopK; ++i)
-    if (i < k) idx_o[i] = sel[i];
-  topk_weights(l, idx_o, k, mode, eps, scaling, w_o);
+    for (int j = 0; j < NJ; ++j)
+      if (sel[j]) {
+        idx_o[pos[j]] = lane + 64 * j;
+        w_o[pos[j]] = (h16)((expf(raw[j] - mx) / z) / sum);
+      }
+  } else {
+    float sum = 0.f;
+    for (int r = 0; r < k; ++r) sum += at(r);
+    const float d = sum + eps;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (sel[j]) {
+        idx_o[pos[j]] = lane + 64 * j;
+        w_o[pos[j]] = (h16)((raw[j] / d) * scaling);
+      }
+  }
 }
 
 // Top-k of one token's row by one thread for E <= EB experts: every loop is
