@@ -157,34 +157,35 @@ __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int
     }
     key[j] = ok[j] ? order_key(v) : 0u;
   }
-  // largest t with at least k candidates of key >= t
+  // Largest t with at least k candidates of key >= t.  Every real key is
+  // above 0 (the key of -inf is 0x007fffff) and the thresholds tried are >= 1,
+  // so the zero keys of absent candidates never count: no per-register
+  // conditions, no branches in the 32 steps.
   uint32_t t = 0;
+#pragma unroll
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t c = t | (1u << bit);
     int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (64 * j < E) cnt += __popcll(__ballot(ok[j] && key[j] >= c));
-    if (cnt >= k) t = c;
+    for (int j = 0; j < NJ; ++j) cnt += __popcll(__ballot(key[j] >= c));
+    t = cnt >= k ? c : t;
   }
   bool sel[NJ];
   int above = 0;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j)
-    if (64 * j < E) above += __popcll(__ballot(ok[j] && key[j] > t));
+  for (int j = 0; j < NJ; ++j) above += __popcll(__ballot(key[j] > t));
   int tie = 0;  // ties at t in expert order until k are selected
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const uint64_t m = 64 * j < E ? __ballot(ok[j] && key[j] == t) : 0ull;
-    const bool eq = ok[j] && key[j] == t;
-    sel[j] = (ok[j] && key[j] > t) || (eq && above + tie + __popcll(m & lt) < k);
+    const bool eq = key[j] == t;
+    const uint64_t m = __ballot(eq);
+    sel[j] = key[j] > t || (eq && above + tie + __popcll(m & lt) < k);
     tie += __popcll(m);
   }
   // place of each selected candidate: selected candidates ahead of it
   int pos[NJ] = {0, 0, 0, 0};
 #pragma unroll
   for (int jr = 0; jr < NJ; ++jr) {
-    if (64 * jr >= E) continue;
     uint64_t m = __ballot(sel[jr]);
     while (m) {
       const int L = __builtin_ctzll(m);
@@ -203,7 +204,6 @@ __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int
     float x = 0.f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      if (64 * j >= E) continue;
       const uint64_t m = __ballot(sel[j] && pos[j] == r);
       if (m) x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                      __builtin_bit_cast(int, raw[j]), __builtin_ctzll(m)));
@@ -413,34 +413,46 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
     wt[q] = (float)w[j];
     ++n;
   }
+  // the rows of a batch of B selected experts are loaded before any is used
+  // (independent loads in flight together), then added in expert order
+  constexpr int B = KS == 0 ? 8 : 2;
   for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
     half8_t acc = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int s = 0; s < n; ++s) {
-      half8_t v;
-      if constexpr (KS == 0) {
-        v = *reinterpret_cast<const half8_t*>(y + (long)pos[s] * ld_y + c);
-      } else {
-        float f[8];
+    for (int s0 = 0; s0 < n; s0 += B) {
+      half8_t v[B];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) f[q] = 0.f;
+      for (int u = 0; u < B; ++u) {
+        const int s = s0 + u < n ? s0 + u : n - 1;
+        if constexpr (KS == 0) {
+          v[u] = *reinterpret_cast<const half8_t*>(y + (long)pos[s] * ld_y + c);
+        } else {
+          float f[8];
 #pragma unroll
-        for (int j = 0; j < KS; ++j) {
-          const float* pp = part + j * ks_stride + (long)pos[s] * ld_y + c;
-          const float4_t a = *reinterpret_cast<const float4_t*>(pp);
-          const float4_t b = *reinterpret_cast<const float4_t*>(pp + 4);
+          for (int q = 0; q < 8; ++q) f[q] = 0.f;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            f[q] += a[q];
-            f[4 + q] += b[q];
+          for (int j = 0; j < KS; ++j) {
+            const float* pp = part + j * ks_stride + (long)pos[s] * ld_y + c;
+            const float4_t a = *reinterpret_cast<const float4_t*>(pp);
+            const float4_t b = *reinterpret_cast<const float4_t*>(pp + 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              f[q] += a[q];
+              f[4 + q] += b[q];
+            }
           }
-        }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = (h16)f[q];
+          for (int q = 0; q < 8; ++q) v[u][q] = (h16)f[q];
+        }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const h16 prod = (h16)((float)v[j] * wt[s]);
-        acc[j] = (h16)((float)acc[j] + (float)prod);
+      for (int u = 0; u < B; ++u) {
+        if (s0 + u >= n) break;
+        const float ws = wt[s0 + u];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const h16 prod = (h16)((float)v[u][j] * ws);
+          acc[j] = (h16)((float)acc[j] + (float)prod);
+        }
       }
     }
     if (shared) {

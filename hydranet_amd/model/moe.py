@@ -289,6 +289,19 @@ class MixtralMoELayer(nn.Module):
         return out.view(B, S, H)
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """One extra stream per device (default priority) for work that overlaps
+    the routing kernels."""
+    key = torch.device(device).index if torch.device(device).index is not None else \
+        torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=key)
+    return _SIDE_STREAMS[key]
+
+
 class GLM4DenseMLP(nn.Module):
     """fp16 dense SwiGLU (model/glm4.py:220-235); shared expert of GLM4MoELayer."""
 
@@ -322,20 +335,29 @@ class GLM4MoELayer(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor, skip_routed: bool = False) -> torch.Tensor:
         B, S, H = hidden_states.shape
-        shared = self.shared_expert(hidden_states)
         if skip_routed:
-            return shared
+            return self.shared_expert(hidden_states)
         T = B * S
         flat = hidden_states.reshape(T, H)
         rt = self.router
         if route_fits(T, rt.num_experts, rt.top_k):
+            # the shared expert (fp16 GEMMs) runs on a side stream while the
+            # router and the routing kernels run; joined before the experts
+            cur = torch.cuda.current_stream(flat.device)
+            side = _side_stream(flat.device)
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                shared = self.shared_expert(hidden_states)
             # fp32 logits by the multi-workgroup kernel, the rest in one launch
             logits = router_logits(flat, rt.weight.float() if rt.weight.dtype != torch.float32
                                    else rt.weight)
             r = moe_route(flat, rt.top_k, 1, logits=logits, bias=rt.selection_bias,
                           scaling=rt.routed_scaling_factor)
+            cur.wait_stream(side)
+            shared.record_stream(cur)
             out = moe_dispatch(r, self.experts.table_for(r.idx), shared=shared.reshape(T, H))
             return out.view(B, S, H)
+        shared = self.shared_expert(hidden_states)
         idx, w = rt(hidden_states)
         table = self.experts.table_for(idx)
         out = moe_experts_forward(flat, idx, w, table, shared=shared.reshape(T, H))
