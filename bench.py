@@ -594,7 +594,7 @@ def main():
         sys.exit(1)
     torch.cuda.set_device(0)
     from hydranet_amd import _lib
-    _lib.call("hn_set_decode_path", args.decode_path)
+    _lib.set_decode_path(args.decode_path)
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
     if args.workload == "c2phase":
         c2phase(args)

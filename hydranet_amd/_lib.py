@@ -42,6 +42,8 @@ SIGNATURES: dict[str, list] = {
     "hn_moe_experts_decode": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, P, P, L, L, P, L, P, L,
                               P, L, P],
     "hn_grouped_decode_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, L, P, P, L, P],
+    "hn_moe_decode_layer": [P, L, P, L, L, L, L, P, L, L, L, F, F, P, P, P, P, P, P, P, P, P,
+                            P, L, P, L, P],
 }
 
 # Sizes up to which hn_moe_route (one launch: logits, top-k, permutation,
@@ -81,6 +83,21 @@ def call(name: str, *args) -> None:
     if rc != 0:
         msg = lib().hn_last_error_string().decode(errors="replace")
         raise RuntimeError(f"{name} failed (rc={rc}): {msg}")
+
+
+_DECODE_PATH = 0
+
+
+def set_decode_path(path: int) -> None:
+    """Decode kernel family, process-wide: 0 = the streaming kernels where they
+    apply, 1 = split-K kernels only (A/B measurement and tests)."""
+    global _DECODE_PATH
+    call("hn_set_decode_path", path)
+    _DECODE_PATH = path
+
+
+def decode_path() -> int:
+    return _DECODE_PATH
 
 
 _WORKSPACES: dict = {}

@@ -586,6 +586,13 @@ extern "C" int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, c
                                 const void* w, long T, long k, const void* shared, long ld_sh,
                                 void* out, long ld_o, long H, void* stream);
 // Unpermute (hn_route.hip) from the four fp32 slices of the split down projection.
+extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const void* gate,
+                                            long ld_gate, long T, long E, long k,
+                                            const void* table, long H, long I, long group,
+                                            float eps, float scaling, float* logits_out,
+                                            int* idx, void* w, int* offsets, int* perm,
+                                            int* inv, int* active, int* n_active, void* h_ws,
+                                            void* stream, int dry_run);
 extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, const int* inv,
                                             const int* idx, const void* w, long T, long k,
                                             const void* shared, long ld_sh, void* out,
@@ -917,6 +924,50 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
                                       work_bytes, stream);
   if (rc == 0)
     rc = hn_moe_unpermute(y_ws, H, inv, idx, w, T, k, shared, ld_sh, out, ld_o, H, stream);
+  return rc;
+}
+
+// One Mixtral MoE layer at decode in three launches: the routing (logits,
+// softmax top-2, permutation) computed inside the gate/up streaming kernel,
+// the down projection in four K slices, the ordered weighted unpermute.
+// Same results as hn_moe_route followed by hn_moe_experts_decode.
+extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
+                                   long T, long E, long k, const void* table, long H, long I,
+                                   long group, float eps, float scaling, void* logits_out,
+                                   int* idx, void* w, int* offsets, int* perm, int* inv,
+                                   int* active, int* n_active, void* h_ws, void* out, long ld_o,
+                                   void* work, long work_bytes, void* stream) {
+  const char* who = "hn_moe_decode_layer";
+  HN_ARG_CHECK(aligned16(h) && aligned16(gate_w) && aligned16(h_ws) && aligned16(out) &&
+                   ld_o % 8 == 0,
+               "%s: h, gate, h_ws and out rows must be 16-byte aligned", who);
+  HN_ARG_CHECK(g_decode_path == 0, "%s: needs the streaming kernels (decode path 0)", who);
+  hipStream_t s = (hipStream_t)stream;
+  const long rows = T * k;
+  const bool ok =
+      hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, T, E, k, table, H, I, group, eps,
+                                   scaling, (float*)logits_out, idx, w, offsets, perm, inv,
+                                   active, n_active, h_ws, s, 1) == 0 &&
+      hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H, I, group,
+                                nullptr, s, 1) == 0;
+  HN_ARG_CHECK(ok, "%s: shape not covered (T <= 16, E <= 8, k == 2, H %% 512 == 0, I %% 512 "
+               "== 0, group 128; T=%ld E=%ld k=%ld H=%ld I=%ld group=%ld)", who, T, E, k, H, I,
+               group);
+  const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
+                                                            : hn_cdiv(H, kTileN);
+  const long need = hn_skinny_workspace_bytes(3, rows, H, I, E);
+  HN_ARG_CHECK(work && work_bytes >= need, "%s: workspace too small (%ld < %ld)", who,
+               work_bytes, need);
+  float* part = (float*)((char*)work + ctr_bytes(E * tmax));
+  int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, T, E, k, table, H, I, group, eps,
+                                        scaling, (float*)logits_out, idx, w, offsets, perm, inv,
+                                        active, n_active, h_ws, s, 0);
+  if (rc == 0)
+    rc = hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H, I,
+                                   group, part, s, 0);
+  if (rc == 0)
+    rc = hn_moe_unpermute_split4_impl(part, rows * H, inv, idx, w, T, k, nullptr, H, out, ld_o,
+                                      H, stream);
   return rc;
 }
 

@@ -43,6 +43,7 @@
 //    magnitudes ~1024 |x|, i.e. a relative error ~1e-5 of the result, well
 //    inside the fp16 output rounding.
 #include "hn_common.h"
+#include "hn_topk.h"
 
 namespace {
 
@@ -78,6 +79,16 @@ struct StreamArgs {
   // row r goes to out32[j * ks_stride + r * N + n] in fp32
   float* out32;
   long ks_stride;
+  // ROUTE (grouped gate/up only): the routing of hx computed in the kernel.
+  // hx [T, H] fp16 hidden rows, gate [E, H] fp16; the permuted rows are
+  // staged from hx directly; workgroup 0 writes the routing outputs.
+  const h16* hx; int ld_hx;
+  const h16* gate; int ld_gate;
+  int T, topk;
+  float eps, scaling;
+  float* logits_out;
+  int* idx_out; h16* w_out;
+  int* offsets_out; int* perm_out; int* inv_out; int* active_out; int* n_active_out;
 };
 
 // Weights and scales of one column for one wave.  Scales: with WIDE, dword
@@ -292,15 +303,21 @@ struct StageGeom {
   int m0, Mc, blk_per_tok, nblk;
 };
 
+// ROUTE: rperm (LDS) maps a permuted row to its assignment (token * topk +
+// slot), and the row is read from hx.  t0: the problem's first permuted row.
+template <bool ROUTE = false>
 __device__ __forceinline__ void stage_load(const StreamArgs& A, const h16* x,
-                                           const StageGeom& sg, int base, half8_t v[4]) {
+                                           const StageGeom& sg, int base, half8_t v[4],
+                                           const int* rperm = nullptr, int t0 = 0) {
   const int tid = threadIdx.x, nthr = blockDim.x, K = A.K;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = min(base + tid + j * nthr, sg.nblk - 1);
     const int t = i / sg.blk_per_tok;
     const int k = min((i - t * sg.blk_per_tok) * 8, K - 8);
-    v[j] = *reinterpret_cast<const half8_t*>(x + (long)(sg.m0 + t) * A.ld_x + k);
+    const h16* row = ROUTE ? A.hx + (long)(rperm[t0 + sg.m0 + t] / A.topk) * A.ld_hx
+                           : x + (long)(sg.m0 + t) * A.ld_x;
+    v[j] = *reinterpret_cast<const half8_t*>(row + k);
   }
 }
 
@@ -350,14 +367,16 @@ __device__ __forceinline__ void stage_zero_rows(const StreamArgs& A, int Mc, flo
 }
 
 // Whole staging of one chunk (used when the staged chunk changes mid-stream).
+template <bool ROUTE = false>
 __device__ __forceinline__ void stage(const StreamArgs& A, const h16* x, const StageGeom& sg,
-                                      h16* xs, float* cs) {
+                                      h16* xs, float* cs, const int* rperm = nullptr,
+                                      int t0 = 0) {
   const int nthr = blockDim.x;
   __syncthreads();  // the previous chunk is no longer read
   stage_zero_rows(A, sg.Mc, cs);
   for (int base = 0; base < sg.nblk; base += 4 * nthr) {
     half8_t v[4];
-    stage_load(A, x, sg, base, v);
+    stage_load<ROUTE>(A, x, sg, base, v, rperm, t0);
     stage_store(A, sg, base, v, xs, cs);
   }
   __syncthreads();
@@ -382,6 +401,119 @@ __device__ __forceinline__ void locate(Cursor& cu, const int* chunk_off, int npr
   chunk = gc - cu.lo;
 }
 
+// Decode routing in the gate/up kernel's prologue (ROUTE): Mixtral softmax
+// top-2 of E <= 8 experts over T <= 16 tokens, fp16 gate.  The arithmetic is
+// moe_route_kernel's (hn_route.hip): logits by MFMA over 16 slices of H, the
+// slice partials summed in slice order and rounded to fp16 (the fp16 Linear
+// of TopKRouter, model/router.py:102); top-k and weights by topk_small; the
+// stable order by expert from ballots (torch.where order, model/mixtral.py:
+// 333).  Every workgroup computes it into LDS (part: 16 KiB scratch, reused by
+// the staging afterwards); workgroup 0 also writes the routing outputs.
+// Returns the number of active experts (uniform).
+__device__ int route_prologue(const StreamArgs& A, float* part, int* s_act, int* s_off,
+                              int* rperm, int wave, int lane) {
+  const int tid = threadIdx.x, KW = blockDim.x >> 6;
+  const int T = A.T, E = A.E, H = A.K, k = A.topk, n = T * k;
+  const bool lead = blockIdx.x == 0;
+  float* s_lg = part + 16 * 16 * 16;           // [T * E]
+  int* s_sel = reinterpret_cast<int*>(s_lg + 16 * 16);
+  h16* s_w = reinterpret_cast<h16*>(s_sel + 64);
+  int* s_na = reinterpret_cast<int*>(s_w + 64);
+  // 1. logits: slice sl of H/16 by wave sl % KW; lane (expert tl, tokens 4 (lane >> 4) + r)
+  {
+    const int ksl = H >> 4, steps = ksl >> 5;
+    const int tl = lane & 15, kq = (lane >> 4) * 8;
+    const h16* ap = A.hx + (long)min(tl, T - 1) * A.ld_hx + kq;
+    const h16* bp = A.gate + (long)min(tl, E - 1) * A.ld_gate + kq;
+    // two slices per pass (sl0, sl0 + KW), their loads in flight together
+    for (int sl0 = wave; sl0 < 16; sl0 += 2 * KW) {
+      const int sl1 = sl0 + KW;
+      const bool has1 = sl1 < 16;  // uniform
+      const int kb0 = sl0 * ksl, kb1 = (has1 ? sl1 : sl0) * ksl;
+      float4_t acc0 = float4_t{0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+#pragma unroll 8
+      for (int st = 0; st < steps; ++st) {
+        const half8_t b0 = *reinterpret_cast<const half8_t*>(bp + kb0 + 32 * st);
+        const half8_t a0 = *reinterpret_cast<const half8_t*>(ap + kb0 + 32 * st);
+        const half8_t b1 = *reinterpret_cast<const half8_t*>(bp + kb1 + 32 * st);
+        const half8_t a1 = *reinterpret_cast<const half8_t*>(ap + kb1 + 32 * st);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc1, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        part[(sl0 * 16 + 4 * (lane >> 4) + r) * 16 + tl] = acc0[r];
+        if (has1) part[(sl1 * 16 + 4 * (lane >> 4) + r) * 16 + tl] = acc1[r];
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < T * E; i += blockDim.x) {
+    const int t = i / E, e = i - t * E;
+    float v = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < 16; ++sl) v += part[(sl * 16 + t) * 16 + e];
+    s_lg[i] = (float)(h16)v;
+    if (lead && A.logits_out) A.logits_out[i] = s_lg[i];
+  }
+  __syncthreads();
+  // 2. top-2 and weights, one thread per token
+  for (int t = tid; t < T; t += blockDim.x)
+    topk_small<8, 2, 0>(s_lg + t * E, nullptr, E, 2, 0, A.eps, A.scaling, s_sel + t * 2,
+                        s_w + t * 2);
+  __syncthreads();
+  // 3. stable order by expert (n <= 64: wave 0, one lane per assignment).
+  //    Rank among equal experts from ballots over the bits of e (E <= 8:
+  //    bits 0-2, and bit 3 set only for the -1 of no expert); the counts,
+  //    offsets and the active list are wave-uniform scalar sums over the
+  //    experts in order.
+  if (wave == 0) {
+    const int j = lane;
+    int e = j < n ? s_sel[j] : -1;
+    if (e < 0 || e >= E) e = -1;
+    uint64_t same = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint64_t bal = __ballot((e >> b) & 1);
+      same &= ((e >> b) & 1) ? bal : ~bal;
+    }
+    const int rank = __popcll(same & ((1ull << lane) - 1));
+    int run = 0, nact = 0, off_e = 0;
+    for (int x = 0; x < E; ++x) {  // uniform
+      const int c = __popcll(__ballot(e == x));
+      if (e == x) off_e = run;
+      if (lane == 0) {
+        s_off[x] = run;
+        if (c > 0) s_act[nact] = x;
+        if (lead) {
+          A.offsets_out[x] = run;
+          if (c > 0) A.active_out[nact] = x;
+        }
+      }
+      nact += c > 0 ? 1 : 0;
+      run += c;
+    }
+    if (lane == 0) {
+      s_off[E] = run;
+      *s_na = nact;
+      if (lead) {
+        A.offsets_out[E] = run;
+        *A.n_active_out = nact;
+      }
+    }
+    const int pos = off_e + rank;
+    if (e >= 0) rperm[pos] = j;
+    if (lead && j < n) {
+      A.idx_out[j] = s_sel[j];
+      A.w_out[j] = s_w[j];
+      A.inv_out[j] = e >= 0 ? pos : -1;
+      if (e >= 0) A.perm_out[pos] = j;
+    }
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(*s_na);
+}
+
 // At most 8 waves per workgroup and one workgroup per CU: 2 waves per SIMD,
 // 256 VGPRs each.
 // KS > 1: the columns of a chunk are (k slice, tile), the slices one after
@@ -389,7 +521,8 @@ __device__ __forceinline__ void locate(Cursor& cu, const int* chunk_off, int npr
 // slice (one staging); each column's wave-reduced partial is written in fp32
 // and the caller sums the KS slices in order.  A slice keeps the workgroup's
 // activations and the pipeline short where K is long (the down projection).
-template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS>
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS,
+          bool ROUTE = false>
 __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
                                                      const SExpert* __restrict__ table,
                                                      const int* __restrict__ active,
@@ -424,20 +557,31 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
 
   // ---- token chunks per problem -> prefix (chunk_off); columns = chunks * tiles
   int nprob = 1;
+  int* rperm = nullptr;  // ROUTE: permuted row -> assignment
   if (GROUPED) {
     // one round of independent loads: active list, offsets, weight pointers
+    // (ROUTE: the pointers only; the active list and offsets are computed)
     const int E = A.E;
     int* s_act = reinterpret_cast<int*>(red + 2 * kRedSlots);
     int* s_off = s_act + ((E + 1) & ~1);
     uint64_t* s_ptr = reinterpret_cast<uint64_t*>(s_off + ((E + 2) & ~1));
-    const int na = *n_active;
     const uint64_t* tw = reinterpret_cast<const uint64_t*>(table);
-    for (int i = tid; i < E; i += blockDim.x) s_act[i] = active[i];
-    for (int i = tid; i <= E; i += blockDim.x) s_off[i] = offsets[i];
-    for (int i = tid; i < 4 * E; i += blockDim.x) {
-      const int e = i >> 2, j = i & 3;
-      const int f = A.phase == 0 ? j : 4 + (j & 1);  // gate_q gate_s up_q up_s | down_q down_s
-      s_ptr[i] = tw[6 * e + f];
+    int na;
+    if constexpr (ROUTE) {
+      // pointers requested first, stored once the routing is done (4 E <= 32 threads)
+      const uint64_t pv = tid < 4 * E ? tw[6 * (tid >> 2) + (tid & 3)] : 0;
+      rperm = reinterpret_cast<int*>(s_ptr + 4 * E);
+      na = route_prologue(A, reinterpret_cast<float*>(smem), s_act, s_off, rperm, wave, lane);
+      if (tid < 4 * E) s_ptr[tid] = pv;
+    } else {
+      na = *n_active;
+      for (int i = tid; i < E; i += blockDim.x) s_act[i] = active[i];
+      for (int i = tid; i <= E; i += blockDim.x) s_off[i] = offsets[i];
+      for (int i = tid; i < 4 * E; i += blockDim.x) {
+        const int e = i >> 2, j = i & 3;
+        const int f = A.phase == 0 ? j : 4 + (j & 1);  // gate_q gate_s up_q up_s | down_q down_s
+        s_ptr[i] = tw[6 * e + f];
+      }
     }
     meta = {s_act, s_off, s_ptr};
     nprob = min(na, min(E, kMaxActive));
@@ -522,8 +666,10 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
   };
 
   WBuf<MATS, PAIRS, WIDE> b0, b1, b2;
-  // ---- prologue: the first chunk's activations are requested before the
-  //      first columns' weights and waited for alone
+  // ---- prologue: the first chunk's activations (up to two rounds of loads)
+  //      are requested before the first columns' weights and waited for
+  //      alone (loads complete in issue order: a round issued after the
+  //      weights would wait for them)
   {
     int p, ch, t;
     locate(cu_c, chunk_off, nprob, tiles, cb, p, ch, t);
@@ -535,14 +681,18 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     pi_last = p;
     sg = geom(ch);
     const h16* xsl = st_pr.x + st_kj * A.K;
-    half8_t v[4];
-    stage_load(A, xsl, sg, 0, v);
+    const int round = 4 * (int)blockDim.x;
+    const bool two = sg.nblk > round;  // uniform
+    half8_t v[4], v2[4];
+    stage_load<ROUTE>(A, xsl, sg, 0, v, rperm, st_pr.t0);
+    if (two) stage_load<ROUTE>(A, xsl, sg, round, v2, rperm, st_pr.t0);
     issue_next(b0);
     if (NBUF == 3) issue_next(b1);
     stage_zero_rows(A, sg.Mc, cs);
     stage_store(A, sg, 0, v, xs, cs);
-    for (int base = 4 * (int)blockDim.x; base < sg.nblk; base += 4 * blockDim.x) {
-      stage_load(A, xsl, sg, base, v);
+    if (two) stage_store(A, sg, round, v2, xs, cs);
+    for (int base = 2 * round; base < sg.nblk; base += round) {
+      stage_load<ROUTE>(A, xsl, sg, base, v, rperm, st_pr.t0);
       stage_store(A, sg, base, v, xs, cs);
     }
     __syncthreads();
@@ -563,7 +713,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
         st_ch = ch;
         st_kj = kj;
         sg = geom(ch);
-        stage(A, st_pr.x + st_kj * A.K, sg, xs, cs);
+        stage<ROUTE>(A, st_pr.x + st_kj * A.K, sg, xs, cs, rperm, st_pr.t0);
       }
     }
     issue_next(nxt);
@@ -678,7 +828,11 @@ struct StreamPlan {
 // per column, the smallest that covers K with 8 waves; three column buffers
 // when they fit the register budget, else two.  tc <= 8 tokens per chunk,
 // limited by the LDS left after the corrections and the reduction buffers.
-StreamPlan stream_plan(long K, int mats, long rows, long E = 0) {
+// LDS scratch of the routing prologue (ROUTE), in front of the metadata:
+// 16 slice partials of 16 x 16 logits, the logits, the selection.
+constexpr int kRouteScratch = 16 * 16 * 16 * 4 + 256 * 4 + 64 * 4 + 64 * 2 + 16;
+
+StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = false) {
   StreamPlan p{};
   const long G = K / 128;
   int lpw = 2;
@@ -695,11 +849,13 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0) {
   const int per_tok = 2 * p.ldx * 2;
   const int want = (int)(rows < kMaxTc ? rows : kMaxTc);
   // grouped metadata copy: active [E], offsets [E + 1] (each padded to even), pointers [E][4]
-  const int meta = (int)(((E + 1) & ~1L) * 4 + ((E + 2) & ~1L) * 4 + E * 32);
+  // (ROUTE: and the permuted-row map, 64 entries)
+  const int meta = (int)(((E + 1) & ~1L) * 4 + ((E + 2) & ~1L) * 4 + E * 32) + (route ? 256 : 0);
   const int tcmax = (kLdsPerCu - kStaticLds - red - cs - meta) / per_tok;
   p.tc = tcmax < want ? tcmax : want;
   if (p.tc < 1) return p;
   p.lds = p.tc * per_tok + cs + red + meta;
+  if (route && p.tc * per_tok + cs + red < kRouteScratch) return p;
   p.ok = true;
   return p;
 }
@@ -718,9 +874,10 @@ int num_cus() {
   return n;
 }
 
-template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS = 1>
+template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS = 1,
+          bool ROUTE = false>
 int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
-  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS>;
+  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS, ROUTE>;
   static int attr = -1;  // per instantiation
   if (attr < 0) {
     attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -882,5 +1039,65 @@ extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const
   const int rc = launch_one<true, 1, 0, 4, 3, true, kDownSplit>(A, g, pw, (hipStream_t)stream);
   if (rc) return rc;
   HN_LAUNCH_CHECK("hn_stream_down_split");
+  return 0;
+}
+
+// Decode routing fused into the grouped gate/up launch: Mixtral softmax top-2
+// over E <= 8 experts, T <= 16 tokens, fp16 gate [E, H] (the arithmetic of
+// hn_moe_route), then h_ws = SwiGLU gate/up of the routed rows, staged from
+// hx directly (no x_perm).  Workgroup 0 writes logits_out (optional), idx, w,
+// offsets, perm, inv, active and n_active for the down projection and the
+// unpermute.  Returns HN_NOT_HANDLED when the shape is not covered.
+extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const void* gate,
+                                            long ld_gate, long T, long E, long k,
+                                            const void* table, long H, long I, long group,
+                                            float eps, float scaling, float* logits_out,
+                                            int* idx, void* w, int* offsets, int* perm,
+                                            int* inv, int* active, int* n_active, void* h_ws,
+                                            void* stream, int dry_run) {
+  if (T < 1 || T > 16 || E < 1 || E > 8 || k != 2 || H % 512 != 0 || group != 128 ||
+      I % 128 != 0 || ld_hx % 8 != 0 || ld_gate % 8 != 0 || ld_hx >= (1L << 31) ||
+      ld_gate >= (1L << 31))
+    return HN_NOT_HANDLED;
+  const StreamPlan p = stream_plan(H, 2, T, E, true);
+  if (!p.ok || p.lpw > 8 || !wide_scales_ok(p, H, H / group)) return HN_NOT_HANDLED;
+  if (I * (H / 2) >= (long)kOOB || I * (H / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
+  if (dry_run) return 0;
+  StreamPlan pw = p;
+  pw.wide = true;
+  StreamArgs A = {};
+  A.x = (const h16*)hx;  // unused: rows come from hx through the permutation
+  A.ld_x = 0;
+  A.phase = 0;
+  A.E = (int)E;
+  A.ld_q = (int)(H / 2);
+  A.ld_s = (int)(H / group);
+  A.out = (h16*)h_ws;
+  A.ld_o = (int)I;
+  fill_common(A, p, I, H);
+  A.hx = (const h16*)hx;
+  A.ld_hx = (int)ld_hx;
+  A.gate = (const h16*)gate;
+  A.ld_gate = (int)ld_gate;
+  A.T = (int)T;
+  A.topk = (int)k;
+  A.eps = eps;
+  A.scaling = scaling;
+  A.logits_out = logits_out;
+  A.idx_out = idx;
+  A.w_out = (h16*)w;
+  A.offsets_out = offsets;
+  A.perm_out = perm;
+  A.inv_out = inv;
+  A.active_out = active;
+  A.n_active_out = n_active;
+  const GroupedPtrs g = {(const SExpert*)table, nullptr, nullptr, nullptr};
+  hipStream_t s = (hipStream_t)stream;
+  int rc = HN_NOT_HANDLED;
+  if (p.lpw == 2) rc = launch_one<true, 2, 1, 2, 3, true, 1, true>(A, g, pw, s);
+  else if (p.lpw == 4) rc = launch_one<true, 2, 1, 4, 3, true, 1, true>(A, g, pw, s);
+  else if (p.lpw == 8) rc = launch_one<true, 2, 1, 8, 2, true, 1, true>(A, g, pw, s);
+  if (rc) return rc;
+  HN_LAUNCH_CHECK("hn_stream_route_gate_up");
   return 0;
 }

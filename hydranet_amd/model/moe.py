@@ -125,6 +125,45 @@ def moe_route(hidden: torch.Tensor, k: int, mode: int, gate_w: Optional[torch.Te
     return r
 
 
+def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torch.Tensor) -> bool:
+    """Whether hn_moe_decode_layer (routing fused into the gate/up kernel)
+    covers this Mixtral layer call."""
+    H, I, g = table.dims
+    return (_lib.decode_path() == 0 and 1 <= T <= 16 and E <= 8 and k == 2 and g == 128
+            and H % 512 == 0 and I % 512 == 0 and table.num_experts == E
+            and gate_w.shape == (E, H))
+
+
+def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: "ExpertTable",
+                     want_logits: bool = False):
+    """One Mixtral MoE layer at decode in three launches (hn_moe_decode_layer):
+    fp16 gate logits, softmax top-k and the stable permutation computed in the
+    gate/up kernel, the down projection, the ordered weighted unpermute.
+    Returns (out [T, H] fp16, Routed) with the same routing outputs as
+    moe_route (x_perm is not written)."""
+    T, H = hidden.shape
+    _lib.require_gpu(hidden)
+    dev = hidden.device
+    E = gate_w.shape[0]
+    Ht, I, g = table.dims
+    assert Ht == H, f"hidden {H} != expert hidden {Ht}"
+    x = _lib.aligned_rows(hidden.to(torch.float16))
+    ww = _lib.aligned_rows(gate_w.to(torch.float16))
+    r = Routed(T, k, E, 0, dev)
+    if want_logits:
+        r.logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    n = T * k
+    h_ws = torch.empty((n, I), dtype=torch.float16, device=dev)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    work = _lib.skinny_workspace(3, n, H, I, E, dev)
+    _lib.call("hn_moe_decode_layer", _lib.ptr(x), x.stride(0), _lib.ptr(ww), ww.stride(0), T, E,
+              k, _lib.ptr(table.dev), H, I, g, 1e-9, 1.0, _lib.ptr(r.logits), _lib.ptr(r.idx),
+              _lib.ptr(r.w), _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv),
+              _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(h_ws), _lib.ptr(out), H,
+              _lib.ptr(work), work.numel(), _lib.stream(dev))
+    return out, r
+
+
 def moe_dispatch(r: Routed, table: ExpertTable,
                  shared: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Grouped SwiGLU over the routed rows and the weighted, ordered sum back
@@ -224,6 +263,19 @@ class _ResidentExperts:
         if slots is not None:
             self.table = ExpertTable.from_slots(slots)
 
+    def static_table(self, device) -> Optional[ExpertTable]:
+        """The table when it does not depend on the routing (fixed slots, or a
+        cache manager holding every expert of the layer), else None."""
+        cm = self.cache_manager
+        if cm is None:
+            return self.table
+        if cm.is_resident(self.layer_idx):
+            if self._resident_table is None:
+                self._resident_table = ExpertTable.from_slots(cm.resident_slots(self.layer_idx),
+                                                              device)
+            return self._resident_table
+        return None
+
     def table_for(self, idx: torch.Tensor) -> ExpertTable:
         cm = self.cache_manager
         if cm is None:
@@ -272,15 +324,21 @@ class MixtralMoELayer(nn.Module):
         flat = hidden_states.reshape(T, H)
         rt = self.router
         if route_fits(T, self.num_experts, top_k):
-            # decode: routing, permutation and gather in one launch
             logits = None
             if rt.enable_affinity_bonus and rt._is_cached_fn is not None:
                 logits = rt._affinity(router_logits(flat, rt.gate.weight.to(torch.float16)))
-            r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits)
+            table = self.experts.static_table(flat.device) if logits is None else None
+            if table is not None and decode_layer_fits(T, self.num_experts, top_k, table,
+                                                       rt.gate.weight):
+                # decode, resident experts: routing inside the gate/up kernel
+                out, r = moe_decode_layer(flat, rt.gate.weight, top_k, table)
+            else:
+                # decode: routing, permutation and gather in one launch
+                r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits)
+                out = moe_dispatch(r, self.experts.table_for(r.idx))
             if not rt.training:
                 rt.usage_counts += torch.bincount(r.idx.view(-1).long(),
                                                   minlength=self.num_experts)
-            out = moe_dispatch(r, self.experts.table_for(r.idx))
             return out.view(B, S, H)
         ro = rt(hidden_states, top_k_override=top_k)
         idx = ro.expert_indices.reshape(T, top_k)

@@ -156,6 +156,23 @@ int hn_moe_experts_decode(const void* x_perm, const void* table, const int* acti
                           long T, long k, const void* shared, long ld_sh, void* out, long ld_o,
                           void* work, long work_bytes, void* stream);
 
+/* One Mixtral MoE layer at decode (T <= 16 tokens, E <= 8 experts, top-2
+ * softmax, fp16 gate [E, H], group 128, H and I multiples of 512) in three
+ * launches: the routing (logits, top-k, stable permutation) computed inside
+ * the gate/up streaming kernel from h [T, H] directly (no x_perm), the down
+ * projection in four K slices, the ordered weighted unpermute into out
+ * [T, H].  Results equal hn_moe_route + hn_moe_experts_decode; the routing
+ * outputs (logits_out may be NULL, idx, w, offsets [E + 1], perm, inv, active,
+ * n_active) are written as hn_moe_route writes them.  h_ws [T k, I] fp16;
+ * work: hn_skinny_workspace_bytes(3, T k, H, I, E).  Replaces
+ * MixtralMoELayer.forward's router call, per-expert loop and index_add_
+ * (model/mixtral.py:283-368) at decode sizes. */
+int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w, long T, long E,
+                        long k, const void* table, long H, long I, long group, float eps,
+                        float scaling, void* logits_out, int* idx, void* w, int* offsets,
+                        int* perm, int* inv, int* active, int* n_active, void* h_ws, void* out,
+                        long ld_o, void* work, long work_bytes, void* stream);
+
 /* One phase of hn_moe_experts_decode's streaming path on its own (<= 16 rows per
  * expert, group 128): phase 0 reads x [rows, H] (sorted by expert) and writes
  * h_ws [rows, I]; phase 1 reads h_ws-shaped x [rows, I] and writes the four

@@ -38,6 +38,6 @@ def decode_path(request):
     """Run a decode test through both kernel families: 0 = automatic (the
     persistent streaming kernels where they apply), 1 = split-K kernels only."""
     from hydranet_amd import _lib
-    _lib.call("hn_set_decode_path", request.param)
+    _lib.set_decode_path(request.param)
     yield request.param
-    _lib.call("hn_set_decode_path", 0)
+    _lib.set_decode_path(0)

@@ -350,3 +350,35 @@ def test_experts_decode_split_vs_grouped(T, mixtral_experts, decode_path):
         assert torch.equal(got, ref)
     else:
         _close(got, ref)
+
+
+@pytest.mark.parametrize("T", [1, 4, 9, 16])
+def test_decode_layer_fused_routing_matches_route_then_experts(T, mixtral_experts):
+    """hn_moe_decode_layer (routing computed inside the gate/up kernel, rows
+    staged from h through the permutation) vs hn_moe_route followed by
+    hn_moe_experts_decode on the same inputs: routing outputs (logits, idx, w,
+    offsets, active, n_active, perm, inv) and the layer output bit for bit."""
+    from hydranet_amd.model.moe import ExpertTable, moe_decode_layer, moe_dispatch, moe_route
+    slots, _ = mixtral_experts
+    table = ExpertTable.from_slots(slots)
+    g = torch.Generator().manual_seed(70 + T)
+    x = torch.randn(T, 4096, generator=g).half().to(DEV)
+    gw = (torch.randn(8, 4096, generator=g) * 0.02).half().to(DEV)
+    r0 = moe_route(x, 2, 0, gate_w=gw)
+    ref = moe_dispatch(r0, table)
+    out, r1 = moe_decode_layer(x, gw, 2, table, want_logits=True)
+    torch.cuda.synchronize()
+    assert torch.equal(r1.logits, r0.logits)
+    assert torch.equal(r1.idx, r0.idx)
+    assert torch.equal(r1.w, r0.w)
+    na = int(r0.n_active.item())
+    assert int(r1.n_active.item()) == na
+    assert torch.equal(r1.offsets, r0.offsets)
+    assert torch.equal(r1.active[:na], r0.active[:na])
+    assert torch.equal(r1.perm, r0.perm)
+    assert torch.equal(r1.inv, r0.inv)
+    assert torch.equal(out, ref)
+    # a second call on other inputs reuses the workspace: still equal
+    x2 = torch.randn(T, 4096, generator=g).half().to(DEV)
+    out2, _ = moe_decode_layer(x2, gw, 2, table)
+    assert torch.equal(out2, moe_dispatch(moe_route(x2, 2, 0, gate_w=gw), table))
