@@ -18,7 +18,8 @@ not from the 256 MB Infinity Cache.  Steps are replayed from a HIP graph.
 
 roofline: the dominant kernel's algorithmic bytes (flops) per launch divided by
 its average duration, timed with HIP events on the stream the kernel runs on
-(c2: around each launch of the gate/up kernel inside eager layer sequences).
+(c2: around each launch of the routing + gate/up kernel inside eager layer
+sequences).
 cpu_baseline: the torch-CPU restatement of the reference's
 dequantise-then-matmul path (oracle/torch_ref.py) on this host.
 """
@@ -245,69 +246,68 @@ def bench_c2(args, T: int, n_layers: int = 4, phases: bool = False):
 
 def time_decode_phases(layers, x, T, H, I, g, E, reps: int = 12):
     """The two expert phases of the decode layer timed inside the layer's own
-    sequence (routing -> gate/up -> down -> unpermute over the rotating layers,
-    the kernels of hn_moe_route / hn_grouped_decode_phase_int4 /
-    hn_moe_unpermute), an event on the launch stream before and after each
-    expert phase.  Bytes per launch: the active experts' packed weights and scales
-    plus activations in and out (phase 1 writes four fp32 K-slice partials)."""
+    launch sequence over the rotating layers: routing + gate/up (one launch,
+    hn_moe_route_gate_up) -> down in four K slices (hn_grouped_decode_phase_int4
+    phase 1) -> unpermute, with an event on the launch stream before and after
+    each of the first two.  Bytes per launch: the active experts' packed weights
+    and scales plus activations in and out (and the fp16 gate for the routing;
+    the down phase writes four fp32 K-slice partials)."""
     from hydranet_amd import _lib
-    from hydranet_amd.model.moe import moe_route
+    from hydranet_amd.model.moe import Routed
     k = 2
     n = T * k
-    routes = [moe_route(x, k, 0, gate_w=l.router.gate.weight) for l in layers]
-    torch.cuda.synchronize()
-    nact = [int(r.n_active.item()) for r in routes]
+    xx = _lib.aligned_rows(x)
+    gates = [_lib.aligned_rows(l.router.gate.weight.to(torch.float16)) for l in layers]
+    rts = [Routed(T, k, E, 0, "cuda") for _ in layers]
     h_ws = torch.empty(n, I, dtype=torch.float16, device="cuda")
     out = torch.empty(T, H, dtype=torch.float16, device="cuda")
     work = _lib.skinny_workspace(3, n, H, I, E, "cuda")
     lay = layers[0].experts.table.slots[0].layout
     gu = 2 * (lay.gate_packed_size + lay.gate_scales_size)
     dn = lay.down_packed_size + lay.down_scales_size
-    xx = _lib.aligned_rows(x)
     sp = _lib.stream()
-    part = _lib.ptr(work)  # partials start after the counter region (set by the library)
 
-    def route(li):
-        r, lw = routes[li], layers[li].router.gate.weight
-        _lib.call("hn_moe_route", _lib.ptr(xx), H, _lib.ptr(lw), H, 0, None, None, T, E, H, k, 0,
-                  1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w), _lib.ptr(r.offsets),
-                  _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active), _lib.ptr(r.n_active),
-                  _lib.ptr(r.x_perm), H, sp)
+    def route_gate_up(li):
+        r, tb = rts[li], layers[li].experts.table
+        _lib.call("hn_moe_route_gate_up", _lib.ptr(xx), H, _lib.ptr(gates[li]), H, T, E, k,
+                  _lib.ptr(tb.dev), H, I, g, 1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w),
+                  _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active),
+                  _lib.ptr(r.n_active), _lib.ptr(h_ws), sp)
 
-    def phase(li, ph):
-        r, tb = routes[li], layers[li].experts.table
-        xin = r.x_perm if ph == 0 else h_ws
-        _lib.call("hn_grouped_decode_phase_int4", ph, _lib.ptr(xin), _lib.ptr(tb.dev),
+    def down(li):
+        r, tb = rts[li], layers[li].experts.table
+        _lib.call("hn_grouped_decode_phase_int4", 1, _lib.ptr(h_ws), _lib.ptr(tb.dev),
                   _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I, g,
                   _lib.ptr(h_ws), _lib.ptr(work), work.numel(), sp)
 
     def unpermute(li):
-        # stand-in for the unpermute of hn_moe_experts_decode: same kernel, fp16 y path
-        r = routes[li]
+        # same launch shape as the layer's unpermute (fp16 rows of h_ws as y)
+        r = rts[li]
         _lib.call("hn_moe_unpermute", _lib.ptr(h_ws), I, _lib.ptr(r.inv), _lib.ptr(r.idx),
                   _lib.ptr(r.w), T, k, None, H, _lib.ptr(out), H, H, sp)
 
     n_it = 4 * reps
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4 * n_it)]
     for it in range(4):  # warm-up
-        route(it % 4); phase(it % 4, 0); phase(it % 4, 1); unpermute(it % 4)
+        route_gate_up(it % 4); down(it % 4); unpermute(it % 4)
     torch.cuda.synchronize()
     for it in range(n_it):
         li = it % len(layers)
-        route(li)
         ev[4 * it].record()
-        phase(li, 0)
+        route_gate_up(li)
         ev[4 * it + 1].record()
         ev[4 * it + 2].record()
-        phase(li, 1)
+        down(li)
         ev[4 * it + 3].record()
         unpermute(li)
     torch.cuda.synchronize()
+    nact = [int(r.n_active.item()) for r in rts]
     t_gu = sum(ev[4 * it].elapsed_time(ev[4 * it + 1]) for it in range(n_it)) / n_it * 1e3
     t_dn = sum(ev[4 * it + 2].elapsed_time(ev[4 * it + 3]) for it in range(n_it)) / n_it * 1e3
     res = {}
     avg_act = sum(nact) / len(nact)
-    for name, us, nbytes in (("gate_up_silu", t_gu, avg_act * gu + n * H * 2 + n * I * 2),
+    for name, us, nbytes in (("route_gate_up_silu", t_gu,
+                              avg_act * gu + T * H * 2 + E * H * 2 + n * I * 2),
                              ("down_4slices", t_dn, avg_act * dn + n * I * 2 + 4 * n * H * 4)):
         res[name] = {"avg_us": round(us, 3), "bytes_per_launch": int(nbytes),
                      "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -528,45 +528,44 @@ def cpu_baseline_c1(ctx, budget_s: float):
 
 
 def c2phase(args):
-    """Counter run: 20 launches of the C2 T=16 grouped gate/up stream kernel, then 20
-    copies of 512 MiB (the copy calibrates FETCH_SIZE / WRITE_SIZE in bytes)."""
+    """Counter run: 20 launches of the C2 T=16 routing + gate/up stream kernel (the
+    roofline kernel), then 20 copies of 512 MiB (the copy calibrates FETCH_SIZE /
+    WRITE_SIZE in bytes)."""
     from hydranet_amd import _lib
-    from hydranet_amd.model.moe import MixtralMoELayer, moe_route
+    from hydranet_amd.model.moe import ExpertTable, Routed
     from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
     H, I, g, E, T, k = 4096, 14336, 128, 8, 16, 2
     slots = [make_expert_slot(expert_seed(0, e), H, I, g, slot_idx=e) for e in range(E)]
-    layer = MixtralMoELayer(H, E, k, slots=slots).cuda()
-    layer.router.gate.weight.data = normal_f16((E, H), 7000)
+    table = ExpertTable.from_slots(slots)
+    gate = normal_f16((E, H), 7000)
     x = normal_f16((T, H), 1234 + T, std=1.0)
-    r = moe_route(x, k, 0, gate_w=layer.router.gate.weight)
-    torch.cuda.synchronize()
-    maxr = int((r.offsets[1:] - r.offsets[:-1]).max().item())
+    r = Routed(T, k, E, 0, "cuda")
     n = T * k
     h_ws = torch.empty(n, I, dtype=torch.float16, device="cuda")
-    work = _lib.skinny_workspace(3, n, H, I, E, "cuda")
     for _ in range(20):
-        _lib.call("hn_grouped_decode_phase_int4", 0, _lib.ptr(r.x_perm),
-                  _lib.ptr(layer.experts.table.dev), _lib.ptr(r.active), _lib.ptr(r.n_active),
-                  _lib.ptr(r.offsets), E, maxr, n, H, I, g, _lib.ptr(h_ws), _lib.ptr(work),
-                  work.numel(), _lib.stream())
+        _lib.call("hn_moe_route_gate_up", _lib.ptr(x), H, _lib.ptr(gate), H, T, E, k,
+                  _lib.ptr(table.dev), H, I, g, 1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w),
+                  _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active),
+                  _lib.ptr(r.n_active), _lib.ptr(h_ws), _lib.stream())
     src = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(20):
         dst.copy_(src)
     torch.cuda.synchronize()
     lay = slots[0].layout
-    print(json.dumps({"workload": "c2phase", "active_experts": int(r.n_active.item()),
-                      "gate_up_bytes_per_launch": int(r.n_active.item()) * 2 * (
-                          lay.gate_packed_size + lay.gate_scales_size) + n * H * 2 + n * I * 2,
-                      "copy_bytes": src.numel() * 2}), flush=True)
+    na = int(r.n_active.item())
+    print(json.dumps({"workload": "c2phase", "active_experts": na,
+                      "route_gate_up_bytes_per_launch": na * 2 * (
+                          lay.gate_packed_size + lay.gate_scales_size) + T * H * 2 + E * H * 2
+                      + n * I * 2, "copy_bytes": src.numel() * 2}), flush=True)
 
 
-# HBM bytes per launch of the roofline kernel (grouped gate/up stream kernel, C2
-# T=16, 8 active experts): FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes
-# over `bench.py --workload c2phase`, each scaled by the same counter on a 512 MiB
-# copy.  Commands, raw counter values and scale factors:
-# profiles/stream_gate_up_c2_t16_traffic.md.  Re-measure after a kernel change.
-GATE_UP_C2_T16_TRAFFIC = 487_869_183
+# HBM bytes per launch of the roofline kernel (routing + grouped gate/up stream
+# kernel, C2 T=16, 8 active experts): FETCH_SIZE + WRITE_SIZE from two rocprofv3
+# --pmc passes over `bench.py --workload c2phase`, each scaled by the same
+# counter on a 512 MiB copy.  Commands, raw counter values and scale factors:
+# profiles/route_gate_up_c2_t16_traffic.md.  Re-measure after a kernel change.
+ROUTE_GATE_UP_C2_T16_TRAFFIC = 487_463_494
 
 
 def main():
@@ -633,16 +632,17 @@ def main():
         if ph is not None:
             # roofline of the dominant kernel of the headline workload: the grouped
             # gate/up + SiLU stream kernel over the active experts at T = 16
-            gu = ph["gate_up_silu"]
+            gu = ph["route_gate_up_silu"]
             res["c1_roofline"] = res.pop("roofline")
             res["roofline"] = {
-                "bound": "hbm", "kernel": "stream_kernel<grouped, gate+up+SiLU> (C2, T=16)",
+                "bound": "hbm",
+                "kernel": "stream_kernel<grouped, gate+up+SiLU, routing in the prologue> (C2, T=16)",
                 "achieved": gu["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
                 "bytes_per_launch": gu["bytes_per_launch"], "avg_us": gu["avg_us"],
                 "down": ph["down_4slices"], "active_experts": ph["active_experts"]}
             if ph["active_experts"] == 8:
-                res["roofline"]["traffic"] = GATE_UP_C2_T16_TRAFFIC
+                res["roofline"]["traffic"] = ROUTE_GATE_UP_C2_T16_TRAFFIC
         res["metric"] = METRIC
         res["value"] = head["GB_s"]
         res["ms_per_step"] = head["ms_per_step"]

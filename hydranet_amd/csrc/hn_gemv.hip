@@ -927,6 +927,26 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
   return rc;
 }
 
+// The first launch of hn_moe_decode_layer on its own: routing computed in the
+// grouped gate/up streaming kernel, h_ws = SwiGLU gate/up of the routed rows.
+extern "C" int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w, long ld_w,
+                                    long T, long E, long k, const void* table, long H, long I,
+                                    long group, float eps, float scaling, void* logits_out,
+                                    int* idx, void* w, int* offsets, int* perm, int* inv,
+                                    int* active, int* n_active, void* h_ws, void* stream) {
+  const char* who = "hn_moe_route_gate_up";
+  HN_ARG_CHECK(aligned16(h) && aligned16(gate_w) && aligned16(h_ws),
+               "%s: h, gate and h_ws rows must be 16-byte aligned", who);
+  HN_ARG_CHECK(g_decode_path == 0, "%s: needs the streaming kernels (decode path 0)", who);
+  const int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, T, E, k, table, H, I, group,
+                                              eps, scaling, (float*)logits_out, idx, w, offsets,
+                                              perm, inv, active, n_active, h_ws,
+                                              (hipStream_t)stream, 0);
+  HN_ARG_CHECK(rc != HN_NOT_HANDLED, "%s: shape not covered (T <= 16, E <= 8, k == 2, H %% 512 "
+               "== 0, group 128; T=%ld E=%ld k=%ld H=%ld group=%ld)", who, T, E, k, H, group);
+  return rc;
+}
+
 // One Mixtral MoE layer at decode in three launches: the routing (logits,
 // softmax top-2, permutation) computed inside the gate/up streaming kernel,
 // the down projection in four K slices, the ordered weighted unpermute.

@@ -156,6 +156,17 @@ int hn_moe_experts_decode(const void* x_perm, const void* table, const int* acti
                           long T, long k, const void* shared, long ld_sh, void* out, long ld_o,
                           void* work, long work_bytes, void* stream);
 
+/* The first launch of hn_moe_decode_layer alone: the routing computed in the
+ * grouped gate/up streaming kernel and h_ws [T k, I] = fp16(silu(fp16(x Wg^T))
+ * * fp16(x Wu^T)) for the routed rows (same arguments; for per-kernel timing
+ * and counter runs).  Replaces TopKRouter.forward and the gate/up half of the
+ * per-expert loop (model/router.py:96-120, model/mixtral.py:327-354). */
+int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w, long ld_w, long T, long E,
+                         long k, const void* table, long H, long I, long group, float eps,
+                         float scaling, void* logits_out, int* idx, void* w, int* offsets,
+                         int* perm, int* inv, int* active, int* n_active, void* h_ws,
+                         void* stream);
+
 /* One Mixtral MoE layer at decode (T <= 16 tokens, E <= 8 experts, top-2
  * softmax, fp16 gate [E, H], group 128, H and I multiples of 512) in three
  * launches: the routing (logits, top-k, stable permutation) computed inside
