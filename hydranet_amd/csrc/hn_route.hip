@@ -319,13 +319,25 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     float4_t acc[LG];
 #pragma unroll
     for (int u = 0; u < LG; ++u) acc[u] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int st = 0; st < steps; ++st) {
-      const half8_t b = *reinterpret_cast<const half8_t*>(bp + 32 * st);
+    // passes of up to KST steps whose loads go out together (steps past the
+    // slice repeat the last one and are not multiplied)
+    constexpr int KST = LG == 1 ? 8 : 4;
+    for (int s0 = 0; s0 < steps; s0 += KST) {
+      half8_t bv[KST], av[KST][LG];
 #pragma unroll
-      for (int u = 0; u < LG; ++u) {
-        const half8_t a = *reinterpret_cast<const half8_t*>(ap[u] + 32 * st);
-        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[u], 0, 0, 0);
+      for (int i = 0; i < KST; ++i) {
+        const int st = min(s0 + i, steps - 1);
+        bv[i] = *reinterpret_cast<const half8_t*>(bp + 32 * st);
+#pragma unroll
+        for (int u = 0; u < LG; ++u) av[i][u] = *reinterpret_cast<const half8_t*>(ap[u] + 32 * st);
+      }
+#pragma unroll
+      for (int i = 0; i < KST; ++i) {
+        if (s0 + i < steps) {  // uniform
+#pragma unroll
+          for (int u = 0; u < LG; ++u)
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i][u], bv[i], acc[u], 0, 0, 0);
+        }
       }
     }
     // lane: expert tl, tokens 16 u + 4 (lane >> 4) + r

@@ -425,20 +425,33 @@ __device__ int route_prologue(const StreamArgs& A, float* part, int* s_act, int*
     const int tl = lane & 15, kq = (lane >> 4) * 8;
     const h16* ap = A.hx + (long)min(tl, T - 1) * A.ld_hx + kq;
     const h16* bp = A.gate + (long)min(tl, E - 1) * A.ld_gate + kq;
-    // two slices per pass (sl0, sl0 + KW), their loads in flight together
+    // two slices per pass (sl0, sl0 + KW); each pass loads up to 8 steps of
+    // both slices into registers before the MFMAs (steps past the slice
+    // repeat the last one and are not multiplied), so the loads are in flight
+    // together instead of one round trip per step
+    constexpr int kSt = 8;
     for (int sl0 = wave; sl0 < 16; sl0 += 2 * KW) {
       const int sl1 = sl0 + KW;
       const bool has1 = sl1 < 16;  // uniform
       const int kb0 = sl0 * ksl, kb1 = (has1 ? sl1 : sl0) * ksl;
       float4_t acc0 = float4_t{0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-#pragma unroll 8
-      for (int st = 0; st < steps; ++st) {
-        const half8_t b0 = *reinterpret_cast<const half8_t*>(bp + kb0 + 32 * st);
-        const half8_t a0 = *reinterpret_cast<const half8_t*>(ap + kb0 + 32 * st);
-        const half8_t b1 = *reinterpret_cast<const half8_t*>(bp + kb1 + 32 * st);
-        const half8_t a1 = *reinterpret_cast<const half8_t*>(ap + kb1 + 32 * st);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc1, 0, 0, 0);
+      for (int s0 = 0; s0 < steps; s0 += kSt) {
+        half8_t a0[kSt], b0[kSt], a1[kSt], b1[kSt];
+#pragma unroll
+        for (int u = 0; u < kSt; ++u) {
+          const int st = min(s0 + u, steps - 1);
+          b0[u] = *reinterpret_cast<const half8_t*>(bp + kb0 + 32 * st);
+          a0[u] = *reinterpret_cast<const half8_t*>(ap + kb0 + 32 * st);
+          b1[u] = *reinterpret_cast<const half8_t*>(bp + kb1 + 32 * st);
+          a1[u] = *reinterpret_cast<const half8_t*>(ap + kb1 + 32 * st);
+        }
+#pragma unroll
+        for (int u = 0; u < kSt; ++u) {
+          if (s0 + u < steps) {  // uniform
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[u], b0[u], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[u], b1[u], acc1, 0, 0, 0);
+          }
+        }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
