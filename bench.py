@@ -438,6 +438,7 @@ def bench_c4(args):
     x_perm = torch.empty(n, H, dtype=torch.float16, device=dev)
     h_ws = torch.empty(n, I, dtype=torch.float16, device=dev)
     y_perm = torch.empty(n, H, dtype=torch.float16, device=dev)
+    work = _lib.gemm_workspace(dev)
     sp = ctypes_stream(st)
     torch.cuda.synchronize()
     _lib.call("hn_moe_permute", _lib.ptr(idx), T, k, E, _lib.ptr(offs), _lib.ptr(perm),
@@ -449,7 +450,7 @@ def bench_c4(args):
         def launch():
             _lib.call("hn_grouped_expert_phase_int4", phase, _lib.ptr(x_perm), _lib.ptr(table.dev),
                       _lib.ptr(act), _lib.ptr(nact), _lib.ptr(offs), E, n, H, I, g,
-                      _lib.ptr(h_ws), _lib.ptr(y_perm), sp)
+                      _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work), work.numel(), sp)
         for _ in range(2):
             launch()
         e0 = torch.cuda.Event(enable_timing=True)

@@ -36,12 +36,14 @@ SIGNATURES: dict[str, list] = {
     "hn_moe_unpermute": [P, L, P, P, P, L, L, P, L, P, L, L, P],
     "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],
     "hn_set_decode_path": [I],
-    "hn_grouped_expert_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, P, P, P],
+    "hn_gemm_workspace_bytes": [],
+    "hn_grouped_expert_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, P, P, P, L, P],
     "hn_moe_route": [P, L, P, L, I, P, P, L, L, L, L, I, F, F, P, P, P, P, P, P, P, P, P, L,
                      P],
     "hn_moe_experts_decode": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, P, P, L, L, P, L, P, L,
                               P, L, P],
     "hn_grouped_decode_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, L, P, P, L, P],
+    "hn_moe_decode_layer_check": [L, L, L, L, L, L],
     "hn_moe_route_gate_up": [P, L, P, L, L, L, L, P, L, L, L, F, F, P, P, P, P, P, P, P, P, P,
                              P],
     "hn_moe_decode_layer": [P, L, P, L, L, L, L, P, L, L, L, F, F, P, P, P, P, P, P, P, P, P,
@@ -53,7 +55,7 @@ SIGNATURES: dict[str, list] = {
 ROUTE_MAX_LOGITS = 8192   # T * E
 ROUTE_MAX_ASSIGN = 1024   # T * k
 
-RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long}
+RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long, "hn_gemm_workspace_bytes": ctypes.c_long}
 
 # Tokens per weight matrix up to which the decode (skinny / streaming) kernels
 # run; above it the MFMA GEMM kernels do (kMaxRows in csrc/hn_gemv.hip).
@@ -121,6 +123,11 @@ def workspace(nbytes: int, device) -> torch.Tensor:
 
 def skinny_workspace(kind: int, M: int, N: int, K: int, E: int, device) -> torch.Tensor:
     return workspace(lib().hn_skinny_workspace_bytes(kind, M, N, K, E), device)
+
+
+def gemm_workspace(device) -> torch.Tensor:
+    """Workspace of the prefill GEMM kernels' stream-K split (about 128 MiB)."""
+    return workspace(lib().hn_gemm_workspace_bytes(), device)
 
 
 

@@ -36,7 +36,8 @@
 
 namespace {
 
-constexpr int kBM = 128;          // tokens per tile
+constexpr int kRBMax = 8;         // 32-token row blocks of the largest tile
+constexpr int kBMMax = 32 * kRBMax;  // tokens per tile, at most
 constexpr int kWaves = 4;         // waves per workgroup (split N)
 constexpr int kMaxProb = 256;     // experts per grouped launch
 constexpr int kSuperM = 8;        // M-tiles per super-block
@@ -59,6 +60,12 @@ struct GemmArgs {
   int ld_q;         // packed row stride (bytes)
   int ld_s;         // scale row stride (elements)
   uint32_t m_pair, magic;
+  // stream-K (part != nullptr): the workgroups split the (tile, k-stage)
+  // iterations evenly; a tile whose stages span several workgroups is summed
+  // from fp32 partial slots by the last of them to arrive (per wave).
+  float* part;      // [4 * grid][kWaves][kWaveSlot]
+  int* ctr;         // [tiles * kWaves], zero between launches
+  int sk_ch;        // stages per stream-K chunk (chunks start on whole scale groups)
 };
 
 struct Prob {
@@ -142,7 +149,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // of stages t + 1 and t + 2 in flight while stage t computes.
 // ---------------------------------------------------------------------------
 #ifndef HN_GEMM_KSM
-#define HN_GEMM_KSM 2         // k per stage = 64 * KSM
+#define HN_GEMM_KSM 1         // k per stage = 64 * KSM
 #endif
 #ifndef HN_GEMM_OCC
 #define HN_GEMM_OCC 1         // workgroups per CU (waves per SIMD)
@@ -155,18 +162,20 @@ constexpr int kSteps = 4 * kKSM;   // MFMA k-steps (16 k) per stage
 constexpr int kChunks = 8 * kKSM;  // 16-byte activation chunks per row per stage
 constexpr int kNST = 3;            // LDS stages
 
-// LDS stage (bytes): activations [128 rows][kChunks chunks of 16 B], chunk c of
+// LDS stage (bytes): activations [256 rows][kChunks chunks of 16 B], chunk c of
 // row r at slot c ^ key(r), so the 8 or 16 rows an A-fragment read serves per
 // LDS cycle hit distinct banks; packed weights [wave][block][d][lane] 16 B;
 // scale dwords [wave][block][lane] 4 B.
 struct Stage {
   static constexpr int kA = 0;
-  static constexpr int kB = kBM * kChunks * 16;
+  static constexpr int kB = kBMMax * kChunks * 16;
   static constexpr int kS = kB + kWaves * kBlk * kKSM * 1024;
   static constexpr int kSize = kS + kWaves * kBlk * 256;
 };
-constexpr int kALoads = kChunks * kBM / (kWaves * 64);         // activation loads per lane
-constexpr int kLoadsPerStage = kALoads + kBlk * kKSM + kBlk;   // + weights + scales
+// activation loads per lane for a tile of NRB row blocks; loads per stage
+template <int NRB> constexpr int a_loads() { return kChunks * 32 * NRB / (kWaves * 64); }
+template <int NRB> constexpr int loads_per_stage() { return a_loads<NRB>() + kBlk * kKSM + kBlk; }
+constexpr int kALoadsMax = a_loads<kRBMax>();
 
 __device__ __forceinline__ int akey(int r) {
   return kChunks == 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
@@ -181,18 +190,19 @@ struct TileLoads {
   const void* pq[kBlk];               // packed weights of each block's matrix
   const void* ps[kBlk];               // scales
   int nq, ns;                         // bytes of one packed / scale matrix
-  uint32_t va[kALoads];               // activation chunk offsets
+  uint32_t va[kALoadsMax];            // activation chunk offsets (first a_loads<NRB>)
   uint32_t vq[kBlk];                  // weight byte offset of (lane's row, lane's 16 B)
   uint32_t vs[kBlk];                  // scale byte offset of (lane's row, lane's k)
   int group;
 };
 
-// Activation loads: wave w issues kALoads loads of 64 consecutive LDS chunks
-// (1 KiB each); LDS chunk L = (row r, slot c') holds global chunk c' ^ key(r)
-// of row r.  Rows past the valid ones repeat the last valid row (their
-// results are never stored).
+// Activation loads: wave w issues a_loads<NRB> loads of 64 consecutive LDS
+// chunks (1 KiB each); LDS chunk L = (row r, slot c') holds global chunk
+// c' ^ key(r) of row r.  Rows past the valid ones repeat the last valid row
+// (their results are never stored).
+template <int NRB>
 __device__ __forceinline__ uint32_t a_offset(int j, int wave, int lane, int rows, long ld_x) {
-  const int L = (wave * kALoads + j) * 64 + lane;
+  const int L = (wave * a_loads<NRB>() + j) * 64 + lane;
   const int r = L / kChunks;
   const int c = (L % kChunks) ^ akey(r);
   return (uint32_t)((min(r, rows - 1) * (int)ld_x + 8 * c) * 2);
@@ -202,13 +212,15 @@ __device__ __forceinline__ uint32_t a_offset(int j, int wave, int lane, int rows
 // block kKSM loads; load d brings lane l's 16 bytes at 16 kKSM (l / 32) + 16 d
 // of row (l % 32)'s 32 kKSM bytes of the stage.  Scales: the dword holding the
 // lane's scale.
+template <int NRB>
 __device__ __forceinline__ void issue_stage(const TileLoads& tl, int t, uint32_t st, int wave) {
   using L = Stage;
+  constexpr int NA = a_loads<NRB>();
   {
     const __amdgpu_buffer_rsrc_t r = rsrc(tl.px, tl.nx);
 #pragma unroll
-    for (int j = 0; j < kALoads; ++j)
-      dma_b128(r, tl.va[j], 2 * kKS * t, st + L::kA + (wave * kALoads + j) * 1024);
+    for (int j = 0; j < NA; ++j)
+      dma_b128(r, tl.va[j], 2 * kKS * t, st + L::kA + (wave * NA + j) * 1024);
   }
 #pragma unroll
   for (int b = 0; b < kBlk; ++b) {
@@ -264,7 +276,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 struct Ops {
   uint32_t pk[kBlk][kSteps];  // packed weights of the current stage, one dword per step
   half2_t s2[kBlk];       // scales, both halves
-  half8_t af[2][4];       // A fragments of the 4 row blocks
+  half8_t af[2][kRBMax];  // A fragments of the row blocks
   half8_t bw[2][kBlk];    // unpacked weights
 };
 
@@ -272,10 +284,12 @@ __device__ __forceinline__ uint32_t a_addr(uint32_t st, int s, int row32, int h)
   return st + row32 * (kChunks * 16) + (((h * kSteps + s) ^ akey(row32)) << 4);
 }
 
+template <int NRB>
 __device__ __forceinline__ void read_a(Ops& o, int buf, uint32_t st, int s, int row32, int h) {
   const uint32_t base = a_addr(st, s, row32, h);
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) o.af[buf][rb] = lds_read<half8_t>(base + rb * 32 * kChunks * 16);
+  for (int rb = 0; rb < NRB; ++rb)
+    o.af[buf][rb] = lds_read<half8_t>(base + rb * 32 * kChunks * 16);
 }
 
 // Weights + scales of the stage at st (stage number t); half-word of each
@@ -305,24 +319,25 @@ __device__ __forceinline__ void deq_step(Ops& o, int buf, int s, const DeqRegs& 
   for (int b = 0; b < kBlk; ++b) o.bw[buf][b] = deq8(o.pk[b][s], dr, o.s2[b]);
 }
 
-__device__ __forceinline__ void mfma_step(const Ops& o, int buf, f32x16 (&acc)[4][kBlk]) {
+template <int NRB>
+__device__ __forceinline__ void mfma_step(const Ops& o, int buf, f32x16 (&acc)[kRBMax][kBlk]) {
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
     for (int b = 0; b < kBlk; ++b)
       acc[rb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.af[buf][rb], o.bw[buf][b], acc[rb][b],
                                                           0, 0, 0);
 }
 
-// Interleave hint for one step: LDS reads first, then 4 kBlk x (1 MFMA,
-// 4 VALU) -- the next step's unpack under this step's MFMAs.
-template <int NDS>
+// Interleave hint for one step: LDS reads first, then NRB kBlk x (1 MFMA,
+// 16 / NRB VALU) -- the next step's unpack under this step's MFMAs.
+template <int NRB, int NDS>
 __device__ __forceinline__ void sched_step() {
   if (NDS) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // DS read
 #pragma unroll
-  for (int i = 0; i < 4 * kBlk; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+  for (int i = 0; i < NRB * kBlk; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 16 / NRB, 0);   // VALU
   }
 }
 
@@ -331,61 +346,144 @@ __device__ __forceinline__ void sched_step() {
 // step the wave waits for its own loads of stage t + 1 (those of t + 2 stay in
 // flight), reads that stage's weights and unpacks its first step; the barrier
 // then makes every wave's activation loads of t + 1 visible.
-__device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int T, uint32_t lds0,
+template <int NRB>
+__device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int te, uint32_t lds0,
                                        int row32, int h, int wave, int lane, const DeqRegs& dr,
-                                       f32x16 (&acc)[4][kBlk]) {
+                                       f32x16 (&acc)[kRBMax][kBlk]) {
   using L = Stage;
+  constexpr int LPS = loads_per_stage<NRB>();
   Ops o;
-  issue_stage(tl, tb, lds0, wave);
-  if (tb + 1 < T) {
-    issue_stage(tl, tb + 1, lds0 + L::kSize, wave);
-    wait_vmcnt<kLoadsPerStage>();
+  issue_stage<NRB>(tl, tb, lds0, wave);
+  if (tb + 1 < te) {
+    issue_stage<NRB>(tl, tb + 1, lds0 + L::kSize, wave);
+    wait_vmcnt<LPS>();
   } else {
     wait_vmcnt<0>();
   }
   __syncthreads();
   read_b(o, tl, lds0, tb, wave, lane);
   deq_step(o, 0, 0, dr);
-  read_a(o, 0, lds0, 0, row32, h);
+  read_a<NRB>(o, 0, lds0, 0, row32, h);
   int sc = 0;  // LDS stage of stage t
-  for (int t = tb; t < T; ++t) {
+  for (int t = tb; t < te; ++t) {
     const int s1 = sc + 1 == kNST ? 0 : sc + 1;
     const int s2 = s1 + 1 == kNST ? 0 : s1 + 1;
     const uint32_t cur = lds0 + sc * L::kSize;
     const uint32_t nxt = lds0 + s1 * L::kSize;
-    const bool ahead = t + 2 < T;  // uniform
-    if (ahead) issue_stage(tl, t + 2, lds0 + s2 * L::kSize, wave);
+    const bool ahead = t + 2 < te;  // uniform
+    if (ahead) issue_stage<NRB>(tl, t + 2, lds0 + s2 * L::kSize, wave);
 #pragma unroll
     for (int s = 0; s < kSteps - 1; ++s) {
       // step s + 1's A fragments are requested before step s's MFMAs (the
       // scheduling fences keep them there); its unpack runs under them
-      read_a(o, (s + 1) & 1, cur, s + 1, row32, h);
+      read_a<NRB>(o, (s + 1) & 1, cur, s + 1, row32, h);
       __builtin_amdgcn_sched_barrier(0);
       deq_step(o, (s + 1) & 1, s + 1, dr);
-      mfma_step(o, s & 1, acc);
-      sched_step<0>();
+      mfma_step<NRB>(o, s & 1, acc);
+      sched_step<NRB, 0>();
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (ahead) wait_vmcnt<kLoadsPerStage>();
+    if (ahead) wait_vmcnt<LPS>();
     else wait_vmcnt<0>();
     read_b(o, tl, nxt, t + 1, wave, lane);
     deq_step(o, 0, 0, dr);
-    mfma_step(o, 1, acc);
-    sched_step<kBlk * kKSM + kBlk>();
+    mfma_step<NRB>(o, 1, acc);
+    sched_step<NRB, kBlk * kKSM + kBlk>();
     __syncthreads();
-    if (t + 1 < T) read_a(o, 0, nxt, 0, row32, h);
+    if (t + 1 < te) read_a<NRB>(o, 0, nxt, 0, row32, h);
     sc = s1;
   }
 }
 
-template <bool GROUPED, int MATS>
+// Stream-K partial slots: one wave's accumulators (kRBMax x kBlk 32x32 fp32
+// blocks), lane-interleaved so every store / load instruction is coalesced.
+constexpr long kWaveSlot = (long)kRBMax * kBlk * 16 * 64;  // floats
+
+// Stream-K: the iterations (tile, stage) are split evenly over the ranks
+// 0..nr-1 (rank r: [it_total r / nr, it_total (r + 1) / nr)); nr <= it_total,
+// so no range is empty and a tile's segments belong to consecutive ranks.
+// A tile whose stages belong to several ranks ("segments") is finished by the
+// wave that arrives last: every segment stores its fp32 partial (relaxed
+// agent-scope atomics: coherent across XCDs without L2 write-back), then
+// counts itself in; the last one sums all the partials from the slots in
+// segment order (deterministic) and resets the counter.
+struct SkSeg {
+  int wf, nseg;  // first rank of the tile's segments, their number
+};
+
+__device__ __forceinline__ long sk_slot(int r, int tile, int pass, int T, long it_total, int nr) {
+  // a rank's slot for a tile of a pass: 4 r + 2 pass, + 1 unless the tile is
+  // the rank's first of the pass
+  const long br = it_total * r / nr;
+  return 4L * r + 2 * pass + (br / T == tile ? 0 : 1);
+}
+
+// Stores this wave's partial and counts it in.  True when it was the last
+// segment of the tile (the caller then finishes the tile from the slots).
+template <int RBM>
+__device__ __forceinline__ bool streamk_arrive(const GemmArgs& A, const f32x16 (&acc)[kRBMax][kBlk],
+                                               int nrb, int tile, int ctile, int pass, int T,
+                                               long it_total, int nr, int rank, int wave,
+                                               int lane, SkSeg& sgi) {
+  const long i0 = (long)tile * T, i1 = i0 + T - 1;
+  // rank owning iteration i: the largest r with it_total r / nr <= i
+  auto owner = [&](long i) { return (int)(((i + 1) * nr + it_total - 1) / it_total - 1); };
+  sgi.wf = owner(i0);
+  sgi.nseg = owner(i1) - sgi.wf + 1;
+  float* mine =
+      A.part + (sk_slot(rank, tile, pass, T, it_total, nr) * kWaves + wave) * kWaveSlot;
+#pragma unroll
+  for (int rb = 0; rb < RBM; ++rb)
+    if (rb < nrb)  // uniform
+#pragma unroll
+      for (int b = 0; b < kBlk; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          __hip_atomic_store(mine + ((rb * kBlk + b) * 16 + r) * 64 + lane, acc[rb][b][r],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  int* c = A.ctr + (long)ctile * kWaves + wave;
+  int last = 0;
+  if (lane == 0)
+    last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           sgi.nseg - 1;
+  last = __builtin_amdgcn_readfirstlane(last);
+  if (last && lane == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last != 0;
+}
+
+// The sum over the tile's segments of one accumulator register r of block
+// (rb, b), in segment order.
+__device__ __forceinline__ void sk_sum16(const GemmArgs& A, const SkSeg& sgi, int tile, int pass,
+                                         int T, long it_total, int nr, int wave, int lane,
+                                         int rb, int b, float (&v)[16]) {
+  for (int sg = 0; sg < sgi.nseg; ++sg) {
+    const float* src =
+        A.part + (sk_slot(sgi.wf + sg, tile, pass, T, it_total, nr) * kWaves + wave) * kWaveSlot +
+                       (long)(rb * kBlk + b) * 16 * 64 + lane;
+    float pv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      pv[r] = __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = sg == 0 ? pv[r] : v[r] + pv[r];
+  }
+}
+
+// RBM: row blocks of 32 tokens per M-tile (4 or 8).  With 8, a tile whose
+// rows fit in 128 runs the 4-block K loop (no MFMAs or loads for absent
+// rows beyond that granularity).
+template <bool GROUPED, int MATS, int RBM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOccW))) void gemm_kernel(
     GemmArgs A, const GExpert* __restrict__ table, const int* __restrict__ active,
     const int* __restrict__ n_active, const int* __restrict__ offsets) {
+  static_assert(RBM == 4 || RBM == 8, "M-tile of 128 or 256 tokens");
+  constexpr int BM = 32 * RBM;
   constexpr int WN = kWaves * 32 * kBlk / MATS;  // output columns per tile
   using L = Stage;
   __shared__ __align__(16) unsigned char lds[kNST * L::kSize];
   __shared__ int toff[kMaxProb + 1];
+  __shared__ int thalf[kMaxProb + 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -401,80 +499,165 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
   dr.mul = hn_vgpr(0x2C003C00u);  // half2(1, 0.0625)
   dr.add = hn_vgpr(0xD480E408u);  // half2(-1032, -72)
 
-  // ---- M-tiles per problem -> prefix toff[]
+  // ---- M-tiles per problem: toff[] = prefix of the full ones, thalf[] of
+  //      the short remainders (RBM 8: a last M-tile of <= 128 rows, run by the
+  //      4-block K loop at about half the cost).  The work is two passes, the
+  //      full tiles, then the short ones, each spread evenly over the
+  //      workgroups.
   int nprob = 1;
+  auto count = [&](int rows_p, int& nf, int& nh) {
+    const int mt = (rows_p + BM - 1) / BM;
+    const int rem = rows_p - (mt - 1) * BM;
+    nh = (RBM == 8 && mt > 0 && rem <= 128) ? 1 : 0;
+    nf = mt - nh;
+  };
   if (GROUPED) {
     nprob = min(*n_active, kMaxProb);
     for (int i = tid; i < nprob; i += blockDim.x) {
       const int e = active[i];
-      toff[i + 1] = (offsets[e + 1] - offsets[e] + kBM - 1) / kBM;
+      int nf, nh;
+      count(offsets[e + 1] - offsets[e], nf, nh);
+      toff[i + 1] = nf;
+      thalf[i + 1] = nh;
     }
     __syncthreads();
     if (tid == 0) {
       toff[0] = 0;
-      for (int i = 1; i <= nprob; ++i) toff[i] += toff[i - 1];
+      thalf[0] = 0;
+      for (int i = 1; i <= nprob; ++i) {
+        toff[i] += toff[i - 1];
+        thalf[i] += thalf[i - 1];
+      }
     }
   } else if (tid == 0) {
+    int nf, nh;
+    count(A.M, nf, nh);
     toff[0] = 0;
-    toff[1] = (A.M + kBM - 1) / kBM;
+    toff[1] = nf;
+    thalf[0] = 0;
+    thalf[1] = nh;
   }
   __syncthreads();
   if (nprob <= 0) return;
-  const int total = __builtin_amdgcn_readfirstlane(toff[nprob]) * NT;
+  const int tot_f = __builtin_amdgcn_readfirstlane(toff[nprob]) * NT;   // full tiles
+  const int tot_h = __builtin_amdgcn_readfirstlane(thalf[nprob]) * NT;  // short tiles
   const int nwg = gridDim.x;
   const int bid = blockIdx.x;
   // workgroups are dealt round-robin to the 8 XCDs: give each XCD a
   // contiguous run of tile numbers
   const int vid = (nwg % 8 == 0) ? (bid % 8) * (nwg / 8) + bid / 8 : bid;
 
-  for (int tile = vid; tile < total; tile += nwg) {
+  // Work items: whole tiles round-robin, or (stream-K) this rank's range of
+  // (tile, chunk of A.sk_ch stages) iterations of each pass, ranks = min(grid,
+  // iterations) so that no range is empty and a tile's segments belong to
+  // consecutive ranks.  A segment starts the K loop at stage 0 of tile
+  // pointers moved to its first chunk (whole scale dwords), so the loop never
+  // starts at a run-time stage.
+  const bool sk = A.part != nullptr;
+  const int CH = sk ? A.sk_ch : T;
+  const int NCH = T / CH;  // chunks per tile
+  int pass = 0;
+  long it = 0, it_end = 0, it_total = 0;
+  int nr = 1;
+  int tile_rr = vid;
+  auto start_pass = [&](int ps) {
+    pass = ps;
+    const int tot = ps == 0 ? tot_f : tot_h;
+    it_total = (long)tot * NCH;
+    nr = (int)max(1L, min((long)nwg, it_total));
+    it = sk && vid < nr ? it_total * vid / nr : 0;
+    it_end = sk && vid < nr ? it_total * (vid + 1) / nr : 0;
+    tile_rr = vid;
+  };
+  start_pass(0);
+  while (true) {
+    int tile, c0, c1;
+    if (sk) {
+      if (it >= it_end) {
+        if (pass == 0) { start_pass(1); continue; }
+        break;
+      }
+      tile = (int)(it / NCH);
+      c0 = (int)(it - (long)tile * NCH);
+      c1 = (int)min((long)NCH, (long)c0 + (it_end - it));
+      it += c1 - c0;
+    } else {
+      if (tile_rr >= (pass == 0 ? tot_f : tot_h)) {
+        if (pass == 0) { start_pass(1); continue; }
+        break;
+      }
+      tile = tile_rr;
+      c0 = 0;
+      c1 = NCH;
+      tile_rr += nwg;
+    }
+    tile = __builtin_amdgcn_readfirstlane(tile);
+    c0 = __builtin_amdgcn_readfirstlane(c0);
+    c1 = __builtin_amdgcn_readfirstlane(c1);
+    const int k0 = c0 * CH * kKS;               // first k of this segment
+    const int nst = (c1 - c0) * CH;              // its stages
     // ---- tile -> (problem, m-tile, n-tile)
+    const int* pref = pass == 0 ? toff : thalf;
     int p = 0;
     {
-      const int mg = tile / NT;  // toff[p] <= mg < toff[p + 1]
+      const int mg = tile / NT;  // pref[p] <= mg < pref[p + 1]
       int lo = 0, hi = nprob - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (toff[mid] <= mg) lo = mid; else hi = mid - 1;
+        if (pref[mid] <= mg) lo = mid; else hi = mid - 1;
       }
       p = __builtin_amdgcn_readfirstlane(lo);  // uniform: keep the tile state in SGPRs
     }
-    const int pt0 = __builtin_amdgcn_readfirstlane(toff[p]);
-    const int mtp = __builtin_amdgcn_readfirstlane(toff[p + 1]) - pt0;
-    const int local = tile - pt0 * NT;
-    const int sb = local / (kSuperM * NT);           // super-block
-    const int sm0 = sb * kSuperM;
-    const int sbm = min(kSuperM, mtp - sm0);         // M-tiles in this super-block
-    const int inb = local - sb * kSuperM * NT;
-    const int mtile = sm0 + inb % sbm;
-    const int ntile = inb / sbm;
+    int mtile, ntile;
+    if (pass == 0) {
+      const int pt0 = __builtin_amdgcn_readfirstlane(toff[p]);
+      const int mtp = __builtin_amdgcn_readfirstlane(toff[p + 1]) - pt0;
+      const int local = tile - pt0 * NT;
+      const int sb = local / (kSuperM * NT);           // super-block
+      const int sm0 = sb * kSuperM;
+      const int sbm = min(kSuperM, mtp - sm0);         // M-tiles in this super-block
+      const int inb = local - sb * kSuperM * NT;
+      mtile = sm0 + inb % sbm;
+      ntile = inb / sbm;
+    } else {
+      // the problem's short M-tile comes after its full ones
+      mtile = __builtin_amdgcn_readfirstlane(toff[p + 1] - toff[p]);
+      ntile = tile - __builtin_amdgcn_readfirstlane(thalf[p]) * NT;
+    }
+    const int ctile = pass == 0 ? tile : tot_f + tile;  // counter index
     const Prob pr = resolve<GROUPED>(A, table, active, offsets, p);
-    const int m0 = mtile * kBM;
-    const int rows = min(kBM, pr.rows - m0);
+    const int m0 = mtile * BM;
+    const int rows = min(BM, pr.rows - m0);
+    const bool full = RBM == 8 && rows > 128;  // uniform: the 8-block K loop
     // output column of this lane in block 0
     const int n0 = ntile * WN + wave * 32 * kBlk / MATS + row32;
 
     TileLoads tl;
-    tl.px = pr.x + (long)m0 * A.ld_x;
-    tl.nx = (int)(rows * A.ld_x * 2);
+    tl.px = pr.x + (long)m0 * A.ld_x + k0;
+    tl.nx = (int)(rows * A.ld_x * 2 - 2 * k0);
+    if (full) {
 #pragma unroll
-    for (int j = 0; j < kALoads; ++j) tl.va[j] = a_offset(j, wave, lane, rows, A.ld_x);
-    tl.nq = N * A.ld_q;
-    tl.ns = N * A.ld_s * 2;
+      for (int j = 0; j < a_loads<8>(); ++j) tl.va[j] = a_offset<8>(j, wave, lane, rows, A.ld_x);
+    } else {
+#pragma unroll
+      for (int j = 0; j < a_loads<4>(); ++j) tl.va[j] = a_offset<4>(j, wave, lane, rows, A.ld_x);
+    }
+    tl.nq = N * A.ld_q - k0 / 2;
+    tl.ns = (N * A.ld_s - k0 / A.group) * 2;
     tl.group = A.group;
 #pragma unroll
     for (int b = 0; b < kBlk; ++b) {
       const int mt = MATS == 2 ? b : 0;
       const int row = MATS == 2 ? n0 : n0 + 32 * b;
-      tl.pq[b] = pr.q[mt];
-      tl.ps[b] = pr.s[mt];
+      tl.pq[b] = pr.q[mt] + k0 / 2;
+      tl.ps[b] = pr.s[mt] + k0 / A.group;
       const bool ok = row < N;
       tl.vq[b] = ok ? (uint32_t)(row * A.ld_q + 16 * kKSM * h) : kOOB;
       tl.vs[b] = ok ? (uint32_t)(2 * (row * A.ld_s + (A.group == 32 * kKSM ? h : 0))) : kOOB;
     }
-    f32x16 acc[4][kBlk];
+    f32x16 acc[kRBMax][kBlk];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RBM; ++rb)
 #pragma unroll
       for (int b = 0; b < kBlk; ++b)
 #pragma unroll
@@ -482,7 +665,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
 
     // the previous tile's last reads of the stages end before anyone restages
     __syncthreads();
-    k_loop(tl, 0, T, lds0, row32, h, wave, lane, dr, acc);
+    if constexpr (RBM == 8) {
+      if (full) k_loop<8>(tl, 0, nst, lds0, row32, h, wave, lane, dr, acc);
+      else k_loop<4>(tl, 0, nst, lds0, row32, h, wave, lane, dr, acc);
+    } else {
+      k_loop<4>(tl, 0, nst, lds0, row32, h, wave, lane, dr, acc);
+    }
+    if (c0 != 0 || c1 != NCH) {  // a segment of the tile (uniform)
+      SkSeg sgi;
+      if (!streamk_arrive<RBM>(A, acc, full ? 8 : 4, tile, ctile, pass, NCH, it_total, nr, vid,
+                               wave, lane, sgi))
+        continue;  // another segment finishes this wave's part of the tile
+      // last segment: the epilogue from the partial slots (acc no longer used)
+#pragma unroll 1
+      for (int rb = 0; rb < (full ? 8 : 4); ++rb) {
+#pragma unroll
+        for (int ob = 0; ob < kBlk / MATS; ++ob) {
+          const int n = n0 + 32 * ob;
+          float g[16], u[16];
+          sk_sum16(A, sgi, tile, pass, NCH, it_total, nr, wave, lane, rb, MATS == 2 ? 0 : ob, g);
+          if (MATS == 2) sk_sum16(A, sgi, tile, pass, NCH, it_total, nr, wave, lane, rb, 1, u);
+          if (n < N) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int m = 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3);
+              if (m < rows) {
+                h16 o;
+                if (MATS == 2) {
+                  const float gv = (float)(h16)g[r];
+                  const float uv = (float)(h16)u[r];
+                  o = (h16)(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
+                } else {
+                  o = (h16)g[r];
+                }
+                pr.out[(long)(m0 + m) * A.ld_o + n] = o;
+              }
+            }
+          }
+        }
+      }
+      continue;
+    }
 
     // ---- epilogue: lane holds column n, tokens 32 rb + 8 (r / 4) + 4 h + r % 4
 #pragma unroll
@@ -490,7 +713,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
       const int n = n0 + 32 * ob;
       if (n < N) {
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < RBM; ++rb) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int m = 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -536,11 +759,49 @@ void fill_consts(GemmArgs& A) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 constexpr int kOcc = kOccW;  // workgroups per CU
+#ifndef HN_GEMM_RB_GU
+#define HN_GEMM_RB_GU 8
+#endif
+#ifndef HN_GEMM_RB_DN
+#define HN_GEMM_RB_DN 8
+#endif
+constexpr int kRBGateUp = HN_GEMM_RB_GU;  // row blocks per M-tile, grouped gate/up
+constexpr int kRBDown = HN_GEMM_RB_DN;    // and grouped down
 
 // Workgroups: OCC per CU, fewer when there are fewer tiles.
 int grid_for(long tiles_upper) {
   const long cap = (long)kOcc * num_cus();
   return (int)(tiles_upper < cap ? (tiles_upper < 1 ? 1 : tiles_upper) : cap);
+}
+
+// Stream-K workspace: per-(tile, wave) counters, then four partial slots per
+// workgroup of the full grid (the first and last tile of each pass).
+constexpr long kSkCounters = 1L << 16;          // tiles * kWaves
+constexpr long kSkCtrBytes = kSkCounters * 4;
+constexpr int kSkMaxGrid = 256;   // workgroups (one per CU on MI355X)
+
+long sk_bytes() { return kSkCtrBytes + 4L * kSkMaxGrid * kWaves * kWaveSlot * 4; }
+
+// Stream-K over the full grid when the workspace holds its counters and slots
+// (then every CU takes an equal share of the k-stages, tiles split at the
+// shares' ends); else whole tiles round-robin.
+bool sk_setup(GemmArgs& A, void* work, long work_bytes, long tiles_upper, dim3& grid) {
+  const int g = kOcc * num_cus();
+  if (!work || work_bytes < sk_bytes() || tiles_upper * kWaves > kSkCounters || g > kSkMaxGrid)
+    return false;
+  // chunk: the largest divisor of the stages per tile up to 16 whose k span
+  // is an even number of scale groups (segment pointers then move by whole
+  // scale dwords)
+  const int T = A.K / kKS;
+  int ch = 0;
+  for (int c = T < 16 ? T : 16; c >= 1; --c)
+    if (T % c == 0 && (c * kKS) % (2 * A.group) == 0) { ch = c; break; }
+  if (ch == 0) return false;
+  A.sk_ch = ch;
+  A.ctr = (int*)work;
+  A.part = (float*)((char*)work + kSkCtrBytes);
+  grid = dim3(g);
+  return true;
 }
 
 
@@ -563,13 +824,18 @@ static int gemm_shape_ok(long N, long K, long group, long ld_q, long ld_s) {
 // Single problem: out[M, N] = x @ deq(W)^T (mats 1) or the SwiGLU h (mats 2).
 // Returns HN_NOT_HANDLED when the shape is not handled here, 0 after a launch,
 // a HIP error code when the launch failed.
+// Bytes of workspace for the stream-K split (a caller's workspace of at least
+// this size enables it; the counters must be zero at the first use and are
+// left at zero).
+extern "C" long hn_gemm_workspace_bytes() { return sk_bytes(); }
+
 extern "C" int hn_gemm_linear_impl(int mats, const void* x, long ld_x, const void* q0,
                                    const void* s0, const void* q1, const void* s1, long ld_q,
                                    long ld_s, void* out, long ld_o, long M, long N, long K,
-                                   long group, void* stream) {
+                                   long group, void* work, long work_bytes, void* stream) {
   if (!gemm_shape_ok(N, K, group, ld_q, ld_s)) return HN_NOT_HANDLED;
   if (!aligned16(x) || ld_x % 8 != 0 || !aligned16(q0) || !aligned16(q1)) return HN_NOT_HANDLED;
-  if (ld_x * 2 * kBM >= (long)kOOB) return HN_NOT_HANDLED;
+  if (ld_x * 2 * kBMMax >= (long)kOOB) return HN_NOT_HANDLED;
   if (M <= 0 || N <= 0) return 0;
   GemmArgs A = {};
   A.x = (const h16*)x;
@@ -586,14 +852,22 @@ extern "C" int hn_gemm_linear_impl(int mats, const void* x, long ld_x, const voi
   A.ld_s = (int)ld_s;
   fill_consts(A);
   const long wn = kWaves * 32 * kBlk / mats;
-  const long tiles = ((M + kBM - 1) / kBM) * ((N + wn - 1) / wn);
+  const long bm = M > 128 ? 256 : 128;  // M-tile
+  const long tiles = ((M + bm - 1) / bm) * ((N + wn - 1) / wn);
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(grid_for(tiles));
-  if (mats == 2)
-    hipLaunchKernelGGL((gemm_kernel<false, 2>), grid, dim3(256), 0, s, A, nullptr, nullptr,
+  dim3 grid(grid_for(tiles));
+  sk_setup(A, work, work_bytes, tiles, grid);
+  if (mats == 2 && bm == 256)
+    hipLaunchKernelGGL((gemm_kernel<false, 2, 8>), grid, dim3(256), 0, s, A, nullptr, nullptr,
+                       nullptr, nullptr);
+  else if (mats == 2)
+    hipLaunchKernelGGL((gemm_kernel<false, 2, 4>), grid, dim3(256), 0, s, A, nullptr, nullptr,
+                       nullptr, nullptr);
+  else if (bm == 256)
+    hipLaunchKernelGGL((gemm_kernel<false, 1, 8>), grid, dim3(256), 0, s, A, nullptr, nullptr,
                        nullptr, nullptr);
   else
-    hipLaunchKernelGGL((gemm_kernel<false, 1>), grid, dim3(256), 0, s, A, nullptr, nullptr,
+    hipLaunchKernelGGL((gemm_kernel<false, 1, 4>), grid, dim3(256), 0, s, A, nullptr, nullptr,
                        nullptr, nullptr);
   HN_LAUNCH_CHECK("hn_gemm_linear");
   return 0;
@@ -605,10 +879,10 @@ extern "C" int hn_gemm_linear_impl(int mats, const void* x, long ld_x, const voi
 extern "C" int hn_gemm_grouped_impl(int phase, const void* x, long ld_x, const void* table,
                                     const int* active, const int* n_active, const int* offsets,
                                     long E, long rows, long H, long I, long group, void* out,
-                                    long ld_o, void* stream) {
+                                    long ld_o, void* work, long work_bytes, void* stream) {
   const long K = phase == 0 ? H : I, N = phase == 0 ? I : H;
   if (E > kMaxProb || !gemm_shape_ok(N, K, group, K / 2, K / group)) return HN_NOT_HANDLED;
-  if (!aligned16(x) || ld_x % 8 != 0 || ld_x * 2 * kBM >= (long)kOOB) return HN_NOT_HANDLED;
+  if (!aligned16(x) || ld_x % 8 != 0 || ld_x * 2 * kBMMax >= (long)kOOB) return HN_NOT_HANDLED;
   if (rows <= 0) return 0;
   GemmArgs A = {};
   A.x = (const h16*)x;
@@ -622,18 +896,22 @@ extern "C" int hn_gemm_grouped_impl(int phase, const void* x, long ld_x, const v
   A.ld_q = (int)(K / 2);
   A.ld_s = (int)(K / group);
   fill_consts(A);
+  // 256-token M-tiles (128-token ones for the short remainders); with the
+  // stream-K workspace the work spreads evenly whatever the tile count
   const long wn = kWaves * 32 * kBlk / (phase == 0 ? 2 : 1);
-  const long mt_upper = (rows + kBM - 1) / kBM + (E < rows ? E : rows);
+  const long bm = phase == 0 ? 32 * kRBGateUp : 32 * kRBDown;
+  const long mt_upper = (rows + bm - 1) / bm + (E < rows ? E : rows);
   const long tiles = mt_upper * ((N + wn - 1) / wn);
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(grid_for(tiles));
+  dim3 grid(grid_for(tiles));
+  sk_setup(A, work, work_bytes, tiles, grid);
   const GExpert* tb = (const GExpert*)table;
   if (phase == 0)
-    hipLaunchKernelGGL((gemm_kernel<true, 2>), grid, dim3(256), 0, s, A, tb, active, n_active,
-                       offsets);
+    hipLaunchKernelGGL((gemm_kernel<true, 2, kRBGateUp>), grid, dim3(256), 0, s, A, tb, active,
+                       n_active, offsets);
   else
-    hipLaunchKernelGGL((gemm_kernel<true, 1>), grid, dim3(256), 0, s, A, tb, active, n_active,
-                       offsets);
+    hipLaunchKernelGGL((gemm_kernel<true, 1, kRBDown>), grid, dim3(256), 0, s, A, tb, active,
+                       n_active, offsets);
   HN_LAUNCH_CHECK("hn_gemm_grouped");
   return 0;
 }

@@ -602,11 +602,12 @@ extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, c
 extern "C" int hn_gemm_linear_impl(int mats, const void* x, long ld_x, const void* q0,
                                    const void* s0, const void* q1, const void* s1, long ld_q,
                                    long ld_s, void* out, long ld_o, long M, long N, long K,
-                                   long group, void* stream);
+                                   long group, void* work, long work_bytes, void* stream);
 extern "C" int hn_gemm_grouped_impl(int phase, const void* x, long ld_x, const void* table,
                                     const int* active, const int* n_active, const int* offsets,
                                     long E, long rows, long H, long I, long group, void* out,
-                                    long ld_o, void* stream);
+                                    long ld_o, void* work, long work_bytes, void* stream);
+extern "C" long hn_gemm_workspace_bytes();
 
 // Decode kernel family: 0 = automatic (streaming kernels where they apply),
 // 1 = split-K kernels only.  Process-wide; for A/B measurement and tests.
@@ -652,7 +653,7 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
   const bool premul = (group % 128) != 0;
   if (M > kMaxRows) {
     const int rc = hn_gemm_linear_impl(mats, x, ld_x, w0.q, w0.s, w1.q, w1.s, w0.ld_q, w0.ld_s,
-                                       out, ld_o, M, N, K, group, s);
+                                       out, ld_o, M, N, K, group, ws, ws_size, s);
     if (rc != HN_NOT_HANDLED) return rc;
   }
   if (g_decode_path == 0 && !premul && M <= kStreamMaxRows) {
@@ -773,16 +774,17 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
                "%s: one weight matrix must stay below 2 GiB - 16 B", who);
   if (max_rows_per_expert == 0 || rows == 0) return 0;
   if (max_rows_per_expert > kMaxRows) {
-    // prefill: the grouped MFMA GEMM (no workspace)
+    // prefill: the grouped MFMA GEMM (a workspace of hn_gemm_workspace_bytes
+    // enables its stream-K split; without one whole tiles go round-robin)
     HN_ARG_CHECK(I % 128 == 0 && E <= 256,
                  "%s: more than %d rows per expert needs I %% 128 == 0 and E <= 256 "
                  "(I=%ld, E=%ld)", who, kMaxRows, I, E);
     hipStream_t s = (hipStream_t)stream;
     int rc = hn_gemm_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E, rows, H, I,
-                                  group, h_ws, I, s);
+                                  group, h_ws, I, work, work_bytes, s);
     if (rc == 0)
       rc = hn_gemm_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E, rows, H, I,
-                                group, y_perm, H, s);
+                                group, y_perm, H, work, work_bytes, s);
     if (rc == HN_NOT_HANDLED) {
       hn_set_error("%s: shape not handled by the prefill GEMM (group=%ld)", who, group);
       return -22;
@@ -857,7 +859,7 @@ extern "C" int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const
                                             const int* active, const int* n_active,
                                             const int* offsets, long E, long rows, long H,
                                             long I, long group, void* h_ws, void* y_perm,
-                                            void* stream) {
+                                            void* work, long work_bytes, void* stream) {
   const char* who = "hn_grouped_expert_phase_int4";
   HN_ARG_CHECK(phase == 0 || phase == 1, "%s: phase must be 0 or 1", who);
   HN_ARG_CHECK(E > 0 && E <= 256 && rows >= 0, "%s: bad sizes (E=%ld, rows=%ld)", who, E, rows);
@@ -867,9 +869,9 @@ extern "C" int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const
   if (rows == 0) return 0;
   const int rc = phase == 0
       ? hn_gemm_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E, rows, H, I, group,
-                             h_ws, I, stream)
+                             h_ws, I, work, work_bytes, stream)
       : hn_gemm_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E, rows, H, I, group,
-                             y_perm, H, stream);
+                             y_perm, H, work, work_bytes, stream);
   if (rc == HN_NOT_HANDLED) {
     hn_set_error("%s: shape not handled by the GEMM kernels (group=%ld)", who, group);
     return -22;
@@ -945,6 +947,20 @@ extern "C" int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w
   HN_ARG_CHECK(rc != HN_NOT_HANDLED, "%s: shape not covered (T <= 16, E <= 8, k == 2, H %% 512 "
                "== 0, group 128; T=%ld E=%ld k=%ld H=%ld group=%ld)", who, T, E, k, H, group);
   return rc;
+}
+
+// 0 when hn_moe_decode_layer covers the shape (decode path 0 included),
+// otherwise HN_NOT_HANDLED; sets no error.
+extern "C" int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group) {
+  if (g_decode_path != 0) return HN_NOT_HANDLED;
+  // dry runs: shapes only (no pointer is read)
+  const int a = hn_stream_route_gate_up_impl(nullptr, H, nullptr, H, T, E, k, nullptr, H, I,
+                                             group, 0.f, 1.f, nullptr, nullptr, nullptr, nullptr,
+                                             nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                             1);
+  const int b = hn_stream_down_split_impl(nullptr, nullptr, nullptr, nullptr, nullptr, E, T,
+                                          T * k, H, I, group, nullptr, nullptr, 1);
+  return a == 0 && b == 0 ? 0 : HN_NOT_HANDLED;
 }
 
 // One Mixtral MoE layer at decode in three launches: the routing (logits,

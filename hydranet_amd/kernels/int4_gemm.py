@@ -51,7 +51,8 @@ def int4_linear(
     wq = _lib.aligned_rows(w_packed)
     ws = w_scales if w_scales.stride(-1) == 1 else w_scales.contiguous()
     out = torch.empty((M, N), dtype=torch.float16, device=x.device)
-    work = _lib.skinny_workspace(0, M, N, K, 0, x.device)
+    work = (_lib.skinny_workspace(0, M, N, K, 0, x.device) if M <= _lib.DECODE_MAX_ROWS
+            else _lib.gemm_workspace(x.device))
     _lib.call("hn_int4_linear", _lib.ptr(xh), xh.stride(0), _lib.ptr(wq), wq.stride(0),
               _lib.ptr(ws), ws.stride(0), _lib.ptr(out), out.stride(0), M, N, K, group_size,
               _lib.ptr(work), work.numel(), _lib.stream(x.device))
@@ -118,7 +119,8 @@ def expert_mlp_int4_fused(
     h_ws = torch.empty((T, I), dtype=torch.float16, device=x.device)
     out = torch.empty((T, H), dtype=torch.float16, device=x.device)
     if T > 0:
-        work = _lib.skinny_workspace(2, T, H, I, 0, x.device)
+        work = (_lib.skinny_workspace(2, T, H, I, 0, x.device) if T <= _lib.DECODE_MAX_ROWS
+                else _lib.gemm_workspace(x.device))
         _lib.call("hn_expert_mlp_int4", _lib.ptr(xh), *[_lib.ptr(m) for m in mats], _lib.ptr(out),
                   T, H, I, group_size, _lib.ptr(h_ws), _lib.ptr(work), work.numel(),
                   _lib.stream(x.device))

@@ -129,9 +129,9 @@ def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torc
     """Whether hn_moe_decode_layer (routing fused into the gate/up kernel)
     covers this Mixtral layer call."""
     H, I, g = table.dims
-    return (_lib.decode_path() == 0 and 1 <= T <= 16 and E <= 8 and k == 2 and g == 128
-            and H % 512 == 0 and I % 512 == 0 and table.num_experts == E
-            and gate_w.shape == (E, H))
+    if table.num_experts != E or tuple(gate_w.shape) != (E, H):
+        return False
+    return _lib.lib().hn_moe_decode_layer_check(T, E, k, H, I, g) == 0
 
 
 def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: "ExpertTable",
@@ -191,7 +191,7 @@ def moe_dispatch(r: Routed, table: ExpertTable,
                   _lib.ptr(r.w), T, k, _lib.ptr(sh), H if sh is None else sh.stride(0),
                   _lib.ptr(out), H, _lib.ptr(work), work.numel(), st)
         return out
-    work = None
+    work = _lib.gemm_workspace(dev)  # stream-K split of the prefill GEMM
     _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(r.x_perm), _lib.ptr(table.dev),
               _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I, g,
               _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work),
@@ -236,7 +236,8 @@ def moe_experts_forward(hidden: torch.Tensor, idx: torch.Tensor, w: torch.Tensor
     y_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
     # above DECODE_MAX_ROWS tokens per expert the grouped prefill GEMM runs,
     # which needs no workspace
-    work = _lib.skinny_workspace(3, n, H, I, E, dev) if T <= _lib.DECODE_MAX_ROWS else None
+    work = (_lib.skinny_workspace(3, n, H, I, E, dev) if T <= _lib.DECODE_MAX_ROWS
+            else _lib.gemm_workspace(dev))
     _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(x_perm), _lib.ptr(table.dev),
               _lib.ptr(active), _lib.ptr(n_active), _lib.ptr(offsets), E, T, n, H, I, g,
               _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work),

@@ -49,6 +49,15 @@ int hn_int4_quantize(const void* w, long ld_w, int dtype, int mode, void* packed
  * No counterpart in the reference (Triton needs no split-K workspace). */
 long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long E);
 
+/* Workspace bytes of the prefill (MFMA GEMM) kernels' stream-K split: fp32
+ * partial slots for two tile segments per workgroup plus per-(tile, wave)
+ * counters.  Passed (zero-filled once; the kernels leave the counters at zero)
+ * as the work argument of the entry points below at prefill sizes, it makes
+ * every CU take an equal share of the (tile, k-stage) iterations, tiles split
+ * at the shares' ends being summed in a fixed order by the last segment to
+ * finish.  No counterpart in the reference (Triton's GEMM takes no workspace). */
+long hn_gemm_workspace_bytes(void);
+
 /* out[M, N] = fp16(x[M, K] @ deq(W)^T), fp32 accumulation.  Replaces the
  * int4_matmul_kernel launch in int4_gemm.int4_linear (kernels/int4_gemm.py:124-172)
  * and int4_expert_mlp.int4_linear (kernels/int4_expert_mlp.py:99-156).
@@ -132,7 +141,11 @@ int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* i
  * {gate_q, gate_s, up_q, up_s, down_q, down_s} device pointers (u64), each
  * 16-byte aligned (GpuExpertSlot slabs are); active /
  * n_active / offsets from hn_moe_permute; h_ws [rows, I] fp16 buffer;
- * y_perm [rows, H] fp16 out; work: hn_skinny_workspace_bytes(3, rows, H, I, E).
+ * y_perm [rows, H] fp16 out; work: hn_skinny_workspace_bytes(3, rows, H, I, E),
+ * zero-filled once.  Above 64 rows per expert (the MFMA GEMM kernels) work
+ * may instead hold hn_gemm_workspace_bytes() bytes, which enables their
+ * stream-K split of the k-stages over the CUs, or be NULL (whole tiles go
+ * round-robin).
  * Replaces the per-expert loop calling expert_mlp_int4_fused
  * (model/mixtral.py:327-354, model/glm4.py:421-455). */
 int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int* active,
@@ -167,6 +180,10 @@ int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w, long ld_w
                          int* perm, int* inv, int* active, int* n_active, void* h_ws,
                          void* stream);
 
+/* 0 when hn_moe_decode_layer covers (T, E, k, H, I, group) with the current
+ * decode kernel family, else a nonzero code (no error message is set). */
+int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group);
+
 /* One Mixtral MoE layer at decode (T <= 16 tokens, E <= 8 experts, top-2
  * softmax, fp16 gate [E, H], group 128, H and I multiples of 512) in three
  * launches: the routing (logits, top-k, stable permutation) computed inside
@@ -198,14 +215,19 @@ int hn_grouped_decode_phase_int4(int phase, const void* x, const void* table, co
 /* One phase of hn_grouped_expert_mlp_int4's prefill path (the grouped MFMA GEMM):
  * phase 0 writes h_ws [rows, I] = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T)) per expert,
  * phase 1 writes y_perm [rows, H] = fp16(h_ws Wd^T) per expert.  Any rows per
- * expert; E <= 256; H, I multiples of 128; group 64 or a multiple of 128.
+ * expert; E <= 256; H, I multiples of 128; group 32 or a multiple of 64.
+ * work (may be NULL / 0): with hn_gemm_workspace_bytes() bytes, zero-filled
+ * once, the k-stages are split evenly over
+ * the CUs (stream-K; tiles split at the shares' ends are summed in a fixed
+ * order); without, whole tiles go round-robin.  Calls that run concurrently
+ * need distinct workspaces.
  * No separate counterpart in the reference (its loop calls
  * expert_mlp_int4_fused per expert, model/mixtral.py:342-354); lets a caller
  * time or schedule the two phases apart. */
 int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const void* table,
                                  const int* active, const int* n_active, const int* offsets,
                                  long E, long rows, long H, long I, long group, void* h_ws,
-                                 void* y_perm, void* stream);
+                                 void* y_perm, void* work, long work_bytes, void* stream);
 
 /* Decode kernel family for hn_int4_linear, hn_int4_gate_up_silu,
  * hn_expert_mlp_int4 and hn_grouped_expert_mlp_int4 (process-wide):
