@@ -561,6 +561,42 @@ def c2phase(args):
                       + n * I * 2, "copy_bytes": src.numel() * 2}), flush=True)
 
 
+def c4phase(args):
+    """Counter run: the C4 layer's grouped gate/up and down GEMM launches (three
+    each, with the stream-K workspace), for rocprofv3 --pmc MFMA counters."""
+    from hydranet_amd import _lib
+    from hydranet_amd.model.moe import ExpertTable
+    from hydranet_amd.model.router import topk_from_logits
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
+    H, I, g, E, T, k = 4096, 14336, 128, 8, 2048, 2
+    slots = [make_expert_slot(expert_seed(0, e), H, I, g, slot_idx=e) for e in range(E)]
+    table = ExpertTable.from_slots(slots)
+    x = normal_f16((T, H), 4242, std=1.0)
+    idx, _ = topk_from_logits(zipf_logits(T, E, 2048), k, mode=0)
+    n = T * k
+    dev = x.device
+    meta = torch.empty(3 * E + 2 + 2 * n, dtype=torch.int32, device=dev)
+    offs, act, nact = meta[:E + 1], meta[E + 1:2 * E + 1], meta[2 * E + 1:2 * E + 2]
+    perm, inv = meta[2 * E + 2:2 * E + 2 + n], meta[2 * E + 2 + n:]
+    x_perm = torch.empty(n, H, dtype=torch.float16, device=dev)
+    h_ws = torch.empty(n, I, dtype=torch.float16, device=dev)
+    y_perm = torch.empty(n, H, dtype=torch.float16, device=dev)
+    work = _lib.gemm_workspace(dev)
+    sp = _lib.stream()
+    _lib.call("hn_moe_permute", _lib.ptr(idx), T, k, E, _lib.ptr(offs), _lib.ptr(perm),
+              _lib.ptr(inv), _lib.ptr(act), _lib.ptr(nact), sp)
+    _lib.call("hn_moe_gather", _lib.ptr(x), H, _lib.ptr(perm), k, _lib.ptr(offs), E,
+              _lib.ptr(x_perm), H, n, H, sp)
+    for phase in (0, 1):
+        for _ in range(3):
+            _lib.call("hn_grouped_expert_phase_int4", phase, _lib.ptr(x_perm),
+                      _lib.ptr(table.dev), _lib.ptr(act), _lib.ptr(nact), _lib.ptr(offs), E, n,
+                      H, I, g, _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work), work.numel(), sp)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "c4phase", "gate_up_flops": 2.0 * n * 2 * H * I,
+                      "down_flops": 2.0 * n * H * I}), flush=True)
+
+
 # HBM bytes per launch of the roofline kernel (routing + grouped gate/up stream
 # kernel, C2 T=16, 8 active experts): FETCH_SIZE + WRITE_SIZE from two rocprofv3
 # --pmc passes over `bench.py --workload c2phase`, each scaled by the same
@@ -574,9 +610,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c2phase"],
-                    help="c2phase: only the C2 T=16 gate/up phase kernel and a 512 MiB copy "
-                         "(the two kernels whose rocprofv3 counters give roofline.traffic)")
+    ap.add_argument("--workload", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c2phase", "c4phase"],
+                    help="c2phase: only the C2 T=16 routing + gate/up kernel and a 512 MiB copy "
+                         "(the two kernels whose rocprofv3 counters give roofline.traffic); "
+                         "c4phase: only the C4 grouped GEMM launches (MFMA counters)")
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -598,6 +636,9 @@ def main():
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
     if args.workload == "c2phase":
         c2phase(args)
+        return
+    if args.workload == "c4phase":
+        c4phase(args)
         return
     if args.workload == "c3":
         c3 = bench_c3(args)
