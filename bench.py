@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X INT4 expert-MLP hot path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c3|c4|c2phase] [--tokens T]
+    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c3|c4|c5|c2phase] [--tokens T]
 
 Prints ONE JSON line.  A "step" is one pass of the hot path over one batch of
 synthetic input already resident in HBM:
@@ -11,6 +11,8 @@ synthetic input already resident in HBM:
   c1  one Mixtral expert SwiGLU (H 4096, I 14336, INT4 g128), T tokens (default 1)
   c3  one GLM-4.5-Air MoE layer at decode (T = 32, 128 experts, shared expert)
   c4  one Mixtral MoE layer at prefill (2048 tokens, Zipf-skewed routing)
+  c5  the whole Mixtral-8x7B-shaped decoder: 64 x 512-token prompts, greedy
+      decode (tokens/s over the decode forwards)
 
 Weights are seeded N(0, 0.02) fp16 packed to INT4 by the GPU packer.  Steps
 rotate over enough distinct experts (>= 0.7 GB) that weights stream from HBM,
@@ -597,6 +599,69 @@ def c4phase(args):
                       "down_flops": 2.0 * n * H * I}), flush=True)
 
 
+# ----------------------------------------------------------------------------- C5
+def bench_c5(args):
+    """Full Mixtral-8x7B-shaped decoder (32 layers, H 4096, 32 Q / 8 KV heads,
+    head_dim 128, vocab 32000), random init N(0, 0.02) fp16, norms 1, all 256
+    experts INT4 g128 resident in HBM.  64 sequences x 512 seeded random prompt
+    ids, greedy decode of `--decode-tokens` tokens (top-2 routing at prefill,
+    top-1 at decode).  Timed: the decode forwards after `--warmup-decode`
+    untimed ones; tokens/s = 64 x timed forwards / time.  bytes_per_step counts
+    every expert of every layer once (64 tokens at top-1 leave an expert of a
+    layer unused with probability (7/8)^64), the dense weights, the LM head and
+    the KV cache read at the step's context length."""
+    from hydranet_amd.model.decoder import MixtralDecoderConfig, build_synthetic_decoder
+
+    B, P, N = 64, 512, args.decode_tokens
+    cfg = MixtralDecoderConfig(max_position_embeddings=P + N)
+    t0 = time.perf_counter()
+    model = build_synthetic_decoder(cfg, "cuda", decode_top_k=1, seed=5)
+    torch.cuda.synchronize()
+    _log("c5 built in", round(time.perf_counter() - t0, 1), "s")
+    H, I, L = cfg.hidden_dim, cfg.intermediate_dim, cfg.num_layers
+    blob = model.layers[0].moe.experts.table.slots[0].layout.total_size
+    nh, nkv, hd = cfg.num_attention_heads, cfg.num_kv_heads, cfg.head_dim
+    dense = (2 * H * nh * hd + 2 * H * nkv * hd) * 2 + cfg.num_experts * H * 2
+    kv_per_pos = B * L * nkv * hd * 2 * 2
+    ids = torch.randint(0, cfg.vocab_size, (B, P), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(512))
+    cache = model.new_cache(B, P + N)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = model(ids, cache)
+    tok = logits[:, -1].argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    del logits
+    W = min(args.warmup_decode, N - 2)
+    for _ in range(W):
+        tok = model(tok, cache)[:, -1].argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    n = N - 1 - W
+    ctx0 = cache.cur_len
+    t0 = time.perf_counter()
+    out = [tok]
+    for _ in range(n):
+        tok = model(tok, cache)[:, -1].argmax(-1, keepdim=True)
+        out.append(tok)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    total_bytes = sum(L * (cfg.num_experts * blob + dense) + cfg.vocab_size * H * 2
+                      + kv_per_pos * (ctx0 + i + 1) for i in range(n))
+    gbs = total_bytes / dt / 1e9
+    toks = torch.cat(out, 1)
+    return {"workload": "C5: Mixtral-8x7B-shaped decoder (32 layers, H 4096, 32/8 heads, "
+                        "head_dim 128, vocab 32000, 8 INT4 g128 experts per layer resident), "
+                        "64 x 512-token random prompts, greedy decode (top-1 routing)",
+            "batch": B, "prompt": P, "decode_tokens": N, "timed_forwards": n,
+            "ms_per_step": round(dt * 1e3 / n, 4), "tokens_per_s": round(B * n / dt, 1),
+            "prefill_s": round(prefill_s, 3),
+            "prefill_tokens_per_s": round(B * P / prefill_s, 1),
+            "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_step_avg": int(total_bytes / n),
+            "distinct_last_tokens": int(torch.unique(toks[:, -1]).numel())}
+
+
 # HBM bytes per launch of the roofline kernel (routing + grouped gate/up stream
 # kernel, C2 T=16, 8 active experts): FETCH_SIZE + WRITE_SIZE from two rocprofv3
 # --pmc passes over `bench.py --workload c2phase`, each scaled by the same
@@ -611,11 +676,13 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c2phase", "c4phase"],
+                    choices=["c1", "c2", "c3", "c4", "c5", "c2phase", "c4phase"],
                     help="c2phase: only the C2 T=16 routing + gate/up kernel and a 512 MiB copy "
                          "(the two kernels whose rocprofv3 counters give roofline.traffic); "
                          "c4phase: only the C4 grouped GEMM launches (MFMA counters)")
     ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--decode-tokens", type=int, default=256, help="c5: tokens generated")
+    ap.add_argument("--warmup-decode", type=int, default=3, help="c5: untimed decode forwards")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-path", type=int, default=0, choices=[0, 1],
@@ -647,6 +714,14 @@ def main():
                                     "1 GPU)", "value": c3["GB_s"], "unit": "GB/s", "n_gpus": 1,
                           "ms_per_step": c3["ms_per_step"], "higher_is_better": True,
                           "dtype": "fp16", "data": "synthetic", "config": c3}), flush=True)
+        return
+    if args.workload == "c5":
+        c5 = bench_c5(args)
+        _log("c5", c5)
+        print(json.dumps({"metric": "Mixtral-shape decode tokens/sec, 1 GPU", "value":
+                          c5["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+                          "ms_per_step": c5["ms_per_step"], "higher_is_better": True,
+                          "dtype": "fp16", "data": "synthetic", "config": c5}), flush=True)
         return
     if args.workload == "c4":
         c4 = bench_c4(args)

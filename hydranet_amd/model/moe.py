@@ -234,8 +234,8 @@ def moe_experts_forward(hidden: torch.Tensor, idx: torch.Tensor, w: torch.Tensor
               _lib.ptr(x_perm), H, n, H, st)
     h_ws = torch.empty((max(n, 1), I), dtype=torch.float16, device=dev)
     y_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
-    # above DECODE_MAX_ROWS tokens per expert the grouped prefill GEMM runs,
-    # which needs no workspace
+    # above DECODE_MAX_ROWS tokens the grouped prefill GEMM runs, its workspace
+    # holding the stream-K counters and partial sums
     work = (_lib.skinny_workspace(3, n, H, I, E, dev) if T <= _lib.DECODE_MAX_ROWS
             else _lib.gemm_workspace(dev))
     _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(x_perm), _lib.ptr(table.dev),
