@@ -617,10 +617,11 @@ constexpr long kStreamMaxRows = 16;
 // Whether the streaming kernels take a grouped decode launch.  They stage at
 // most 8 tokens of an expert per pass over its weights, so an expert with more
 // rows streams its weights once per 8; they are used up to 16 rows per expert,
-// or up to 64 when the average over the experts is at most 4 (many experts,
-// few rows each: GLM-4.5-Air's 128 experts x top-8).
+// or up to 64 when the average over the experts is at most 8 (few rows per
+// expert: GLM-4.5-Air's 128 experts x top-8; 64 tokens over 8 experts at top-1
+// pass over each expert's weights about 1.4 times on average).
 static bool stream_rows_ok(long max_rows, long rows, long E) {
-  return max_rows <= kStreamMaxRows || (max_rows <= kMaxRows && rows <= 4 * E);
+  return max_rows <= kStreamMaxRows || (max_rows <= kMaxRows && rows <= 8 * E);
 }
 
 extern "C" int hn_set_decode_path(int path) {
@@ -1026,7 +1027,7 @@ extern "C" int hn_grouped_decode_phase_int4(int phase, const void* x, const void
                "%s: H, I multiples of 128 and 16-byte aligned buffers", who);
   HN_ARG_CHECK(stream_rows_ok(max_rows_per_expert, rows, E) && group == 128,
                "%s: the streaming kernels take <= %ld rows per expert (<= %ld when rows <= "
-               "4 E) and group 128", who, kStreamMaxRows, kMaxRows);
+               "8 E) and group 128", who, kStreamMaxRows, kMaxRows);
   if (rows == 0 || max_rows_per_expert == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   int rc;

@@ -273,7 +273,8 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
 // then copies its share of the permuted rows x_perm[p] = h[perm[p] / k];
 // workgroup 0 also writes the routing outputs.  Top-k and the order are those
 // of router_topk_kernel / moe_permute_kernel.  Logits (LG):
-//  * 1, 2: MFMA (fp16 gate, T <= 16 / 32 tokens, E <= 16, H % 512 == 0):
+//  * 1, 2, 4: MFMA (fp16 gate, T <= 16 / 32 / 64 tokens, E <= 16, T * E <= 512,
+//    H % 512 == 0):
 //    each of the 16 waves multiplies one 1/16 slice of H (all its loads in
 //    flight together), the 16 partial 16x16 tiles are summed in wave order,
 //    then rounded to fp16 (the fp16 Linear of the reference);
@@ -291,8 +292,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     int* __restrict__ idx_out, h16* __restrict__ w_out, int* __restrict__ offsets,
     int* __restrict__ perm, int* __restrict__ inv, int* __restrict__ active,
     int* __restrict__ n_active, h16* __restrict__ x_perm, long ld_p) {
-  __shared__ float s_buf[kRouteMaxLogits];  // logits, or the MFMA partial tiles
-  __shared__ float s_lg[512];               // MFMA logits (T <= 32, E <= 16)
+  // logits, or the MFMA partial tiles (16 waves x 16 LG tokens x 16 experts)
+  __shared__ float s_buf[LG == 4 ? 16 * 64 * 16 : kRouteMaxLogits];
+  __shared__ float s_lg[512];               // MFMA logits (T * E <= 512)
   __shared__ int s_sel[kRouteMaxAssign];
   __shared__ h16 s_w[kRouteMaxAssign];
   __shared__ int s_perm[kRouteMaxAssign];
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     for (int u = 0; u < LG; ++u) acc[u] = float4_t{0.f, 0.f, 0.f, 0.f};
     // passes of up to KST steps whose loads go out together (steps past the
     // slice repeat the last one and are not multiplied)
-    constexpr int KST = LG == 1 ? 8 : 4;
+    constexpr int KST = LG == 1 ? 8 : (LG == 2 ? 4 : 2);
     for (int s0 = 0; s0 < steps; s0 += KST) {
       half8_t bv[KST], av[KST][LG];
 #pragma unroll
@@ -340,18 +342,20 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         }
       }
     }
-    // lane: expert tl, tokens 16 u + 4 (lane >> 4) + r
+    // lane: expert tl, tokens 16 u + 4 (lane >> 4) + r; a wave's partial
+    // tile holds TS tokens
+    constexpr int TS = LG == 4 ? 64 : 32;
 #pragma unroll
     for (int u = 0; u < LG; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        s_buf[(wave * 32 + 16 * u + 4 * (lane >> 4) + r) * 16 + tl] = acc[u][r];
+        s_buf[(wave * TS + 16 * u + 4 * (lane >> 4) + r) * 16 + tl] = acc[u][r];
     __syncthreads();
     for (int i = tid; i < T * E; i += blockDim.x) {
       const int t = i / E, e = i - t * E;
       float v = 0.f;
 #pragma unroll
-      for (int w2 = 0; w2 < kRouteWaves; ++w2) v += s_buf[(w2 * 32 + t) * 16 + e];
+      for (int w2 = 0; w2 < kRouteWaves; ++w2) v += s_buf[(w2 * TS + t) * 16 + e];
       s_lg[i] = ROUND16 ? (float)(h16)v : v;
     }
     lg = s_lg;
@@ -587,8 +591,9 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
   const long bytes = T * k * H * 2;
   const int grid = (int)std::min(128L, std::max(1L, (bytes + 65535) / 65536));
   hipStream_t s = (hipStream_t)stream;
-  // logits by MFMA for an fp16 gate with T <= 32, E <= 16, H % 512 == 0
-  const int lgv = (logits_in || w_dtype != 0 || E > 16 || H % 512 != 0) ? 0 : (T <= 16 ? 1 : (T <= 32 ? 2 : 0));
+  // logits by MFMA for an fp16 gate with T <= 64, T * E <= 512, E <= 16, H % 512 == 0
+  const int lgv = (logits_in || w_dtype != 0 || E > 16 || H % 512 != 0 || T * E > 512)
+                      ? 0 : (T <= 16 ? 1 : (T <= 32 ? 2 : (T <= 64 ? 4 : 0)));
   const bool mix = E <= 8 && k == 2 && mode == 0;
 #define HN_ROUTE_LAUNCH(TW, R16, LGV, TKV)                                                          \
   hipLaunchKernelGGL((moe_route_kernel<TW, R16, LGV, TKV>), dim3(grid), dim3(kRouteThreads), 0, s, \
@@ -599,8 +604,10 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
   if (w_dtype == 0) {
     if (lgv == 1 && mix) HN_ROUTE_LAUNCH(h16, true, 1, 1);
     else if (lgv == 2 && mix) HN_ROUTE_LAUNCH(h16, true, 2, 1);
+    else if (lgv == 4 && mix) HN_ROUTE_LAUNCH(h16, true, 4, 1);
     else if (lgv == 1) HN_ROUTE_LAUNCH(h16, true, 1, 0);
     else if (lgv == 2) HN_ROUTE_LAUNCH(h16, true, 2, 0);
+    else if (lgv == 4) HN_ROUTE_LAUNCH(h16, true, 4, 0);
     else HN_ROUTE_LAUNCH(h16, true, 0, 0);
   } else {
     HN_ROUTE_LAUNCH(float, false, 0, 0);

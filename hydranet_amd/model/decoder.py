@@ -68,10 +68,9 @@ class RotaryEmbedding(nn.Module):
         self.register_buffer("cos_cached", emb.cos(), persistent=False)
         self.register_buffer("sin_cached", emb.sin(), persistent=False)
 
-    def forward(self, position_ids: torch.Tensor):
-        # [B, S] -> [B, 1, S, head_dim], broadcast over heads
-        return (self.cos_cached[position_ids].unsqueeze(1),
-                self.sin_cached[position_ids].unsqueeze(1))
+    def forward(self, pos: torch.Tensor):
+        """pos [S] -> cos, sin [S, head_dim] (broadcast over batch and heads)."""
+        return self.cos_cached[pos], self.sin_cached[pos]
 
 
 def rotate_half(x: torch.Tensor) -> torch.Tensor:
@@ -84,38 +83,47 @@ def apply_rotary(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch
 
 
 class KVCache:
-    """Preallocated K/V per layer, [B, kv_heads, max_len, head_dim], one
-    current length for the whole batch (SimpleKVCache's fp16 mode)."""
+    """Preallocated K/V per layer with one current length for the whole batch
+    (SimpleKVCache's fp16 mode).  Keys are stored transposed,
+    kt[layer] = [B, kv_heads, head_dim, max_len], so the score product reads
+    them as a row-major right operand; values as v[layer] = [B, kv_heads,
+    max_len, head_dim].  Writes go to positions given as a device tensor, which
+    lets a captured decode step write where its position counter points."""
 
     def __init__(self, num_layers: int, batch: int, num_kv_heads: int, head_dim: int,
                  max_len: int, device, dtype=torch.float16):
-        shape = (batch, num_kv_heads, max_len, head_dim)
-        self.k = [torch.zeros(shape, device=device, dtype=dtype) for _ in range(num_layers)]
-        self.v = [torch.zeros(shape, device=device, dtype=dtype) for _ in range(num_layers)]
+        self.kt = [torch.zeros((batch, num_kv_heads, head_dim, max_len), device=device,
+                               dtype=dtype) for _ in range(num_layers)]
+        self.v = [torch.zeros((batch, num_kv_heads, max_len, head_dim), device=device,
+                              dtype=dtype) for _ in range(num_layers)]
         self.max_len = max_len
         self.cur_len = 0
 
-    def update(self, layer: int, k: torch.Tensor, v: torch.Tensor, start: int) -> None:
-        end = start + k.shape[2]
-        assert end <= self.max_len, f"KV cache full ({end} > {self.max_len})"
-        self.k[layer][:, :, start:end] = k
-        self.v[layer][:, :, start:end] = v
+    def update(self, layer: int, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor) -> None:
+        """k, v [B, kv_heads, S, head_dim] at positions pos [S] (int64, on the device)."""
+        self.kt[layer].index_copy_(3, pos, k.transpose(2, 3))
+        self.v[layer].index_copy_(2, pos, v)
 
     def get(self, layer: int, total: int):
-        return self.k[layer][:, :, :total], self.v[layer][:, :, :total]
+        """(K^T [B, kvh, hd, total], V [B, kvh, total, hd]) views of the first positions."""
+        return self.kt[layer][..., :total], self.v[layer][:, :, :total]
 
     def advance(self, n: int) -> None:
         self.cur_len += n
+        assert self.cur_len <= self.max_len, f"KV cache full ({self.cur_len} > {self.max_len})"
 
     def reset(self) -> None:
         self.cur_len = 0
 
 
 class Attention(nn.Module):
-    """Grouped-query attention with RoPE and the KV cache; scores and softmax
-    as the reference computes them (fp16 products, fp32 softmax)."""
+    """Grouped-query attention over the KV cache; scores and softmax as the
+    reference computes them (fp16 products scaled by 1/sqrt(head_dim), fp32
+    softmax).  The query heads that share a KV head are stacked as the rows of
+    one product with that head's keys (head h uses KV head h // (heads /
+    kv_heads), as repeat_interleave gives), so the cache is never expanded."""
 
-    def __init__(self, cfg: MixtralDecoderConfig, device=None):
+    def __init__(self, cfg: MixtralDecoderConfig):
         super().__init__()
         self.nh, self.nkv, self.hd = cfg.num_attention_heads, cfg.num_kv_heads, cfg.head_dim
         H = cfg.hidden_dim
@@ -123,51 +131,57 @@ class Attention(nn.Module):
         self.k_proj = nn.Linear(H, self.nkv * self.hd, bias=False)
         self.v_proj = nn.Linear(H, self.nkv * self.hd, bias=False)
         self.o_proj = nn.Linear(self.nh * self.hd, H, bias=False)
-        self.rope = RotaryEmbedding(self.hd, cfg.max_position_embeddings, cfg.rope_theta, device)
 
-    def forward(self, x: torch.Tensor, position_ids: torch.Tensor, cache: KVCache,
-                layer: int) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
+                cache: KVCache, layer: int, kv_len: int,
+                mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x [B, S, H]; cos, sin [S, head_dim] at positions pos [S]; attends
+        over the cache's first kv_len positions, adding mask [S, kv_len]
+        (0 / -inf) when given."""
         B, S, _ = x.shape
-        q = self.q_proj(x).view(B, S, self.nh, self.hd).transpose(1, 2)
-        k = self.k_proj(x).view(B, S, self.nkv, self.hd).transpose(1, 2)
-        v = self.v_proj(x).view(B, S, self.nkv, self.hd).transpose(1, 2)
-        cos, sin = self.rope(position_ids)
+        nh, nkv, hd = self.nh, self.nkv, self.hd
+        q = self.q_proj(x).view(B, S, nh, hd).transpose(1, 2)
+        k = self.k_proj(x).view(B, S, nkv, hd).transpose(1, 2)
+        v = self.v_proj(x).view(B, S, nkv, hd).transpose(1, 2)
         q, k = apply_rotary(q, k, cos.to(q.dtype), sin.to(q.dtype))
-        start = cache.cur_len
-        cache.update(layer, k, v, start)
-        kf, vf = cache.get(layer, start + S)
-        rep = self.nh // self.nkv
-        kf = kf.repeat_interleave(rep, dim=1)  # contiguous [B, nh, L, hd]
-        vf = vf.repeat_interleave(rep, dim=1)
-        scores = torch.matmul(q.contiguous(), kf.transpose(2, 3).contiguous()) / math.sqrt(self.hd)
-        if S > 1:  # causal over the new tokens (positions start .. start + S - 1)
-            L = start + S
-            mask = torch.full((S, L), float("-inf"), device=x.device, dtype=scores.dtype)
-            mask = torch.triu(mask, diagonal=start + 1)
-            scores = scores + mask
+        cache.update(layer, k, v, pos)
+        kt, vv = cache.get(layer, kv_len)
+        rep = nh // nkv
+        qg = q.reshape(B, nkv, rep * S, hd)  # rows: (head within the group, token)
+        scores = torch.matmul(qg, kt) / math.sqrt(hd)  # [B, nkv, rep * S, kv_len]
+        if mask is not None:
+            scores = (scores.view(B, nkv, rep, S, kv_len) + mask).view(B, nkv, rep * S, kv_len)
         p = F.softmax(scores, dim=-1, dtype=torch.float32).to(q.dtype)
-        o = torch.matmul(p, vf)
-        return self.o_proj(o.transpose(1, 2).reshape(B, S, self.nh * self.hd))
+        o = torch.matmul(p, vv).view(B, nh, S, hd)
+        return self.o_proj(o.transpose(1, 2).reshape(B, S, nh * hd))
+
+
+def causal_mask(start: int, S: int, device, dtype=torch.float16) -> torch.Tensor:
+    """[S, start + S]: token i (position start + i) sees positions <= start + i."""
+    m = torch.full((S, start + S), float("-inf"), device=device, dtype=dtype)
+    return torch.triu(m, diagonal=start + 1)
 
 
 class DecoderBlock(nn.Module):
-    def __init__(self, cfg: MixtralDecoderConfig, layer_idx: int, slots, device=None):
+    def __init__(self, cfg: MixtralDecoderConfig, layer_idx: int, slots):
         super().__init__()
         self.layer_idx = layer_idx
         self.input_layernorm = RMSNorm(cfg.hidden_dim, cfg.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(cfg.hidden_dim, cfg.rms_norm_eps)
-        self.self_attn = Attention(cfg, device)
+        self.self_attn = Attention(cfg)
         self.moe = MixtralMoELayer(cfg.hidden_dim, cfg.num_experts, cfg.experts_per_token,
                                    layer_idx=layer_idx, slots=slots)
 
-    def forward(self, x, position_ids, cache: KVCache, top_k: int):
-        x = x + self.self_attn(self.input_layernorm(x), position_ids, cache, self.layer_idx)
+    def forward(self, x, cos, sin, pos, cache: KVCache, kv_len: int, mask, top_k: int):
+        x = x + self.self_attn(self.input_layernorm(x), cos, sin, pos, cache, self.layer_idx,
+                               kv_len, mask)
         return x + self.moe(self.post_attention_layernorm(x), top_k=top_k)
 
 
 class MixtralDecoder(nn.Module):
     """Embeddings -> blocks -> norm -> LM head (model/mixtral.py:430-599), with
-    every expert resident (one GpuExpertSlot per expert, `slots[layer][e]`)."""
+    every expert resident (one GpuExpertSlot per expert, `slots[layer][e]`).
+    One RoPE table serves every layer (the positions are the same)."""
 
     def __init__(self, cfg: MixtralDecoderConfig, slots: List[list], device=None,
                  decode_top_k: int = 1):
@@ -175,15 +189,28 @@ class MixtralDecoder(nn.Module):
         self.cfg = cfg
         self.decode_top_k = decode_top_k
         self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_dim)
-        self.layers = nn.ModuleList([DecoderBlock(cfg, i, slots[i], device)
+        self.layers = nn.ModuleList([DecoderBlock(cfg, i, slots[i])
                                      for i in range(cfg.num_layers)])
         self.norm = RMSNorm(cfg.hidden_dim, cfg.rms_norm_eps)
         self.lm_head = nn.Linear(cfg.hidden_dim, cfg.vocab_size, bias=False)
+        self.rotary = RotaryEmbedding(cfg.head_dim, cfg.max_position_embeddings, cfg.rope_theta,
+                                      device)
 
     def new_cache(self, batch: int, max_len: int) -> KVCache:
         dev = self.embed_tokens.weight.device
         return KVCache(self.cfg.num_layers, batch, self.cfg.num_kv_heads, self.cfg.head_dim,
                        max_len, dev, self.embed_tokens.weight.dtype)
+
+    def step(self, input_ids: torch.Tensor, pos: torch.Tensor, cache: KVCache, kv_len: int,
+             mask: Optional[torch.Tensor], top_k: int) -> torch.Tensor:
+        """One pass over every layer: tokens input_ids [B, S] at positions pos
+        [S] (device int64), attention over the first kv_len cache positions.
+        Does not move cache.cur_len."""
+        cos, sin = self.rotary(pos)
+        x = self.embed_tokens(input_ids)
+        for blk in self.layers:
+            x = blk(x, cos, sin, pos, cache, kv_len, mask, top_k)
+        return self.lm_head(self.norm(x))
 
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, cache: KVCache,
@@ -191,32 +218,81 @@ class MixtralDecoder(nn.Module):
         """input_ids [B, S] -> logits [B, S, vocab]; appends S positions to the
         cache (prefill when it is empty: top-2; decode: decode_top_k)."""
         B, S = input_ids.shape
+        start = cache.cur_len
         if top_k is None:
-            top_k = 2 if cache.cur_len == 0 else self.decode_top_k
-        pos = torch.arange(cache.cur_len, cache.cur_len + S, device=input_ids.device)
-        pos = pos.unsqueeze(0).expand(B, S)
-        x = self.embed_tokens(input_ids)
-        for blk in self.layers:
-            x = blk(x, pos, cache, top_k)
+            top_k = 2 if start == 0 else self.decode_top_k
+        pos = torch.arange(start, start + S, device=input_ids.device)
+        mask = causal_mask(start, S, input_ids.device) if S > 1 else None
+        logits = self.step(input_ids, pos, cache, start + S, mask, top_k)
         cache.advance(S)
-        return self.lm_head(self.norm(x))
+        return logits
 
     @torch.no_grad()
     def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
-                        cache: Optional[KVCache] = None) -> torch.Tensor:
+                        cache: Optional[KVCache] = None, graph: bool = True) -> torch.Tensor:
         """Greedy (top-1 token) decode of max_new_tokens after the prompt; the
-        batch shares one length (uniform prompts, no early stop)."""
+        batch shares one length (uniform prompts, no early stop).  graph: the
+        decode steps are replayed from one captured HIP graph (GraphDecoder)."""
         B, S = input_ids.shape
         if cache is None:
             cache = self.new_cache(B, S + max_new_tokens)
         logits = self.forward(input_ids, cache)
         tok = logits[:, -1].argmax(-1, keepdim=True)
         out = [tok]
+        if graph and max_new_tokens > 1:
+            gd = GraphDecoder(self, cache, tok)
+            for _ in range(max_new_tokens - 1):
+                out.append(gd.step().clone())
+            return torch.cat(out, dim=1)
         for _ in range(max_new_tokens - 1):
-            logits = self.forward(tok, cache)
-            tok = logits[:, -1].argmax(-1, keepdim=True)
+            tok = self.forward(tok, cache)[:, -1].argmax(-1, keepdim=True)
             out.append(tok)
         return torch.cat(out, dim=1)
+
+
+class GraphDecoder:
+    """Greedy decode steps replayed from one captured HIP graph.
+
+    The captured step attends over the whole cache (max_len positions, those
+    after the current one masked to -inf, so they add exp(-inf) = 0 to the
+    softmax), reads its position from a device scalar, writes the next tokens
+    into a static buffer and advances the position itself: successive replays
+    need no host work and no host-device sync.  `tok` holds the tokens fed to
+    the next step; `logits` the last step's logits."""
+
+    def __init__(self, model: MixtralDecoder, cache: KVCache, tok: torch.Tensor):
+        self.model, self.cache = model, cache
+        dev = tok.device
+        L = cache.max_len
+        self.tok = tok.clone()
+        self.pos = torch.full((1,), cache.cur_len, dtype=torch.int64, device=dev)
+        self.ar = torch.arange(L, device=dev)
+        tok0 = self.tok.clone()
+        k = model.decode_top_k
+
+        def body():
+            mask = torch.zeros((1, L), dtype=torch.float16, device=dev).masked_fill_(
+                self.ar > self.pos, float("-inf"))
+            self.logits = model.step(self.tok, self.pos, cache, L, mask, k)
+            self.tok.copy_(self.logits[:, -1].argmax(-1, keepdim=True))
+            self.pos.add_(1)
+
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.no_grad(), torch.cuda.stream(s):
+            body()  # warm-up (allocator, library handles): writes position cur_len, rewritten below
+        torch.cuda.current_stream(dev).wait_stream(s)
+        self.pos.fill_(cache.cur_len)
+        self.tok.copy_(tok0)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.no_grad(), torch.cuda.graph(self.graph):
+            body()
+
+    def step(self) -> torch.Tensor:
+        """One decode step; returns the static buffer of the tokens it chose."""
+        self.graph.replay()
+        self.cache.advance(1)
+        return self.tok
 
 
 def build_synthetic_decoder(cfg: MixtralDecoderConfig, device="cuda", decode_top_k: int = 1,
@@ -233,6 +309,8 @@ def build_synthetic_decoder(cfg: MixtralDecoderConfig, device="cuda", decode_top
     with torch.device(dev):  # dense modules allocated on the GPU, not initialised on the host
         m = MixtralDecoder(cfg, slots, device=dev, decode_top_k=decode_top_k)
     m = m.to(device=dev, dtype=torch.float16)
+    # the RoPE table is computed in fp32 (the cast to fp16 happens where it is applied)
+    m.rotary = RotaryEmbedding(cfg.head_dim, cfg.max_position_embeddings, cfg.rope_theta, dev)
     g = torch.Generator(device=dev).manual_seed(seed)
     with torch.no_grad():
         for name, p in m.named_parameters():

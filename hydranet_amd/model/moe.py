@@ -338,8 +338,8 @@ class MixtralMoELayer(nn.Module):
                 r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits)
                 out = moe_dispatch(r, self.experts.table_for(r.idx))
             if not rt.training:
-                rt.usage_counts += torch.bincount(r.idx.view(-1).long(),
-                                                  minlength=self.num_experts)
+                sel = r.idx.view(-1).long()  # no host sync: graph-capturable
+                rt.usage_counts.scatter_add_(0, sel, torch.ones_like(sel))
             return out.view(B, S, H)
         ro = rt(hidden_states, top_k_override=top_k)
         idx = ro.expert_indices.reshape(T, top_k)

@@ -120,7 +120,9 @@ class TopKRouter(nn.Module):
             logits = self._affinity(logits)
         idx, w = topk_from_logits(logits, k, 0)
         if not self.training:
-            self.usage_counts += torch.bincount(idx.view(-1).long(), minlength=self.num_experts)
+            # scatter_add_ rather than bincount: no device-to-host sync (graph-capturable)
+            flat = idx.view(-1).long()
+            self.usage_counts.scatter_add_(0, flat, torch.ones_like(flat))
         return RouterOutput(idx.view(B, S, k), w.view(B, S, k).to(hidden_states.dtype),
                             logits.view(B, S, self.num_experts))
 

@@ -1,15 +1,17 @@
 """CPU checks of the decoder harness's attention and KV cache
-(hydranet_amd/model/decoder.py), fp32: prefill of S tokens at once equals S
+(hydranet_amd/model/decoder.py), float64: prefill of S tokens at once equals S
 single-token decode steps through the cache (the causal mask's offset and the
-cache's positions), grouped-query attention equals full multi-head attention
-with each KV head repeated, and RoPE preserves norms and is relative
+cache's positions), attention over the whole cache with the later positions
+masked equals attention over the filled part (the captured decode step's
+form), grouped-query attention equals textbook per-head attention with KV head
+h // (heads / kv_heads), and RoPE preserves norms and is relative
 (q(m) . k(n) depends on m - n only)."""
 import math
 
 import torch
 
 from hydranet_amd.model.decoder import (Attention, KVCache, MixtralDecoderConfig, RMSNorm,
-                                        RotaryEmbedding, apply_rotary)
+                                        RotaryEmbedding, apply_rotary, causal_mask)
 
 
 def _cfg():
@@ -18,53 +20,72 @@ def _cfg():
                                 vocab_size=50, max_position_embeddings=32)
 
 
-def test_prefill_equals_stepwise_decode():
-    torch.manual_seed(0)
+def _setup(seed):
+    torch.manual_seed(seed)
     cfg = _cfg()
     att = Attention(cfg).double()
+    rope = RotaryEmbedding(cfg.head_dim, 32, cfg.rope_theta).double()
+    return cfg, att, rope
+
+
+def _run(att, rope, x, cache, start, mask=None, kv_len=None):
+    S = x.shape[1]
+    pos = torch.arange(start, start + S)
+    cos, sin = rope(pos)
+    if mask is None and S > 1:
+        mask = causal_mask(start, S, "cpu", torch.float64)
+    return att(x, cos, sin, pos, cache, 0, kv_len or start + S, mask)
+
+
+def test_prefill_equals_stepwise_decode():
+    cfg, att, rope = _setup(0)
     B, S = 2, 7
     x = torch.randn(B, S, cfg.hidden_dim, dtype=torch.float64)
-    c1 = KVCache(1, B, cfg.num_kv_heads, cfg.head_dim, S, "cpu", torch.float64)
-    pos = torch.arange(S).unsqueeze(0).expand(B, S)
-    full = att(x, pos, c1, 0)
-    c2 = KVCache(1, B, cfg.num_kv_heads, cfg.head_dim, S, "cpu", torch.float64)
-    steps = []
-    for t in range(S):
-        steps.append(att(x[:, t:t + 1], pos[:, t:t + 1], c2, 0))
-        c2.advance(1)
-    torch.testing.assert_close(full, torch.cat(steps, 1), rtol=1e-10, atol=1e-10)
+    mk = lambda L: KVCache(1, B, cfg.num_kv_heads, cfg.head_dim, L, "cpu", torch.float64)
+    c1 = mk(S)
+    full = _run(att, rope, x, c1, 0)
+    c2 = mk(S)
+    steps = [_run(att, rope, x[:, t:t + 1], c2, t) for t in range(S)]
+    # the module's softmax runs in fp32 (as the reference's): fp32-level agreement
+    torch.testing.assert_close(full, torch.cat(steps, 1), rtol=1e-5, atol=1e-7)
     # two-chunk prefill (the mask offset when the cache is not empty)
-    c3 = KVCache(1, B, cfg.num_kv_heads, cfg.head_dim, S, "cpu", torch.float64)
-    a = att(x[:, :3], pos[:, :3], c3, 0)
-    c3.advance(3)
-    b = att(x[:, 3:], pos[:, 3:], c3, 0)
-    torch.testing.assert_close(full, torch.cat([a, b], 1), rtol=1e-10, atol=1e-10)
+    c3 = mk(S)
+    a = _run(att, rope, x[:, :3], c3, 0)
+    b = _run(att, rope, x[:, 3:], c3, 3)
+    torch.testing.assert_close(full, torch.cat([a, b], 1), rtol=1e-5, atol=1e-7)
+    # decode over the whole cache with the positions after the current one masked
+    L = 12
+    c4 = mk(L)
+    ar = torch.arange(L)
+    outs = []
+    for t in range(S):
+        m = torch.zeros(1, L, dtype=torch.float64).masked_fill_(ar > t, float("-inf"))
+        outs.append(_run(att, rope, x[:, t:t + 1], c4, t, mask=m, kv_len=L))
+    torch.testing.assert_close(full, torch.cat(outs, 1), rtol=1e-5, atol=1e-7)
 
 
-def test_gqa_equals_repeated_heads_mha():
-    torch.manual_seed(1)
-    cfg = _cfg()
-    att = Attention(cfg).double()
-    B, S, nh, nkv, hd = 1, 5, cfg.num_attention_heads, cfg.num_kv_heads, cfg.head_dim
+def test_gqa_equals_textbook_attention():
+    cfg, att, rope = _setup(1)
+    B, S, nh, nkv, hd = 2, 5, cfg.num_attention_heads, cfg.num_kv_heads, cfg.head_dim
     x = torch.randn(B, S, cfg.hidden_dim, dtype=torch.float64)
     cache = KVCache(1, B, nkv, hd, S, "cpu", torch.float64)
-    pos = torch.arange(S).unsqueeze(0)
-    got = att(x, pos, cache, 0)
-    # textbook causal attention, written out per head
+    got = _run(att, rope, x, cache, 0)
     q = (x @ att.q_proj.weight.T).view(B, S, nh, hd).transpose(1, 2)
     k = (x @ att.k_proj.weight.T).view(B, S, nkv, hd).transpose(1, 2)
     v = (x @ att.v_proj.weight.T).view(B, S, nkv, hd).transpose(1, 2)
-    cos, sin = att.rope(pos)
-    q, k = apply_rotary(q, k, cos.double(), sin.double())
+    cos, sin = rope(torch.arange(S))
+    q, k = apply_rotary(q, k, cos, sin)
     o = torch.zeros(B, nh, S, hd, dtype=torch.float64)
     for h in range(nh):
-        kh, vh = k[:, h * nkv // nh], v[:, h * nkv // nh]
+        kh, vh = k[:, h // (nh // nkv)], v[:, h // (nh // nkv)]
         for i in range(S):
             sc = (q[:, h, i:i + 1] @ kh[:, :i + 1].transpose(1, 2)) / math.sqrt(hd)
             o[:, h, i] = (torch.softmax(sc, -1) @ vh[:, :i + 1])[:, 0]
     ref = o.transpose(1, 2).reshape(B, S, nh * hd) @ att.o_proj.weight.T
-    # the module's softmax runs in fp32 (as the reference's): fp32-level agreement
     torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-6)
+    # the cache holds the rotated keys (transposed) and the values
+    torch.testing.assert_close(cache.kt[0][..., :S], k.transpose(2, 3))
+    torch.testing.assert_close(cache.v[0][:, :, :S], v)
 
 
 def test_rope_norm_and_relative_position():
@@ -74,7 +95,7 @@ def test_rope_norm_and_relative_position():
     k = torch.randn(1, 1, 1, 16, dtype=torch.float64)
 
     def rot(v, p):
-        c, s = rope(torch.tensor([[p]]))
+        c, s = rope(torch.tensor([p]))
         return apply_rotary(v, v, c.double(), s.double())[0]
 
     for p in (0, 5, 40):
