@@ -132,28 +132,80 @@ class Attention(nn.Module):
         self.v_proj = nn.Linear(H, self.nkv * self.hd, bias=False)
         self.o_proj = nn.Linear(self.nh * self.hd, H, bias=False)
 
-    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
+    def _qkv_weight(self) -> torch.Tensor:
+        """q, k and v projection weights stacked into one matrix (one GEMM),
+        rebuilt when a weight is replaced or modified."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+        key = tuple((w.data_ptr(), w._version) for w in ws)
+        if getattr(self, "_wqkv_key", None) != key:
+            self._wqkv = torch.cat([w.detach() for w in ws], 0)
+            self._wqkv_key = key
+        return self._wqkv
+
+    def forward(self, x: torch.Tensor, rope: "RotaryEmbedding", pos: torch.Tensor,
                 cache: KVCache, layer: int, kv_len: int,
                 mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """x [B, S, H]; cos, sin [S, head_dim] at positions pos [S]; attends
-        over the cache's first kv_len positions, adding mask [S, kv_len]
-        (0 / -inf) when given."""
+        """x [B, S, H]; tokens at positions pos [S] (int64, x's device);
+        attends over the cache's first kv_len positions, adding mask
+        [S, kv_len] (0 / -inf) when given.  On the GPU the projections run
+        as one GEMM and RoPE + the cache append as one kernel
+        (hn_rope_append); on the CPU, the same steps in torch."""
         B, S, _ = x.shape
         nh, nkv, hd = self.nh, self.nkv, self.hd
-        q = self.q_proj(x).view(B, S, nh, hd).transpose(1, 2)
-        k = self.k_proj(x).view(B, S, nkv, hd).transpose(1, 2)
-        v = self.v_proj(x).view(B, S, nkv, hd).transpose(1, 2)
-        q, k = apply_rotary(q, k, cos.to(q.dtype), sin.to(q.dtype))
-        cache.update(layer, k, v, pos)
-        kt, vv = cache.get(layer, kv_len)
         rep = nh // nkv
-        qg = q.reshape(B, nkv, rep * S, hd)  # rows: (head within the group, token)
+        if x.is_cuda:
+            from .. import _lib
+            # positions are < cache.max_len (checked by the callers), so the
+            # RoPE table rows read are in range
+            assert cache.max_len <= rope.cos_cached.shape[0], "RoPE table shorter than the cache"
+            qkv = F.linear(x.reshape(B * S, -1), self._qkv_weight())
+            wq, wk = nh * hd, nkv * hd
+            qg = torch.empty((B, nkv, rep * S, hd), dtype=x.dtype, device=x.device)
+            ld = qkv.stride(0)
+            base = qkv.data_ptr()
+            _lib.call("hn_rope_append", base, ld, base + 2 * wq, ld, base + 2 * (wq + wk), ld,
+                      _lib.ptr(rope.cos_cached), _lib.ptr(rope.sin_cached), _lib.ptr(pos), B, S,
+                      nh, nkv, hd, _lib.ptr(qg), _lib.ptr(cache.kt[layer]),
+                      _lib.ptr(cache.v[layer]), cache.max_len, _lib.stream(x.device))
+        else:
+            q = self.q_proj(x).view(B, S, nh, hd).transpose(1, 2)
+            k = self.k_proj(x).view(B, S, nkv, hd).transpose(1, 2)
+            v = self.v_proj(x).view(B, S, nkv, hd).transpose(1, 2)
+            cos, sin = rope(pos)
+            q, k = apply_rotary(q, k, cos.to(q.dtype), sin.to(q.dtype))
+            cache.update(layer, k, v, pos)
+            qg = q.reshape(B, nkv, rep * S, hd)  # rows: (head within the group, token)
+        kt, vv = cache.get(layer, kv_len)
         scores = torch.matmul(qg, kt) / math.sqrt(hd)  # [B, nkv, rep * S, kv_len]
         if mask is not None:
             scores = (scores.view(B, nkv, rep, S, kv_len) + mask).view(B, nkv, rep * S, kv_len)
-        p = F.softmax(scores, dim=-1, dtype=torch.float32).to(q.dtype)
+        p = F.softmax(scores, dim=-1, dtype=torch.float32).to(qg.dtype)
         o = torch.matmul(p, vv).view(B, nh, S, hd)
         return self.o_proj(o.transpose(1, 2).reshape(B, S, nh * hd))
+
+
+def add_rmsnorm(x: torch.Tensor, res: Optional[torch.Tensor], norm: RMSNorm):
+    """(x + res, norm(x + res)); res None: (x, norm(x)).  On the GPU one
+    kernel (hn_add_rmsnorm) with the torch formulation's fp16 add and fp32
+    normalisation."""
+    if not x.is_cuda:
+        if res is not None:
+            x = x + res
+        return x, norm(x)
+    from .. import _lib
+    H = x.shape[-1]
+    assert norm.weight.dtype == torch.float16 and x.dtype == torch.float16
+    x2 = x.reshape(-1, H).contiguous()
+    T = x2.shape[0]
+    out = torch.empty_like(x2)
+    xo, r2 = x2, None
+    if res is not None:
+        r2 = res.reshape(-1, H).contiguous()
+        xo = torch.empty_like(x2)
+    _lib.call("hn_add_rmsnorm", _lib.ptr(x2), H, _lib.ptr(r2), H,
+              _lib.ptr(xo) if res is not None else None, H, _lib.ptr(norm.weight), _lib.ptr(out),
+              H, T, H, norm.eps, _lib.stream(x.device))
+    return xo.view(x.shape), out.view(x.shape)
 
 
 def causal_mask(start: int, S: int, device, dtype=torch.float16) -> torch.Tensor:
@@ -172,10 +224,16 @@ class DecoderBlock(nn.Module):
         self.moe = MixtralMoELayer(cfg.hidden_dim, cfg.num_experts, cfg.experts_per_token,
                                    layer_idx=layer_idx, slots=slots)
 
-    def forward(self, x, cos, sin, pos, cache: KVCache, kv_len: int, mask, top_k: int):
-        x = x + self.self_attn(self.input_layernorm(x), cos, sin, pos, cache, self.layer_idx,
-                               kv_len, mask)
-        return x + self.moe(self.post_attention_layernorm(x), top_k=top_k)
+    def forward(self, x, rope, pos, cache: KVCache, kv_len: int, mask, top_k: int,
+                pending: Optional[torch.Tensor] = None):
+        """x + attn(norm(x)), then + moe(norm(.)) (model/mixtral.py:407-427).
+        Returns (x after the attention residual, the MoE output still to be
+        added): the caller folds that add into the next RMSNorm.  pending: the
+        previous block's MoE output, added to x first."""
+        x, h = add_rmsnorm(x, pending, self.input_layernorm)
+        a = self.self_attn(h, rope, pos, cache, self.layer_idx, kv_len, mask)
+        x, h = add_rmsnorm(x, a, self.post_attention_layernorm)
+        return x, self.moe(h, top_k=top_k)
 
 
 class MixtralDecoder(nn.Module):
@@ -206,11 +264,12 @@ class MixtralDecoder(nn.Module):
         """One pass over every layer: tokens input_ids [B, S] at positions pos
         [S] (device int64), attention over the first kv_len cache positions.
         Does not move cache.cur_len."""
-        cos, sin = self.rotary(pos)
         x = self.embed_tokens(input_ids)
+        pending = None
         for blk in self.layers:
-            x = blk(x, cos, sin, pos, cache, kv_len, mask, top_k)
-        return self.lm_head(self.norm(x))
+            x, pending = blk(x, self.rotary, pos, cache, kv_len, mask, top_k, pending)
+        _, h = add_rmsnorm(x, pending, self.norm)
+        return self.lm_head(h)
 
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, cache: KVCache,
@@ -219,6 +278,8 @@ class MixtralDecoder(nn.Module):
         cache (prefill when it is empty: top-2; decode: decode_top_k)."""
         B, S = input_ids.shape
         start = cache.cur_len
+        if start + S > cache.max_len:
+            raise RuntimeError(f"KV cache full ({start + S} > {cache.max_len})")
         if top_k is None:
             top_k = 2 if start == 0 else self.decode_top_k
         pos = torch.arange(start, start + S, device=input_ids.device)
@@ -264,6 +325,8 @@ class GraphDecoder:
         self.model, self.cache = model, cache
         dev = tok.device
         L = cache.max_len
+        if cache.cur_len >= L:
+            raise RuntimeError(f"KV cache full ({L} positions)")
         self.tok = tok.clone()
         self.pos = torch.full((1,), cache.cur_len, dtype=torch.int64, device=dev)
         self.ar = torch.arange(L, device=dev)
@@ -290,6 +353,8 @@ class GraphDecoder:
 
     def step(self) -> torch.Tensor:
         """One decode step; returns the static buffer of the tokens it chose."""
+        if self.cache.cur_len >= self.cache.max_len:
+            raise RuntimeError(f"KV cache full ({self.cache.max_len} positions)")
         self.graph.replay()
         self.cache.advance(1)
         return self.tok

@@ -229,6 +229,31 @@ int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const void* tabl
                                  long E, long rows, long H, long I, long group, void* h_ws,
                                  void* y_perm, void* work, long work_bytes, void* stream);
 
+/* Decoder-step helpers around the MoE layer (the whole-model decode harness).
+ *
+ * hn_add_rmsnorm: for rows t < T of H fp16 (H % 8 == 0, H <= 8192):
+ *   x' = fp16(x[t] + res[t]) when res is given (written to x_out, which may
+ *   alias x), else x' = x[t];  out[t] = fp16(w * (x' * rsqrt(mean(x'^2) + eps)))
+ *   in fp32.  Replaces the residual add and RMSNorm of the reference's decoder
+ *   block (model/mixtral.py:23-37, 407-427); the mean's fp32 summation order
+ *   is its own (outputs within an fp16 ulp of the torch formulation).
+ *
+ * hn_rope_append: q [B*S, nh*hd], k / v [B*S, nkv*hd] (row b*S + s, fp16), the
+ *   fp32 RoPE tables cos_t / sin_t [max_pos, hd], positions pos [S] (int64, on
+ *   the device).  Writes the rotated queries to q_out [B, nkv, nh/nkv, S, hd]
+ *   (the query heads sharing a KV head stacked), the rotated keys to
+ *   kt [B, nkv, hd, max_len] at column pos[s] and the values to
+ *   vc [B, nkv, max_len, hd] at row pos[s].  RoPE in the reference's fp16 steps
+ *   (apply_rotary_pos_emb, model/mixtral.py:82-101; cache update,
+ *   cache/kv_cache.py:26-284), bit for bit. */
+int hn_add_rmsnorm(const void* x, long ld_x, const void* res, long ld_r, void* x_out,
+                   long ld_xo, const void* w, void* out, long ld_o, long T, long H, float eps,
+                   void* stream);
+int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k, const void* v, long ld_v,
+                   const float* cos_t, const float* sin_t, const long* pos, long B, long S,
+                   long nh, long nkv, long hd, void* q_out, void* kt, void* vc, long max_len,
+                   void* stream);
+
 /* Decode kernel family for hn_int4_linear, hn_int4_gate_up_silu,
  * hn_expert_mlp_int4 and hn_grouped_expert_mlp_int4 (process-wide):
  *   0  automatic: the persistent streaming kernels for group 128 and at most

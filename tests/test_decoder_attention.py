@@ -31,10 +31,9 @@ def _setup(seed):
 def _run(att, rope, x, cache, start, mask=None, kv_len=None):
     S = x.shape[1]
     pos = torch.arange(start, start + S)
-    cos, sin = rope(pos)
     if mask is None and S > 1:
         mask = causal_mask(start, S, "cpu", torch.float64)
-    return att(x, cos, sin, pos, cache, 0, kv_len or start + S, mask)
+    return att(x, rope, pos, cache, 0, kv_len or start + S, mask)
 
 
 def test_prefill_equals_stepwise_decode():

@@ -34,10 +34,9 @@ def _ref_forward(model, ids, cache, top_k, cpu_experts):
     start = cache.cur_len
     pos = torch.arange(start, start + S, device=ids.device)
     mask = causal_mask(start, S, ids.device) if S > 1 else None
-    cos, sin = model.rotary(pos)
     x = model.embed_tokens(ids)
     for blk in model.layers:
-        x = x + blk.self_attn(blk.input_layernorm(x), cos, sin, pos, cache, blk.layer_idx,
+        x = x + blk.self_attn(blk.input_layernorm(x), model.rotary, pos, cache, blk.layer_idx,
                               start + S, mask)
         h = blk.post_attention_layernorm(x)
         ro = blk.moe.router(h, top_k_override=top_k)

@@ -1,0 +1,95 @@
+"""GPU tests of the decoder-step kernels (hn_add_rmsnorm, hn_rope_append)
+against the reference's torch formulation of the same steps
+(model/mixtral.py:23-37 RMSNorm, 82-101 RoPE; the KV-cache append):
+the residual add, RoPE and the cache writes bit for bit; RMSNorm within one
+fp16 ulp (fp32 mean in another summation order), nearly all elements equal."""
+import pytest
+import torch
+
+from hydranet_amd import _lib
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _torch_rmsnorm(x, w, eps):
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (w * xf).to(torch.float16)
+
+
+@pytest.mark.parametrize("T,H", [(1, 4096), (64, 4096), (5, 512), (3, 8192), (0, 4096)])
+def test_add_rmsnorm(T, H):
+    g = torch.Generator(device=DEV).manual_seed(T * 7 + H)
+    x = torch.randn(T, H, generator=g, device=DEV).half()
+    r = (torch.randn(T, H, generator=g, device=DEV) * 0.5).half()
+    w = (1 + 0.1 * torch.randn(H, generator=g, device=DEV)).half()
+    st = _lib.stream()
+    for res in (None, r):
+        out = torch.empty_like(x)
+        xo = torch.empty_like(x)
+        _lib.call("hn_add_rmsnorm", _lib.ptr(x), H, _lib.ptr(res), H,
+                  _lib.ptr(xo) if res is not None else None, H, _lib.ptr(w), _lib.ptr(out), H,
+                  T, H, 1e-5, st)
+        xs = x if res is None else x + res
+        if res is not None:
+            assert torch.equal(xo, xs)
+        ref = _torch_rmsnorm(xs, w, 1e-5)
+        if T == 0:
+            continue
+        ulp = torch.pow(2.0, torch.floor(torch.log2(ref.float().abs().clamp_min(2.0 ** -14))) - 10)
+        assert bool(((out.float() - ref.float()).abs() <= ulp).all())
+        assert (out != ref).float().mean().item() < 0.02
+
+
+def test_add_rmsnorm_in_place_residual():
+    """x_out may alias x (the residual stream updated in place)."""
+    H, T = 1024, 4
+    x = torch.randn(T, H, device=DEV).half()
+    r = torch.randn(T, H, device=DEV).half()
+    w = torch.ones(H, device=DEV).half()
+    want = x + r
+    out = torch.empty_like(x)
+    _lib.call("hn_add_rmsnorm", _lib.ptr(x), H, _lib.ptr(r), H, _lib.ptr(x), H, _lib.ptr(w),
+              _lib.ptr(out), H, T, H, 1e-5, _lib.stream())
+    assert torch.equal(x, want)
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+@pytest.mark.parametrize("B,S,start", [(3, 1, 7), (2, 5, 0), (2, 4, 9), (64, 1, 600)])
+def test_rope_append(B, S, start):
+    nh, nkv, hd, L = 8, 2, 64, 1024
+    rep = nh // nkv
+    g = torch.Generator(device=DEV).manual_seed(B * 100 + S)
+    q = torch.randn(B * S, nh * hd, generator=g, device=DEV).half()
+    k = torch.randn(B * S, nkv * hd, generator=g, device=DEV).half()
+    v = torch.randn(B * S, nkv * hd, generator=g, device=DEV).half()
+    inv = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=DEV).float() / hd))
+    t = torch.arange(L, device=DEV, dtype=torch.float32)
+    emb = torch.cat([torch.outer(t, inv)] * 2, -1)
+    cos_t, sin_t = emb.cos().contiguous(), emb.sin().contiguous()
+    pos = torch.arange(start, start + S, device=DEV)
+    qg = torch.full((B, nkv, rep * S, hd), 7.0, dtype=torch.float16, device=DEV)
+    kt = torch.zeros(B, nkv, hd, L, dtype=torch.float16, device=DEV)
+    vc = torch.zeros(B, nkv, L, hd, dtype=torch.float16, device=DEV)
+    _lib.call("hn_rope_append", _lib.ptr(q), nh * hd, _lib.ptr(k), nkv * hd, _lib.ptr(v),
+              nkv * hd, _lib.ptr(cos_t), _lib.ptr(sin_t), _lib.ptr(pos), B, S, nh, nkv, hd,
+              _lib.ptr(qg), _lib.ptr(kt), _lib.ptr(vc), L, _lib.stream())
+    # torch formulation: fp16 tables, fp16 products and sum
+    c, s = cos_t[pos].half(), sin_t[pos].half()
+    qh = q.view(B, S, nh, hd).transpose(1, 2)
+    kh = k.view(B, S, nkv, hd).transpose(1, 2)
+    vh = v.view(B, S, nkv, hd).transpose(1, 2)
+    q_ref = qh * c + _rotate_half(qh) * s
+    k_ref = kh * c + _rotate_half(kh) * s
+    assert torch.equal(qg, q_ref.reshape(B, nkv, rep * S, hd))
+    kt_ref = torch.zeros_like(kt)
+    kt_ref[..., start:start + S] = k_ref.transpose(2, 3)
+    vc_ref = torch.zeros_like(vc)
+    vc_ref[:, :, start:start + S] = vh
+    assert torch.equal(kt, kt_ref)
+    assert torch.equal(vc, vc_ref)
