@@ -323,7 +323,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     for (int u = 0; u < LG; ++u) acc[u] = float4_t{0.f, 0.f, 0.f, 0.f};
     // passes of up to KST steps whose loads go out together (steps past the
     // slice repeat the last one and are not multiplied)
-    constexpr int KST = LG == 1 ? 8 : (LG == 2 ? 4 : 2);
+    constexpr int KST = LG == 1 ? 8 : 4;
     for (int s0 = 0; s0 < steps; s0 += KST) {
       half8_t bv[KST], av[KST][LG];
 #pragma unroll
