@@ -312,50 +312,66 @@ class MixtralDecoder(nn.Module):
 
 
 class GraphDecoder:
-    """Greedy decode steps replayed from one captured HIP graph.
+    """Greedy decode steps replayed from captured HIP graphs.
 
-    The captured step attends over the whole cache (max_len positions, those
-    after the current one masked to -inf, so they add exp(-inf) = 0 to the
-    softmax), reads its position from a device scalar, writes the next tokens
+    A captured step attends over the first L cache positions, L the current
+    length rounded up to a multiple of `bucket` (positions past the current
+    one masked to -inf, so they add exp(-inf) = 0 to the softmax); one graph
+    per L the decode will reach, all captured up front into one memory pool.
+    The step reads its position from a device scalar, writes the next tokens
     into a static buffer and advances the position itself: successive replays
     need no host work and no host-device sync.  `tok` holds the tokens fed to
-    the next step; `logits` the last step's logits."""
+    the next step; `logits` the last step's logits (valid until the next)."""
 
-    def __init__(self, model: MixtralDecoder, cache: KVCache, tok: torch.Tensor):
+    def __init__(self, model: MixtralDecoder, cache: KVCache, tok: torch.Tensor,
+                 bucket: int = 64):
         self.model, self.cache = model, cache
         dev = tok.device
-        L = cache.max_len
-        if cache.cur_len >= L:
-            raise RuntimeError(f"KV cache full ({L} positions)")
+        if cache.cur_len >= cache.max_len:
+            raise RuntimeError(f"KV cache full ({cache.max_len} positions)")
+        self.bucket = bucket
         self.tok = tok.clone()
         self.pos = torch.full((1,), cache.cur_len, dtype=torch.int64, device=dev)
-        self.ar = torch.arange(L, device=dev)
+        self.ar = torch.arange(cache.max_len, device=dev)
+        self.graphs = {}  # L -> (graph, logits)
+        self.logits = None
         tok0 = self.tok.clone()
-        k = model.decode_top_k
-
-        def body():
-            mask = torch.zeros((1, L), dtype=torch.float16, device=dev).masked_fill_(
-                self.ar > self.pos, float("-inf"))
-            self.logits = model.step(self.tok, self.pos, cache, L, mask, k)
-            self.tok.copy_(self.logits[:, -1].argmax(-1, keepdim=True))
-            self.pos.add_(1)
-
+        lens = sorted({self._len(n) for n in range(cache.cur_len, cache.max_len)})
         s = torch.cuda.Stream(device=dev)
         s.wait_stream(torch.cuda.current_stream(dev))
         with torch.no_grad(), torch.cuda.stream(s):
-            body()  # warm-up (allocator, library handles): writes position cur_len, rewritten below
+            self._body(lens[0])  # warm-up (allocator, library handles): rewritten below
         torch.cuda.current_stream(dev).wait_stream(s)
         self.pos.fill_(cache.cur_len)
         self.tok.copy_(tok0)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.no_grad(), torch.cuda.graph(self.graph):
-            body()
+        pool = None
+        for L in lens:  # capture runs nothing: the buffers keep their values
+            g = torch.cuda.CUDAGraph()
+            with torch.no_grad(), torch.cuda.graph(g, pool=pool):
+                logits = self._body(L)
+            pool = g.pool() if pool is None else pool
+            self.graphs[L] = (g, logits)
+
+    def _len(self, cur_len: int) -> int:
+        """Cache positions a step at length cur_len attends over."""
+        n = -(-(cur_len + 1) // self.bucket) * self.bucket
+        return min(n, self.cache.max_len)
+
+    def _body(self, L: int) -> torch.Tensor:
+        mask = torch.zeros((1, L), dtype=torch.float16, device=self.tok.device).masked_fill_(
+            self.ar[:L] > self.pos, float("-inf"))
+        logits = self.model.step(self.tok, self.pos, self.cache, L, mask,
+                                 self.model.decode_top_k)
+        self.tok.copy_(logits[:, -1].argmax(-1, keepdim=True))
+        self.pos.add_(1)
+        return logits
 
     def step(self) -> torch.Tensor:
         """One decode step; returns the static buffer of the tokens it chose."""
         if self.cache.cur_len >= self.cache.max_len:
             raise RuntimeError(f"KV cache full ({self.cache.max_len} positions)")
-        self.graph.replay()
+        g, self.logits = self.graphs[self._len(self.cache.cur_len)]
+        g.replay()
         self.cache.advance(1)
         return self.tok
 

@@ -339,7 +339,7 @@ class MixtralMoELayer(nn.Module):
                 out = moe_dispatch(r, self.experts.table_for(r.idx))
             if not rt.training:
                 sel = r.idx.view(-1).long()  # no host sync: graph-capturable
-                rt.usage_counts.scatter_add_(0, sel, torch.ones_like(sel))
+                rt.usage_counts.scatter_add_(0, sel, rt._one.expand_as(sel))
             return out.view(B, S, H)
         ro = rt(hidden_states, top_k_override=top_k)
         idx = ro.expert_indices.reshape(T, top_k)

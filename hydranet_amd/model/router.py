@@ -91,6 +91,7 @@ class TopKRouter(nn.Module):
         self.affinity_bonus = affinity_bonus
         self.entropy_threshold = entropy_threshold
         self.enable_affinity_bonus = enable_affinity_bonus
+        self.register_buffer("_one", torch.ones(1, dtype=torch.long), persistent=False)
         self.register_buffer("usage_counts", torch.zeros(num_experts, dtype=torch.long),
                              persistent=False)
         self._is_cached_fn: Optional[Callable[[int], bool]] = None
@@ -122,7 +123,7 @@ class TopKRouter(nn.Module):
         if not self.training:
             # scatter_add_ rather than bincount: no device-to-host sync (graph-capturable)
             flat = idx.view(-1).long()
-            self.usage_counts.scatter_add_(0, flat, torch.ones_like(flat))
+            self.usage_counts.scatter_add_(0, flat, self._one.expand_as(flat))
         return RouterOutput(idx.view(B, S, k), w.view(B, S, k).to(hidden_states.dtype),
                             logits.view(B, S, self.num_experts))
 

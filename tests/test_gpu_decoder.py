@@ -95,7 +95,7 @@ def test_graph_decode_matches_eager():
         l2 = model(ids, c2)
         assert torch.equal(l1, l2)
         tok = l1[:, -1].argmax(-1, keepdim=True)
-        gd = GraphDecoder(model, c1, tok)
+        gd = GraphDecoder(model, c1, tok, bucket=4)  # graphs for L = 8, 12, 14
         for step in range(steps):
             eager = model(tok, c2)
             gd.step()
@@ -105,6 +105,7 @@ def test_graph_decode_matches_eager():
             tok = eager[:, -1].argmax(-1, keepdim=True)
             gd.tok.copy_(tok)  # both continue from the eager tokens
     assert c1.cur_len == c2.cur_len == S + steps
+    assert sorted(gd.graphs) == [8, 12, 14]
 
 
 def test_generate_greedy_shapes_and_determinism():
