@@ -7,7 +7,8 @@ Prints ONE JSON line.  A "step" is one pass of the hot path over one batch of
 synthetic input already resident in HBM:
 
   c2  (default, the headline) one Mixtral MoE layer at decode, T = 1, 4, 16
-      (value: T = 16): route + grouped gate/up + down + unpermute
+      (value: T = 16): route + grouped gate/up + down + unpermute; then the
+      c5 decoder run (decoder_tokens_per_s; --skip-c5 leaves it out)
   c1  one Mixtral expert SwiGLU (H 4096, I 14336, INT4 g128), T tokens (default 1)
   c3  one GLM-4.5-Air MoE layer at decode (T = 32, 128 experts, shared expert)
   c4  one Mixtral MoE layer at prefill (2048 tokens, Zipf-skewed routing)
@@ -689,6 +690,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--decode-tokens", type=int, default=256, help="c5: tokens generated")
     ap.add_argument("--warmup-decode", type=int, default=3, help="c5: untimed decode forwards")
+    ap.add_argument("--skip-c5", action="store_true",
+                    help="c2: leave out the whole-decoder tokens/s run (workload c5)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-path", type=int, default=0, choices=[0, 1],
@@ -776,6 +779,13 @@ def main():
                          "tokens": 16, "experts": 8, "top_k": 2, "layers_rotated": 4,
                          "sweep": sweep, "c1_single_expert_T1": c1,
                          "graph": head["graph"]}
+        if not args.skip_c5:
+            # the metric's second half: whole-decoder decode tokens/s (workload c5)
+            torch.cuda.empty_cache()
+            c5 = bench_c5(args)
+            _log("c5", c5)
+            res["decoder_tokens_per_s"] = c5["tokens_per_s"]
+            res["config"]["c5_decoder"] = c5
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
