@@ -396,3 +396,25 @@ def test_decode_layer_fused_routing_matches_route_then_experts(T, mixtral_expert
     x2 = torch.randn(T, 4096, generator=g).half().to(DEV)
     out2, _ = moe_decode_layer(x2, gw, 2, table)
     assert torch.equal(out2, moe_dispatch(moe_route(x2, 2, 0, gate_w=gw), table))
+
+
+@pytest.mark.parametrize("T", [0, 1])
+def test_moe_layers_empty_and_single_token_batches(T, mixtral_experts):
+    """An empty batch gives an empty output (no launch reads or writes rows);
+    a single token routes to two experts, the other six get no rows."""
+    from hydranet_amd.model.moe import MixtralMoELayer, moe_experts_forward, ExpertTable
+    slots, cpu = mixtral_experts
+    layer = MixtralMoELayer(4096, 8, 2, slots=slots).to(DEV)
+    layer.router.gate.weight.data = _randn(7, (8, 4096), 0.02).to(DEV)
+    h = _randn(300 + T, (1, T, 4096)).to(DEV)
+    out = layer(h, top_k=2)
+    assert out.shape == (1, T, 4096)
+    idx = torch.zeros((T, 2), dtype=torch.int32, device=DEV)
+    w = torch.ones((T, 2), dtype=torch.float16, device=DEV)
+    y = moe_experts_forward(h.view(T, 4096), idx, w, ExpertTable.from_slots(slots))
+    assert y.shape == (T, 4096)
+    if T:
+        ro = layer.router(h, top_k_override=2)
+        ref = torch_ref.moe_dispatch(h.view(T, 4096).cpu(), ro.expert_indices.view(T, 2).long().cpu(),
+                                     ro.expert_weights.view(T, 2).cpu(), cpu)
+        _close(out.view(T, 4096), ref)
