@@ -158,13 +158,17 @@ class Attention(nn.Module):
             # positions are < cache.max_len (checked by the callers), so the
             # RoPE table rows read are in range
             assert cache.max_len <= rope.cos_cached.shape[0], "RoPE table shorter than the cache"
+            assert x.dtype == torch.float16 and pos.dtype == torch.int64
+            # the kernel reads fp32 tables (a module-wide .half() would have cast them)
+            cos_t = rope.cos_cached.float().contiguous()
+            sin_t = rope.sin_cached.float().contiguous()
             qkv = F.linear(x.reshape(B * S, -1), self._qkv_weight())
             wq, wk = nh * hd, nkv * hd
             qg = torch.empty((B, nkv, rep * S, hd), dtype=x.dtype, device=x.device)
             ld = qkv.stride(0)
             base = qkv.data_ptr()
             _lib.call("hn_rope_append", base, ld, base + 2 * wq, ld, base + 2 * (wq + wk), ld,
-                      _lib.ptr(rope.cos_cached), _lib.ptr(rope.sin_cached), _lib.ptr(pos), B, S,
+                      _lib.ptr(cos_t), _lib.ptr(sin_t), _lib.ptr(pos), B, S,
                       nh, nkv, hd, _lib.ptr(qg), _lib.ptr(cache.kt[layer]),
                       _lib.ptr(cache.v[layer]), cache.max_len, _lib.stream(x.device))
         else:
