@@ -835,6 +835,7 @@ struct StreamPlan {
   bool wide;  // vector scale loads (set by the caller after its alignment checks)
   int lpw, nbuf, kw, tc, ldx, npair;
   int lds;  // dynamic LDS bytes per workgroup
+  int occ;  // workgroups per CU
 };
 
 // One workgroup per CU of KW <= 8 waves; LPW (2..16) groups of 128 k per wave
@@ -869,6 +870,9 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   if (p.tc < 1) return p;
   p.lds = p.tc * per_tok + cs + red + meta;
   if (route && p.tc * per_tok + cs + red < kRouteScratch) return p;
+  // single-matrix (down) launches: two workgroups per CU when their LDS and
+  // waves fit, for more loads in flight where a column has little work
+  p.occ = (mats == 1 && !route && 2 * (p.lds + kStaticLds) <= kLdsPerCu && 2 * kw <= 16) ? 2 : 1;
   p.ok = true;
   return p;
 }
@@ -898,7 +902,7 @@ int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, h
     if (!attr) (void)hipGetLastError();  // plans then stay within 64 KiB
   }
   if (!attr && p.lds > 64 * 1024 - kStaticLds) return HN_NOT_HANDLED;
-  hipLaunchKernelGGL(kern, dim3(num_cus()), dim3(p.kw * 64), (size_t)p.lds, s, A, g.table,
+  hipLaunchKernelGGL(kern, dim3(num_cus() * p.occ), dim3(p.kw * 64), (size_t)p.lds, s, A, g.table,
                      g.active, g.n_active, g.offsets);
   return 0;
 }
