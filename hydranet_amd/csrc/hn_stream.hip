@@ -870,9 +870,12 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   if (p.tc < 1) return p;
   p.lds = p.tc * per_tok + cs + red + meta;
   if (route && p.tc * per_tok + cs + red < kRouteScratch) return p;
-  // single-matrix (down) launches: two workgroups per CU when their LDS and
-  // waves fit, for more loads in flight where a column has little work
-  p.occ = (mats == 1 && !route && 2 * (p.lds + kStaticLds) <= kLdsPerCu && 2 * kw <= 16) ? 2 : 1;
+  // single-matrix (down) launches of 4 or more rows per matrix: two
+  // workgroups per CU when their LDS and waves fit, for more loads in flight
+  // where a column has little work (measured: gate/up launches and 1-row
+  // launches are faster with one)
+  p.occ = (mats == 1 && !route && rows >= 4 && 2 * (p.lds + kStaticLds) <= kLdsPerCu &&
+           2 * kw <= 16) ? 2 : 1;
   p.ok = true;
   return p;
 }
