@@ -183,8 +183,9 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const h16* __restrict__
     *reinterpret_cast<half8_t*>(dst + c) = *reinterpret_cast<const half8_t*>(src + c);
 }
 
-// Workgroup (token, column block): each thread owns 8 consecutive columns of
-// the block's stride (gridDim.y blocks split H).  KS = 0:
+// Workgroup (token, column block): each thread owns 8 consecutive columns
+// per pass (blockDim.x * 8 columns per block and pass, gridDim.y blocks
+// interleaved over H).  KS = 0:
 // y is fp16 [rows, ld_y]; KS > 0: y is given as KS fp32 partial sums
 // part[j * ks_stride + row * ld_y] (a K-split down projection), added in
 // slice order and rounded to fp16 once: the expert output the unsplit kernel
@@ -553,10 +554,13 @@ extern "C" int hn_moe_gather(const void* x, long ld_x, const int* perm, long k,
   return 0;
 }
 
-// Column blocks of the unpermute grid: 2048 columns (256 threads x 8) per
-// workgroup, at most 8, so that a small batch still spreads over the CUs.
-static unsigned unpermute_blocks(long H) {
-  const long b = (H + 2047) / 2048;
+// Unpermute grid: (token, column block) workgroups of 8 columns per thread;
+// batches under 64 tokens use 64-thread workgroups (512 columns each) so
+// that a small batch still spreads over the CUs.  At most 8 blocks per token.
+static unsigned unpermute_threads(long T) { return T < 64 ? 64u : 256u; }
+static unsigned unpermute_blocks(long H, long T) {
+  const long cols = 8L * unpermute_threads(T);
+  const long b = (H + cols - 1) / cols;
   return (unsigned)(b < 1 ? 1 : (b > 8 ? 8 : b));
 }
 
@@ -568,7 +572,8 @@ extern "C" int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, c
                    (!shared || (al16(shared) && ld_sh % 8 == 0)),
                "hn_moe_unpermute: rows must be 16-byte aligned");
   if (T <= 0) return 0;
-  hipLaunchKernelGGL(moe_unpermute_kernel<0>, dim3((unsigned)T, unpermute_blocks(H)), dim3(256), 0,
+  hipLaunchKernelGGL(moe_unpermute_kernel<0>, dim3((unsigned)T, unpermute_blocks(H, T)),
+                     dim3(unpermute_threads(T)), 0,
                      (hipStream_t)stream, (const h16*)y_perm, (const float*)nullptr, 0L, ld_y,
                      inv, idx, (const h16*)w, (int)k, (const h16*)shared, ld_sh, (h16*)out, ld_o,
                      (int)H);
@@ -637,7 +642,8 @@ extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, c
                    (!shared || (al16(shared) && ld_sh % 8 == 0)),
                "hn_moe_unpermute: rows must be 16-byte aligned");
   if (T <= 0) return 0;
-  hipLaunchKernelGGL(moe_unpermute_kernel<4>, dim3((unsigned)T, unpermute_blocks(H)), dim3(256), 0,
+  hipLaunchKernelGGL(moe_unpermute_kernel<4>, dim3((unsigned)T, unpermute_blocks(H, T)),
+                     dim3(unpermute_threads(T)), 0,
                      (hipStream_t)stream, (const h16*)nullptr, part, ks_stride, H, inv, idx,
                      (const h16*)w, (int)k, (const h16*)shared, ld_sh, (h16*)out, ld_o, (int)H);
   HN_LAUNCH_CHECK("hn_moe_unpermute");
