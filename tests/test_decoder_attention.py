@@ -113,3 +113,24 @@ def test_rmsnorm_matches_definition():
     ref = (x.float() / torch.sqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-5)
            * torch.arange(1, 9)).half()
     torch.testing.assert_close(n(x), ref, rtol=0, atol=0)
+
+
+def test_causal_mask_brute_force():
+    for start, S in [(0, 1), (0, 5), (3, 4), (7, 1)]:
+        m = causal_mask(start, S, "cpu", torch.float32)
+        assert m.shape == (S, start + S)
+        for i in range(S):
+            for j in range(start + S):
+                want = 0.0 if j <= start + i else float("-inf")
+                assert m[i, j].item() == want, (start, S, i, j)
+
+
+def test_kv_cache_bounds():
+    c = KVCache(1, 1, 1, 4, 3, "cpu", torch.float32)
+    c.advance(3)
+    try:
+        c.advance(1)
+    except AssertionError:
+        pass
+    else:
+        raise AssertionError("advance past max_len must fail")
