@@ -15,22 +15,47 @@ pins, per fixture (all small, CPU, seeded):
   topk_router.npz       TopKRouter.forward, affinity off          (model/router.py:73-130)
   sigmoid_router.npz    GLM4SigmoidRouter.forward                 (model/glm4.py:261-309)
   blob_layout.json      BlobLayout.from_dims at Mixtral/GLM dims  (cache/packed_expert_store.py:77-108)
+  mixtral_moe_layer.npz MixtralMoELayer.forward, top-2 and top-1  (model/mixtral.py:259-370)
+                        (fp16 dequantise-then-F.linear branch, every expert registered in a
+                        CPU ExpertCacheManager, affinity off)
+  glm_moe_layer.npz     GLM4MoELayer.forward with its fp16 shared expert (model/glm4.py:365-473)
+  store_format/         pack_mixtral_experts' legacy per-expert files + metadata.json
+                        (preprocess/pack_weights.py:271-381; files kept as SHA-256 digests)
+                        and pack_to_single_blob's experts.bin / experts.idx
+                        (cache/packed_expert_store.py:627-739)
+
+The layer and store fixtures hold no weights: every expert weight comes from
+gen.py (seeded, integer arithmetic), and the fixtures record the SHA-256 of
+the packed bytes the reference's packer made from them, so a test that
+regenerates the weights can check it packs the same bytes first.
 
 Only data (inputs and the reference's outputs) is written; no reference
 source is copied.
 """
 from __future__ import annotations
 
+import hashlib
 import importlib
 import json
 import os
+import shutil
 import sys
+import tempfile
 import types
+from pathlib import Path
 
 import numpy as np
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+import gen  # noqa: E402
+
+# Layer fixtures: (H, I, group, E, top-k list, tokens (B, S), case seed)
+MIXTRAL_CASE = dict(H=128, I=256, g=128, E=8, topks=(2, 1), B=2, S=3, seed=5)
+GLM_CASE = dict(H=128, I=256, g=128, E=16, k=4, B=1, S=5, seed=6)
+# Store-format fixture: 2 layers x 2 experts
+STORE_CASE = dict(L=2, E=2, H=128, I=128, g=128, seed=7)
 
 
 def _map_reference(root: str) -> None:
@@ -181,7 +206,174 @@ def main(root: str) -> None:
                      **{f: getattr(L, f) for f in L.__dataclass_fields__}}
     with open(os.path.join(HERE, "blob_layout.json"), "w") as f:
         json.dump(lay, f, indent=1, sort_keys=True)
+
+    moe_layer_fixtures(pw, cfg)
+    store_format_fixture(pw, cfg, store)
     print("golden vectors written to", HERE)
+
+
+# ----------------------------------------------------------------------------- MoE layers
+def _packed_expert(pw, case_seed: int, e: int, H: int, I: int, g: int, layer: int = 0):
+    """The reference packer's PackedExpert of the seeded expert, its dequantised
+    fp16 weights, and the SHA-256 of its packed bytes in blob order."""
+    w = {k: torch.from_numpy(v) for k, v in gen.expert_weights(case_seed, e, H, I, layer).items()}
+    packer = pw.ExpertWeightPacker(pw.QuantConfig(bits=4, group_size=g, symmetric=True))
+    pe = packer.pack_expert(layer, e, w)
+    deq = {"gate_proj": packer.dequantize_tensor(pe.gate_proj_packed, pe.gate_proj_scales, I, H),
+           "up_proj": packer.dequantize_tensor(pe.up_proj_packed, pe.up_proj_scales, I, H),
+           "down_proj": packer.dequantize_tensor(pe.down_proj_packed, pe.down_proj_scales, H, I)}
+    h = hashlib.sha256()
+    for t in (pe.gate_proj_packed, pe.gate_proj_scales, pe.up_proj_packed, pe.up_proj_scales,
+              pe.down_proj_packed, pe.down_proj_scales):
+        h.update(t.contiguous().numpy().tobytes())
+    return pe, deq, h.hexdigest()
+
+
+def _cpu_cache_manager(cfg, model_config, n_experts: int):
+    """A CPU ExpertCacheManager with room for every expert (no eviction), no affinity."""
+    cache_mod = importlib.import_module("hydranet.cache.expert_cache")
+    half = (n_experts + 1) // 2
+    cc = cfg.ExpertCacheConfig(pinned_slots=0, hot_slots=half, probation_slots=half,
+                               enable_dynamic_slots=False, enable_affinity_bonus=False,
+                               enable_prefetch=False)
+    mgr = cache_mod.ExpertCacheManager(model_config=model_config, cache_config=cc,
+                                       device=torch.device("cpu"), dtype=torch.float16)
+    return mgr, cc
+
+
+def _assert_tie_free(logits: torch.Tensor, k: int, what: str) -> None:
+    srt = torch.sort(logits.reshape(-1, logits.shape[-1]).double(), dim=-1, descending=True)[0]
+    assert bool((srt[:, k - 1] > srt[:, k]).all()), f"{what}: a top-{k} boundary tie"
+
+
+def moe_layer_fixtures(pw, cfg) -> None:
+    mixtral = importlib.import_module("hydranet.model.mixtral")
+    glm4 = importlib.import_module("hydranet.model.glm4")
+
+    # ---- MixtralMoELayer.forward
+    C = MIXTRAL_CASE
+    H, I, g, E = C["H"], C["I"], C["g"], C["E"]
+    mc = cfg.MixtralConfig()
+    mc.num_layers, mc.num_experts, mc.hidden_dim, mc.intermediate_dim = 1, E, H, I
+    mgr, cc = _cpu_cache_manager(cfg, mc, E)
+    out = {"dims": np.array([H, I, g, E, C["seed"]])}
+    for e in range(E):
+        _, deq, digest = _packed_expert(pw, C["seed"], e, H, I, g)
+        mgr.register_expert(0, e, deq)
+        out[f"sha/{e}"] = np.array(digest)
+    layer = mixtral.MixtralMoELayer(mc, cc, 0, mgr)
+    gate = torch.from_numpy(gen.normal_f16(C["seed"] * 1000 + 901, (E, H), 0.02))
+    layer.router.gate.weight.data = gate.clone()
+    layer.eval()
+    hid = torch.from_numpy(gen.normal_f16(C["seed"] * 1000 + 902, (C["B"], C["S"], H), 1.0))
+    out["gate"] = _bits(gate)
+    out["h"] = _bits(hid)
+    with torch.no_grad():
+        for k in C["topks"]:
+            ro = layer.router(hid, top_k_override=k, apply_affinity=False)
+            _assert_tie_free(ro.router_logits, k, "mixtral fixture")
+            y = layer(hid, top_k=k)
+            out[f"k{k}/idx"] = ro.expert_indices.numpy().astype(np.int32)
+            out[f"k{k}/w"] = _bits(ro.expert_weights)
+            out[f"k{k}/logits"] = ro.router_logits.numpy()
+            out[f"k{k}/out"] = _bits(y)
+    mgr.shutdown()
+    np.savez_compressed(os.path.join(HERE, "mixtral_moe_layer.npz"), **out)
+
+    # ---- GLM4MoELayer.forward (shared fp16 expert + routed experts)
+    C = GLM_CASE
+    H, I, g, E, k = C["H"], C["I"], C["g"], C["E"], C["k"]
+    gc = cfg.GLM4AirConfig()
+    gc.hidden_dim, gc.moe_intermediate_dim, gc.num_experts, gc.experts_per_token = H, I, E, k
+    adapter = types.SimpleNamespace(num_layers=1, num_experts=E,
+                                    expert_size_bytes=3 * H * I * 2)
+    mgr, _ = _cpu_cache_manager(cfg, adapter, E)
+    out = {"dims": np.array([H, I, g, E, k, C["seed"]])}
+    for e in range(E):
+        _, deq, digest = _packed_expert(pw, C["seed"], e, H, I, g)
+        mgr.register_expert(0, e, deq)
+        out[f"sha/{e}"] = np.array(digest)
+    layer = glm4.GLM4MoELayer(gc, 0, mgr)
+    layer.eval()
+    rw = torch.from_numpy(gen.normal(C["seed"] * 1000 + 901, (E, H), 0.02))
+    layer.router.weight.data = rw.clone()
+    sh = gen.expert_weights(C["seed"], 999, H, I)
+    layer.shared_expert.half()
+    for name in ("gate_proj", "up_proj", "down_proj"):
+        getattr(layer.shared_expert, name).weight.data = torch.from_numpy(sh[name]).clone()
+    hid = torch.from_numpy(gen.normal_f16(C["seed"] * 1000 + 902, (C["B"], C["S"], H), 1.0))
+    with torch.no_grad():
+        logits = torch.nn.functional.linear(hid.reshape(-1, H).float(), rw)
+        _assert_tie_free(torch.sigmoid(logits), k, "glm fixture")
+        ti, tw = layer.router(hid)
+        y = layer(hid)
+    out["router_w"] = rw.numpy()
+    out["h"] = _bits(hid)
+    out["idx"] = ti.numpy().astype(np.int32)
+    out["w"] = _bits(tw)
+    out["out"] = _bits(y)
+    out["last_selected"] = np.array(layer.get_last_selected_experts(), dtype=np.int32)
+    mgr.shutdown()
+    np.savez_compressed(os.path.join(HERE, "glm_moe_layer.npz"), **out)
+
+
+# ----------------------------------------------------------------------------- store format
+def store_format_fixture(pw, cfg, store) -> None:
+    """Legacy files written by pack_mixtral_experts and the single blob that
+    pack_to_single_blob makes of them, for seeded 2-layer x 2-expert weights.
+    pack_mixtral_experts reads a checkpoint through model.loader and sizes
+    itself by MixtralConfig(); both are swapped for the call: a loader that
+    yields the seeded experts, and a config with the fixture's dimensions."""
+    C = STORE_CASE
+    L, E, H, I, g = C["L"], C["E"], C["H"], C["I"], C["g"]
+
+    class _SeededLoader:
+        def __init__(self, model_path, config, device, dtype):
+            self.config = config
+
+        def iter_experts(self):
+            for li in range(L):
+                for e in range(E):
+                    yield li, e, {k: torch.from_numpy(v) for k, v in
+                                  gen.expert_weights(C["seed"], e, H, I, layer=li).items()}
+
+    base = cfg.MixtralConfig
+
+    class _SmallMixtral(base):
+        def __init__(self):
+            super().__init__()
+            self.num_layers, self.num_experts = L, E
+            self.hidden_dim, self.intermediate_dim = H, I
+
+    stub = types.ModuleType("hydranet.model.loader")
+    stub.MixtralWeightLoader = _SeededLoader
+    prev = sys.modules.get("hydranet.model.loader")
+    sys.modules["hydranet.model.loader"] = stub
+    cfg.MixtralConfig = _SmallMixtral
+    tmp = tempfile.mkdtemp()
+    try:
+        legacy = Path(tmp) / "legacy"
+        meta = pw.pack_mixtral_experts("unused", str(legacy), pw.QuantConfig(group_size=g))
+        blob_dir = Path(tmp) / "blob"
+        store.pack_to_single_blob(legacy, blob_dir, _SmallMixtral(), group_size=g)
+        dst = os.path.join(HERE, "store_format")
+        os.makedirs(dst, exist_ok=True)
+        digests = {}
+        for f in sorted(legacy.glob("expert_L*_E*.bin")):
+            digests[f.name] = hashlib.sha256(f.read_bytes()).hexdigest()
+        with open(os.path.join(dst, "legacy_files.json"), "w") as f:
+            json.dump({"case": C, "sha256": digests}, f, indent=1, sort_keys=True)
+        shutil.copy(legacy / "metadata.json", os.path.join(dst, "metadata.json"))
+        shutil.copy(blob_dir / "experts.bin", os.path.join(dst, "experts.bin"))
+        shutil.copy(blob_dir / "experts.idx", os.path.join(dst, "experts.idx"))
+        assert meta["format_version"] == "1.0"
+    finally:
+        cfg.MixtralConfig = base
+        if prev is None:
+            del sys.modules["hydranet.model.loader"]
+        else:
+            sys.modules["hydranet.model.loader"] = prev
+        shutil.rmtree(tmp, ignore_errors=True)
 
 
 if __name__ == "__main__":

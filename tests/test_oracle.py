@@ -244,3 +244,146 @@ def test_blob_layout_matches_reference_golden():
     # reference test_int4_pack.py:205-221 identities at 4096/14336/128
     L = BlobLayout.from_dims(4096, 14336, 128)
     assert L.total_size == 90832896
+
+
+# --------------------------------------------------------------------------- MoE layers
+def _gen():
+    import importlib
+    import sys
+    if GOLD not in sys.path:
+        sys.path.insert(0, GOLD)
+    return importlib.import_module("gen")
+
+
+def _seeded_experts(case_seed, E, H, I, g, digests=None, layer=0):
+    """Regenerate the fixture's experts (tests/golden/gen.py) and pack them with
+    the oracle packer; digests: the SHA-256 of the reference packer's bytes."""
+    import hashlib
+    gen = _gen()
+    experts = {}
+    for e in range(E):
+        w = gen.expert_weights(case_seed, e, H, I, layer)
+        parts = []
+        for name in ("gate_proj", "up_proj", "down_proj"):
+            p, s = oracle.quantize(w[name], g, mode=0)
+            parts += [p, s]
+        if digests is not None:
+            h = hashlib.sha256()
+            for a in parts:
+                h.update(np.ascontiguousarray(a).tobytes())
+            assert h.hexdigest() == str(digests[e]), f"expert {e}: packed bytes differ"
+        experts[e] = tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in parts)
+    return experts
+
+
+def _mixtral_fixture():
+    z = _npz("mixtral_moe_layer.npz")
+    H, I, g, E, seed = (int(v) for v in z["dims"])
+    experts = _seeded_experts(seed, E, H, I, g, [z[f"sha/{e}"] for e in range(E)])
+    h = torch.from_numpy(_f16(z["h"]).copy()).reshape(-1, H)
+    gate = torch.from_numpy(_f16(z["gate"]).copy())
+    return z, h, gate, experts, g
+
+
+def test_torch_ref_mixtral_layer_matches_reference_layer():
+    """torch_ref.mixtral_router / mixtral_moe / moe_dispatch against
+    MixtralMoELayer.forward run by the reference (model/mixtral.py:259-370)."""
+    z, h, gate, experts, g = _mixtral_fixture()
+    for k in (2, 1):
+        idx, w, logits = torch_ref.mixtral_router(h, gate, k)
+        assert torch.equal(logits, torch.from_numpy(z[f"k{k}/logits"]).reshape(logits.shape))
+        np.testing.assert_array_equal(idx.numpy(), z[f"k{k}/idx"].reshape(-1, k))
+        np.testing.assert_array_equal(w.view(torch.int16).numpy().view(np.uint16),
+                                      z[f"k{k}/w"].reshape(-1, k))
+        y = torch_ref.mixtral_moe(h, gate, experts, top_k=k, group_size=g)
+        np.testing.assert_array_equal(y.view(torch.int16).numpy().view(np.uint16),
+                                      z[f"k{k}/out"].reshape(y.shape), err_msg=f"top-{k}")
+
+
+def test_moe_dispatch_brute_force_per_token():
+    """out[t] = sum over the token's experts in ascending id of fp16(fp16(y_e[t]) * w),
+    accumulated in fp16 from zero, each y_e computed on the single row x_t."""
+    z, h, gate, experts, g = _mixtral_fixture()
+    for k in (2, 1):
+        idx, w, _ = torch_ref.mixtral_router(h, gate, k)
+        got = torch_ref.moe_dispatch(h, idx, w, experts, g)
+        T, H = h.shape
+        for t in range(T):
+            acc = torch.zeros(H, dtype=torch.float16)
+            for s in sorted(range(k), key=lambda s: int(idx[t, s])):
+                y = torch_ref.expert_mlp(h[t:t + 1], *experts[int(idx[t, s])], group_size=g)[0]
+                acc = acc + y * w[t, s]
+            np.testing.assert_allclose(got[t].float().numpy(), acc.float().numpy(),
+                                       atol=1e-3, rtol=1e-3)
+        # the fixture's rows route tokens to distinct experts, so the ascending
+        # order matters only through the fp16 sum; a wrong weight slot does not pass
+        bad = torch_ref.moe_dispatch(h, idx, w.flip(-1), experts, g)
+        if k > 1:
+            assert not torch.equal(bad, got)
+
+
+def _glm_fixture():
+    z = _npz("glm_moe_layer.npz")
+    H, I, g, E, k, seed = (int(v) for v in z["dims"])
+    experts = _seeded_experts(seed, E, H, I, g, [z[f"sha/{e}"] for e in range(E)])
+    sh = _gen().expert_weights(seed, 999, H, I)
+    shared = tuple(torch.from_numpy(sh[n]) for n in ("gate_proj", "up_proj", "down_proj"))
+    h = torch.from_numpy(_f16(z["h"]).copy()).reshape(-1, H)
+    rw = torch.from_numpy(z["router_w"])
+    return z, h, rw, experts, shared, k, g
+
+
+def test_torch_ref_glm_layer_matches_reference_layer():
+    """torch_ref.glm_router / glm_moe / dense_mlp against GLM4MoELayer.forward
+    (model/glm4.py:365-473) with its fp16 shared expert, run by the reference."""
+    z, h, rw, experts, shared, k, g = _glm_fixture()
+    idx, w, _ = torch_ref.glm_router(h, rw, k)
+    np.testing.assert_array_equal(idx.numpy(), z["idx"])
+    np.testing.assert_array_equal(w.view(torch.int16).numpy().view(np.uint16), z["w"])
+    y = torch_ref.glm_moe(h, rw, experts, shared, top_k=k, group_size=g)
+    np.testing.assert_array_equal(y.view(torch.int16).numpy().view(np.uint16),
+                                  z["out"].reshape(y.shape))
+    # the selected-experts record used for next-layer prefetch (model/glm4.py:469)
+    assert sorted(set(idx.reshape(-1).tolist())) == z["last_selected"].tolist()
+
+
+def test_glm_dense_mlp_brute_force():
+    """dense_mlp: SwiGLU of fp16 Linears, checked against float64 on the same weights."""
+    z, h, rw, experts, shared, k, g = _glm_fixture()
+    got = torch_ref.dense_mlp(h, *shared).double()
+    gw, uw, dw = (t.double() for t in shared)
+    x = h.double()
+    a = x @ gw.t()
+    ref = ((a * torch.sigmoid(a)) * (x @ uw.t())) @ dw.t()
+    np.testing.assert_allclose(got.numpy(), ref.numpy(), atol=2e-3, rtol=1e-2)
+
+
+def _dispatch_variant(h, idx, w, experts, g, order=sorted, fp32=False, init=None):
+    out = torch.zeros(h.shape, dtype=torch.float32 if fp32 else torch.float16) \
+        if init is None else init.clone()
+    for e in order(idx.unique().tolist()):
+        tok, kp = torch.where(idx == e)
+        y = torch_ref.expert_mlp(h[tok], *experts[e], group_size=g)
+        yw = y.float() * w[tok, kp].float().unsqueeze(-1) if fp32 else y * w[tok, kp].unsqueeze(-1)
+        out.index_add_(0, tok, yw)
+    return out.half()
+
+
+def test_planted_layer_mistakes_are_caught():
+    """Plausible slips in the dispatch restatement fail the layer fixtures:
+    fp32 accumulation (Mixtral top-2), descending expert order and the shared
+    expert used as the accumulator's start (GLM top-4)."""
+    z, h, gate, experts, g = _mixtral_fixture()
+    idx, w, _ = torch_ref.mixtral_router(h, gate, 2)
+    bad = _dispatch_variant(h, idx, w, experts, g, fp32=True)
+    assert not np.array_equal(bad.view(torch.int16).numpy().view(np.uint16),
+                              z["k2/out"].reshape(bad.shape))
+    z, h, rw, experts, shared, k, g = _glm_fixture()
+    idx, w, _ = torch_ref.glm_router(h, rw, k)
+    ref = z["out"].reshape(h.shape)
+    sh = torch_ref.dense_mlp(h, *shared)
+    desc = sh + _dispatch_variant(h, idx, w, experts, g,
+                                  order=lambda v: sorted(v, reverse=True))
+    first = _dispatch_variant(h, idx, w, experts, g, init=sh)
+    for bad in (desc, first):
+        assert not np.array_equal(bad.view(torch.int16).numpy().view(np.uint16), ref)

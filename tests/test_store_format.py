@@ -9,6 +9,7 @@ u32, six tensors back to back — and the blob sizes the reference's shape
 tables give at Mixtral and GLM-4.5-Air dims.
 """
 import json
+import os
 import struct
 
 import numpy as np
@@ -181,3 +182,81 @@ def test_checksum_known_answer():
     assert ps.compute_expert_checksum(w) == "0000000000005c40"
     assert ps.verify_expert_checksum(w, "0000000000005c40")
     assert not ps.verify_expert_checksum(dict(w, down_proj=w["down_proj"].t()), "00")
+
+
+# ---------------------------------------------------------------- files the reference wrote
+_REF_STORE = os.path.join(os.path.dirname(__file__), "golden", "store_format")
+
+
+def _ref_case():
+    with open(os.path.join(_REF_STORE, "legacy_files.json")) as f:
+        return json.load(f)
+
+
+def _seeded_packed_experts():
+    """PackedExperts of the fixture's seeded weights, packed by the oracle packer
+    (pinned against the reference packer by tests/test_oracle.py)."""
+    import sys
+    gold = os.path.join(os.path.dirname(__file__), "golden")
+    if gold not in sys.path:
+        sys.path.insert(0, gold)
+    import gen
+    import oracle
+    from hydranet_amd.preprocess.pack_store import PackedExpert, compute_expert_checksum
+    c = _ref_case()["case"]
+    out = []
+    for layer in range(c["L"]):
+        for e in range(c["E"]):
+            w = gen.expert_weights(c["seed"], e, c["H"], c["I"], layer=layer)
+            t = {}
+            for proj, pre in (("gate_proj", "gate"), ("up_proj", "up"), ("down_proj", "down")):
+                p, s = oracle.quantize(w[proj], c["g"], mode=0)
+                t[f"{pre}_packed"] = torch.from_numpy(np.ascontiguousarray(p))
+                t[f"{pre}_scales"] = torch.from_numpy(np.ascontiguousarray(s))
+            ck = compute_expert_checksum({k: torch.from_numpy(v) for k, v in w.items()})
+            out.append(PackedExpert.from_blob_tensors(layer, e, t, c["g"], ck))
+    return c, out
+
+
+def test_reader_reads_reference_single_blob_bit_for_bit():
+    """experts.bin / experts.idx written by the reference's pack_to_single_blob
+    (cache/packed_expert_store.py:627-739) read back through PackedExpertStore."""
+    from hydranet_amd.cache.packed_expert_store import PackedExpertStore
+    from hydranet_amd.preprocess.pack_store import iter_store_experts
+    c, experts = _seeded_packed_experts()
+    st = PackedExpertStore(os.path.join(_REF_STORE, "experts.idx"), device=torch.device("cpu"))
+    try:
+        assert st.format_version == "2.0"
+        assert (st.hidden_dim, st.intermediate_dim, st.group_size) == (c["H"], c["I"], c["g"])
+        got = {(l, e): t for l, e, t in iter_store_experts(st)}
+        assert len(got) == len(experts)
+        for pe in experts:
+            t = got[(pe.layer_idx, pe.expert_idx)]
+            for name, ref in pe.blob_tensors().items():
+                assert torch.equal(t[name].view(torch.uint8).reshape(-1),
+                                   ref.contiguous().view(torch.uint8).reshape(-1)), name
+    finally:
+        st.close()
+
+
+def test_writers_reproduce_reference_files_byte_for_byte(tmp_path):
+    """Legacy files (pack_mixtral_experts, preprocess/pack_weights.py:271-381),
+    their metadata.json and the converted experts.bin/.idx equal the reference's."""
+    from hydranet_amd.preprocess.pack_store import (load_packed_expert, pack_to_single_blob,
+                                                    write_legacy_store)
+    c, experts = _seeded_packed_experts()
+    legacy = tmp_path / "legacy"
+    meta = write_legacy_store(experts, legacy, c["L"], c["E"])
+    with open(os.path.join(_REF_STORE, "metadata.json")) as f:
+        assert meta == json.load(f)   # checksums included (pack_weights.py:36-50)
+    import hashlib
+    for name, digest in _ref_case()["sha256"].items():
+        assert hashlib.sha256((legacy / name).read_bytes()).hexdigest() == digest, name
+        # and the legacy reader parses what the reference wrote
+        pe = load_packed_expert(legacy / name)
+        assert (pe.hidden_dim, pe.intermediate_dim, pe.group_size) == (c["H"], c["I"], c["g"])
+    idx = pack_to_single_blob(legacy, tmp_path / "blob", c["L"], c["E"], c["H"], c["I"], c["g"])
+    ref_bin = open(os.path.join(_REF_STORE, "experts.bin"), "rb").read()
+    assert (tmp_path / "blob" / "experts.bin").read_bytes() == ref_bin
+    with open(os.path.join(_REF_STORE, "experts.idx")) as f:
+        assert idx == json.load(f)
