@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 
 import torch  # noqa: F401  (must precede the CDLL load, see module doc)
 
@@ -91,33 +92,46 @@ def call(name: str, *args) -> None:
         raise RuntimeError(f"{name} failed (rc={rc}): {msg}")
 
 
-_DECODE_PATH = 0
+_DECODE_PATH = threading.local()
 
 
 def set_decode_path(path: int) -> None:
-    """Decode kernel family, process-wide: 0 = the streaming kernels where they
-    apply, 1 = split-K kernels only (A/B measurement and tests)."""
-    global _DECODE_PATH
+    """Decode kernel family of the calling thread: 0 = the streaming kernels
+    where they apply, 1 = split-K kernels only (A/B measurement and tests)."""
     call("hn_set_decode_path", path)
-    _DECODE_PATH = path
+    _DECODE_PATH.value = path
 
 
 def decode_path() -> int:
-    return _DECODE_PATH
+    return getattr(_DECODE_PATH, "value", 0)
 
 
 _WORKSPACES: dict = {}
+# Every workspace ever handed out, per device.  A captured HIP graph keeps the
+# raw pointer of the workspace it was captured with, so a buffer superseded by
+# a larger one must stay allocated (never return to the caching allocator)
+# while such a graph may replay: the process keeps them all.
+_RETIRED: dict = {}
+
+
+def _device_key(dev: torch.device):
+    if dev.type != "cuda":
+        return (dev.type, 0)
+    return (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
 
 
 def workspace(nbytes: int, device) -> torch.Tensor:
     """Zero-filled scratch for the split-K counters and partials, cached per
     device and grown on demand.  The kernels leave the counters at zero, so
     the buffer is only filled once per allocation.  Calls that share a device
-    run in stream order; concurrent calls on different streams would race."""
+    run in stream order; concurrent calls on different streams would race.
+    Growing keeps the old buffer allocated (see _RETIRED)."""
     dev = torch.device(device)
-    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    key = _device_key(dev)
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _RETIRED.setdefault(key, []).append(buf)
         buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = buf
     return buf

@@ -1,6 +1,11 @@
-// C-ABI housekeeping: thread-local last-error string and library version.
+// C-ABI housekeeping: thread-local last-error string, library version, and
+// the per-device property cache (the only state the library keeps between
+// calls besides the thread-local decode-family switch of hn_gemv.hip).
+#include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <atomic>
 
 static thread_local char g_hn_err[512] = "";
 
@@ -14,3 +19,29 @@ extern "C" void hn_set_error(const char* fmt, ...) {
 extern "C" const char* hn_last_error_string(void) { return g_hn_err; }
 
 extern "C" int hn_abi_version(void) { return 1; }
+
+// CU count of the current device, queried once per device.  Concurrent first
+// calls may both query; they store the same value.
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
+}  // namespace
+
+extern "C" int hn_device_cus(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = g_cus[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      v <= 0)
+    v = 256;
+  g_cus[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+extern "C" int hn_current_device(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  return dev;
+}

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 typedef _Float16 h16;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -23,9 +25,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 extern "C" {
 #endif
 void hn_set_error(const char* fmt, ...);
+// CU count of the current device (queried once per device, hn_abi.cpp).
+int hn_device_cus(void);
+// Current device index, clamped to the per-device caches' range (0..63).
+int hn_current_device(void);
 #ifdef __cplusplus
 }
 #endif
+
+// Per-device flag that a kernel's dynamic-LDS limit was raised to the CU's
+// 160 KiB (hipFuncSetAttribute is per device): 0 unknown, 1 raised, 2 refused.
+struct HnLdsAttr {
+  std::atomic<int> state[64] = {};
+};
 
 #define HN_ARG_CHECK(cond, ...)              \
   do {                                       \

@@ -737,19 +737,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
   }
 }
 
-int num_cus() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        v > 0)
-      n = v;
-    else
-      n = 256;
-  }
-  return n;
-}
+int num_cus() { return hn_device_cus(); }
 
 void fill_consts(GemmArgs& A) {
   A.m_pair = 0x00F0000Fu;

@@ -610,8 +610,9 @@ extern "C" int hn_gemm_grouped_impl(int phase, const void* x, long ld_x, const v
 extern "C" long hn_gemm_workspace_bytes();
 
 // Decode kernel family: 0 = automatic (streaming kernels where they apply),
-// 1 = split-K kernels only.  Process-wide; for A/B measurement and tests.
-static int g_decode_path = 0;
+// 1 = split-K kernels only.  Per calling thread (a switch in one thread never
+// changes another thread's calls); for A/B measurement and tests.
+static thread_local int g_decode_path = 0;
 constexpr long kStreamMaxRows = 16;
 
 // Whether the streaming kernels take a grouped decode launch.  They stage at

@@ -880,31 +880,22 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   return p;
 }
 
-int num_cus() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        v > 0)
-      n = v;
-    else
-      n = 256;
-  }
-  return n;
-}
+int num_cus() { return hn_device_cus(); }
 
 template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS = 1,
           bool ROUTE = false>
 int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
   auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS, ROUTE>;
-  static int attr = -1;  // per instantiation
-  if (attr < 0) {
-    attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               kLdsPerCu - kStaticLds) == hipSuccess ? 1 : 0;
-    if (!attr) (void)hipGetLastError();  // plans then stay within 64 KiB
+  static HnLdsAttr attr;  // per instantiation and device
+  std::atomic<int>& sa = attr.state[hn_current_device()];
+  int st = sa.load(std::memory_order_relaxed);
+  if (st == 0) {
+    st = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             kLdsPerCu - kStaticLds) == hipSuccess ? 1 : 2;
+    if (st == 2) (void)hipGetLastError();  // plans then stay within 64 KiB
+    sa.store(st, std::memory_order_relaxed);
   }
-  if (!attr && p.lds > 64 * 1024 - kStaticLds) return HN_NOT_HANDLED;
+  if (st != 1 && p.lds > 64 * 1024 - kStaticLds) return HN_NOT_HANDLED;
   hipLaunchKernelGGL(kern, dim3(num_cus() * p.occ), dim3(p.kw * 64), (size_t)p.lds, s, A, g.table,
                      g.active, g.n_active, g.offsets);
   return 0;

@@ -309,15 +309,27 @@ class MixtralMoELayer(nn.Module):
 
     def __init__(self, hidden_dim: int = 4096, num_experts: int = 8, experts_per_token: int = 2,
                  layer_idx: int = 0, slots=None, cache_manager=None,
-                 enable_affinity_bonus: bool = False):
+                 enable_affinity_bonus: Optional[bool] = None):
         super().__init__()
         self.layer_idx = layer_idx
         self.num_experts = num_experts
+        # the cache-affinity bonus follows the cache manager's config, as the
+        # reference's router reads ExpertCacheConfig (on by default,
+        # config.py:273-275); without a cache manager there is nothing to favour
+        cc = getattr(cache_manager, "cache_config", None)
+        if enable_affinity_bonus is None:
+            enable_affinity_bonus = bool(cc.enable_affinity_bonus) if cc is not None else False
+        kw = {}
+        if cc is not None:
+            kw = dict(affinity_bonus=cc.affinity_bonus,
+                      entropy_threshold=cc.affinity_entropy_threshold)
         self.router = TopKRouter(hidden_dim, num_experts, experts_per_token,
-                                 enable_affinity_bonus=enable_affinity_bonus)
+                                 enable_affinity_bonus=enable_affinity_bonus, **kw)
         self.experts = _ResidentExperts(num_experts, layer_idx, slots, cache_manager)
         if cache_manager is not None:
             self.router.set_cache_checker(lambda e: cache_manager.is_cached(layer_idx, e))
+        # (idx [T, k] int32, w [T, k] fp16) of the last forward, on the device
+        self.last_routing = None
 
     def forward(self, hidden_states: torch.Tensor, top_k: int = 2) -> torch.Tensor:
         B, S, H = hidden_states.shape
@@ -340,11 +352,14 @@ class MixtralMoELayer(nn.Module):
             if not rt.training:
                 sel = r.idx.view(-1).long()  # no host sync: graph-capturable
                 rt.usage_counts.scatter_add_(0, sel, rt._one.expand_as(sel))
+            self.last_routing = (r.idx, r.w)
             return out.view(B, S, H)
         ro = rt(hidden_states, top_k_override=top_k)
         idx = ro.expert_indices.reshape(T, top_k)
+        w = ro.expert_weights.reshape(T, top_k)
         table = self.experts.table_for(idx)
-        out = moe_experts_forward(flat, idx, ro.expert_weights.reshape(T, top_k), table)
+        out = moe_experts_forward(flat, idx, w, table)
+        self.last_routing = (idx, w)
         return out.view(B, S, H)
 
 
@@ -387,10 +402,27 @@ class GLM4MoELayer(nn.Module):
                                         routed_scaling_factor=routed_scaling_factor)
         self.shared_expert = GLM4DenseMLP(hidden_dim, moe_intermediate_dim)
         self.experts = _ResidentExperts(num_experts, layer_idx, slots, cache_manager)
-        self._last_selected_experts: list = []
+        self._last_idx: Optional[torch.Tensor] = None
 
     def get_last_selected_experts(self) -> list:
-        return self._last_selected_experts
+        """Experts the last forward routed to, ascending (the reference records
+        unique(expert_indices) for the next layer's prefetch, model/glm4.py:469,
+        704-713).  The forward keeps the indices on the device; the list is made
+        here, so only a caller that asks pays the device-to-host copy."""
+        if self._last_idx is None:
+            return []
+        return torch.unique(self._last_idx).tolist()
+
+    def prefetch_predicted(self, predicted_experts) -> None:
+        """Start the loads of predicted experts that are not resident
+        (model/glm4.py:351-363): with a cache manager that holds only part of
+        the layer, each miss is scheduled on the store's copy stream."""
+        cm = self.experts.cache_manager
+        if cm is None or cm.is_resident(self.layer_idx):
+            return
+        for e in predicted_experts:
+            if not cm.is_cached(self.layer_idx, int(e)):
+                cm.prefetch_int4_slot(self.layer_idx, int(e))
 
     def forward(self, hidden_states: torch.Tensor, skip_routed: bool = False) -> torch.Tensor:
         B, S, H = hidden_states.shape
@@ -415,9 +447,11 @@ class GLM4MoELayer(nn.Module):
             cur.wait_stream(side)
             shared.record_stream(cur)
             out = moe_dispatch(r, self.experts.table_for(r.idx), shared=shared.reshape(T, H))
+            self._last_idx = r.idx
             return out.view(B, S, H)
         shared = self.shared_expert(hidden_states)
         idx, w = rt(hidden_states)
         table = self.experts.table_for(idx)
         out = moe_experts_forward(flat, idx, w, table, shared=shared.reshape(T, H))
+        self._last_idx = idx
         return out.view(B, S, H)

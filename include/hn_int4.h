@@ -255,7 +255,8 @@ int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k, const voi
                    void* stream);
 
 /* Decode kernel family for hn_int4_linear, hn_int4_gate_up_silu,
- * hn_expert_mlp_int4 and hn_grouped_expert_mlp_int4 (process-wide):
+ * hn_expert_mlp_int4 and hn_grouped_expert_mlp_int4, for the calling thread
+ * only (each thread starts at 0; a switch never affects another thread):
  *   0  automatic: the persistent streaming kernels for group 128 and at most
  *      16 rows per weight matrix, the split-K kernels otherwise (default);
  *   1  split-K kernels only.

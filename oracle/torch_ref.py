@@ -16,8 +16,23 @@ Same op sequence as the reference, on CPU tensors:
 * ``glm_moe``        — GLM4MoELayer.forward (model/glm4.py:378-473) with
                        GLM4SigmoidRouter.forward (:279-309); the optional
                        selection bias is this build's extension.
+
+Pins (tests/test_oracle.py), each from outputs the reference's own code wrote
+(tests/golden/make_golden.py):
+  expert_mlp, dequant           expert_mlp.npz (ExpertMLPTriton.forward), bit for bit
+  mixtral_router, mixtral_moe,  mixtral_moe_layer.npz (MixtralMoELayer.forward at
+  moe_dispatch                  top-2 and top-1), bit for bit; a per-token brute force
+  glm_router, glm_moe,          glm_moe_layer.npz (GLM4MoELayer.forward with its
+  dense_mlp                     shared expert), bit for bit; dense_mlp also against
+                                float64
+  affinity_bonus,               affinity_router.npz (TopKRouter.forward with the
+  mixtral_router(cached=...)    cache-affinity bonus), bit for bit
+  glm_router with a bias        parity unpinned: the reference has no selection bias;
+                                the C oracle's brute-force test covers the selection.
 """
 from __future__ import annotations
+
+import math
 
 import torch
 import torch.nn.functional as F
@@ -46,13 +61,31 @@ def expert_mlp(x, gate_packed, gate_scales, up_packed, up_scales, down_packed, d
     return (gate_out * up_out) @ down_w.t()
 
 
-def mixtral_router(h: torch.Tensor, gate_w: torch.Tensor, top_k: int):
-    """logits = fp16 Linear(h).float(); topk; softmax; renorm; fp16."""
+def mixtral_router(h: torch.Tensor, gate_w: torch.Tensor, top_k: int, cached=None,
+                   bonus: float = 0.1, threshold: float = 0.5):
+    """logits = fp16 Linear(h).float(); [affinity bonus toward `cached`]; topk;
+    softmax; renorm; fp16 (model/router.py:96-120)."""
     logits = F.linear(h, gate_w).float()
+    if cached is not None:
+        logits = affinity_bonus(logits, cached, bonus, threshold)
     topk_logits, idx = torch.topk(logits, top_k, dim=-1)
     w = F.softmax(topk_logits, dim=-1)
     w = w / w.sum(dim=-1, keepdim=True)
     return idx, w.to(h.dtype), logits
+
+
+def affinity_bonus(logits: torch.Tensor, cached, bonus: float = 0.1,
+                   threshold: float = 0.5) -> torch.Tensor:
+    """TopKRouter._apply_affinity_bonus (model/router.py:132-175): + bonus on the
+    cached experts' logits of every token whose softmax entropy / ln E exceeds
+    the threshold.  cached: iterable of expert ids."""
+    E = logits.shape[-1]
+    p = F.softmax(logits, dim=-1)
+    ent = -(p * torch.log(p + 1e-10)).sum(dim=-1) / math.log(E)
+    mask = torch.zeros(E, dtype=logits.dtype)
+    for e in cached:
+        mask[int(e)] = bonus
+    return logits + (ent > threshold).float().unsqueeze(-1) * mask
 
 
 def glm_router(h: torch.Tensor, w: torch.Tensor, top_k: int, bias=None, eps: float = 1e-9,

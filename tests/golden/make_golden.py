@@ -178,6 +178,30 @@ def main(root: str) -> None:
     out["h"] = _bits(h)
     np.savez_compressed(os.path.join(HERE, "topk_router.npz"), **out)
 
+    # ---- TopKRouter.forward with the cache-affinity bonus (model/router.py:132-175):
+    #      experts 1, 4, 6 cached; hidden rows scaled so some tokens are below
+    #      and some above the entropy threshold
+    out = {}
+    r = router.TopKRouter(mc, cfg.ExpertCacheConfig(enable_affinity_bonus=True), 0)
+    ga = _f16(33, (8, 256), 0.02)
+    r.gate.weight.data = ga.clone()
+    r.eval()
+    cached = {1, 4, 6}
+    r.set_cache_checker(lambda e: e in cached)
+    h = _f16(34, (1, 24, 256), 1.0)
+    h[0, ::3] = h[0, ::3] * 40.0  # confident rows: low entropy, no bonus
+    with torch.no_grad():
+        for k in (1, 2):
+            ro = r(h, top_k_override=k)
+            out[f"k{k}/idx"] = ro.expert_indices.numpy().astype(np.int32)
+            out[f"k{k}/w"] = _bits(ro.expert_weights)
+            out[f"k{k}/logits"] = ro.router_logits.numpy()
+    out["gate"] = _bits(ga)
+    out["h"] = _bits(h)
+    out["cached"] = np.array(sorted(cached), dtype=np.int32)
+    out["bonus"] = np.array([r.affinity_bonus, r.entropy_threshold], dtype=np.float64)
+    np.savez_compressed(os.path.join(HERE, "affinity_router.npz"), **out)
+
     # ---- GLM4SigmoidRouter.forward (fp32 weight, top-8 of 128)
     out = {}
     gc = cfg.GLM4AirConfig()

@@ -65,3 +65,15 @@ def test_argument_errors_raise_without_gpu():
         _lib.call("hn_moe_route", None, 4096, None, 4096, 0, None, None, 2048, 8, 4096, 2, 0,
                   ctypes.c_float(0), ctypes.c_float(1), None, None, None, None, None, None, None,
                   None, None, 4096, None)
+
+
+def test_growing_a_workspace_keeps_the_old_buffer_allocated():
+    # a captured graph holds the raw pointer of the workspace it was captured
+    # with: growing must not hand the old buffer back to the allocator
+    from hydranet_amd import _lib
+    a = _lib.workspace(1000, "cpu")
+    pa = a.data_ptr()
+    b = _lib.workspace(1 << 20, "cpu")
+    assert b.data_ptr() != pa and b.numel() >= 1 << 20
+    assert any(t.data_ptr() == pa for t in _lib._RETIRED[("cpu", 0)])
+    assert _lib.workspace(10, "cpu") is b  # smaller requests reuse the current one

@@ -53,7 +53,10 @@ def _fixed_slots(experts, layer):
 def _layers(cm, experts, layer):
     from hydranet_amd.model.moe import MixtralMoELayer
     ref = MixtralMoELayer(H, E, 2, layer_idx=layer, slots=_fixed_slots(experts, layer)).to(DEV)
-    got = MixtralMoELayer(H, E, 2, layer_idx=layer, cache_manager=cm).to(DEV)
+    # affinity off, as the reference's oracle runs (it favours cached experts
+    # and so changes the routing of a partial cache by design)
+    got = MixtralMoELayer(H, E, 2, layer_idx=layer, cache_manager=cm,
+                          enable_affinity_bonus=False).to(DEV)
     g = torch.Generator().manual_seed(5 + layer)
     w = (torch.randn(E, H, generator=g) * 0.05).half()
     for m in (ref, got):
@@ -158,3 +161,50 @@ def test_pack_experts_gpu_quantizer_matches_oracle(tmp_path):
             p, s = oracle.quantize(w[proj].numpy(), G, mode=0)
             t[f"{pre}_packed"], t[f"{pre}_scales"] = torch.from_numpy(p), torch.from_numpy(s.copy())
         assert raw[e * size:(e + 1) * size] == ps.expert_blob(t).tobytes(), e
+
+
+def test_affinity_bonus_with_partial_cache(store):
+    """The reference's default cache-affinity bonus (config.py:273-275,
+    model/router.py:132-175) with a cache holding experts 1, 4 and 6 of the
+    layer: the layer's routing equals the oracle's affinity_bonus + top-k on
+    the same raw logits, and its output the oracle dispatch of that routing."""
+    from oracle import torch_ref
+    from hydranet_amd.model.moe import MixtralMoELayer
+    from hydranet_amd.model.router import router_logits
+    st, experts = store
+    cm = _manager(st, 3)
+    try:
+        layer = MixtralMoELayer(H, E, 2, layer_idx=0, cache_manager=cm).to(DEV)
+        assert layer.router.enable_affinity_bonus  # taken from the cache config
+        g = torch.Generator().manual_seed(31)
+        layer.router.gate.weight.data.copy_((torch.randn(E, H, generator=g) * 0.02).half()
+                                            .to(DEV))
+        layer.eval()
+        for e in (1, 4, 6):
+            cm.get_int4_slot(0, e)
+        torch.cuda.synchronize()
+        gated = 0
+        for step in range(3):
+            x = torch.randn(1, 16, H, generator=g).half().to(DEV)
+            if step == 2:
+                x[0, ::2] *= 30.0  # confident tokens: below the entropy threshold
+            cached = [e for e in range(E) if cm.is_cached(0, e)]
+            raw = router_logits(x.view(16, H), layer.router.gate.weight.to(torch.float16))
+            out = layer(x)
+            idx, w = layer.last_routing
+            lg = torch_ref.affinity_bonus(raw.cpu(), cached)
+            gated += int((lg != raw.cpu()).any(-1).sum())
+            idx_o, w_o = oracle.router_topk(lg.numpy(), 2, mode=0)
+            np.testing.assert_array_equal(idx.cpu().numpy(), idx_o)
+            np.testing.assert_allclose(w.cpu().float().numpy(), w_o.astype(np.float32),
+                                       atol=1e-3)
+            cpu = {e: tuple(experts[(0, e)][n] for n in ("gate_packed", "gate_scales",
+                                                         "up_packed", "up_scales",
+                                                         "down_packed", "down_scales"))
+                   for e in range(E)}
+            ref = torch_ref.moe_dispatch(x.view(16, H).cpu(), idx.long().cpu(), w.cpu(), cpu)
+            err = (out.view(16, H).float().cpu() - ref.float()).abs()
+            assert bool((err <= 1e-2 + 2e-3 * ref.float().abs()).all()), err.max()
+        assert gated > 0
+    finally:
+        cm.shutdown()

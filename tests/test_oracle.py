@@ -387,3 +387,32 @@ def test_planted_layer_mistakes_are_caught():
     first = _dispatch_variant(h, idx, w, experts, g, init=sh)
     for bad in (desc, first):
         assert not np.array_equal(bad.view(torch.int16).numpy().view(np.uint16), ref)
+
+
+def test_affinity_bonus_matches_reference_golden():
+    """TopKRouter.forward with the cache-affinity bonus on (model/router.py:96-175),
+    experts 1, 4, 6 cached: logits, indices and weights bit for bit; the
+    build's TopKRouter._affinity (host torch ops) equals it too."""
+    from hydranet_amd.model.router import TopKRouter
+    z = _npz("affinity_router.npz")
+    h = torch.from_numpy(_f16(z["h"]).copy()).reshape(-1, 256)
+    gate = torch.from_numpy(_f16(z["gate"]).copy())
+    cached = z["cached"].tolist()
+    bonus, thr = (float(v) for v in z["bonus"])
+    raw = torch.nn.functional.linear(h, gate).float()
+    gated = 0
+    for k in (1, 2):
+        idx, w, logits = torch_ref.mixtral_router(h, gate, k, cached=cached, bonus=bonus,
+                                                  threshold=thr)
+        ref_lg = torch.from_numpy(z[f"k{k}/logits"]).reshape(logits.shape)
+        assert torch.equal(logits, ref_lg)
+        np.testing.assert_array_equal(idx.numpy(), z[f"k{k}/idx"].reshape(-1, k))
+        np.testing.assert_array_equal(w.view(torch.int16).numpy().view(np.uint16),
+                                      z[f"k{k}/w"].reshape(-1, k))
+        gated = int((logits != raw).any(-1).sum())
+        r = TopKRouter(256, 8, 2, affinity_bonus=bonus, entropy_threshold=thr,
+                       enable_affinity_bonus=True)
+        r.set_cache_checker(lambda e: e in cached)
+        assert torch.equal(r._affinity(raw), ref_lg)
+    # the fixture has tokens on both sides of the entropy threshold
+    assert 0 < gated < h.shape[0]
