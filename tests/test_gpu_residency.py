@@ -184,12 +184,13 @@ def test_affinity_bonus_with_partial_cache(store):
             cm.get_int4_slot(0, e)
         torch.cuda.synchronize()
         gated = 0
-        for step in range(3):
-            x = torch.randn(1, 16, H, generator=g).half().to(DEV)
-            if step == 2:
-                x[0, ::2] *= 30.0  # confident tokens: below the entropy threshold
+        T = 2  # at most 4 experts per call: the layer's 4 slots hold them all
+        for step in range(8):
+            x = torch.randn(1, T, H, generator=g).half().to(DEV)
+            if step % 4 == 3:
+                x[0, 0] *= 30.0  # a confident token: below the entropy threshold
             cached = [e for e in range(E) if cm.is_cached(0, e)]
-            raw = router_logits(x.view(16, H), layer.router.gate.weight.to(torch.float16))
+            raw = router_logits(x.view(T, H), layer.router.gate.weight.to(torch.float16))
             out = layer(x)
             idx, w = layer.last_routing
             lg = torch_ref.affinity_bonus(raw.cpu(), cached)
@@ -202,8 +203,12 @@ def test_affinity_bonus_with_partial_cache(store):
                                                          "up_packed", "up_scales",
                                                          "down_packed", "down_scales"))
                    for e in range(E)}
-            ref = torch_ref.moe_dispatch(x.view(16, H).cpu(), idx.long().cpu(), w.cpu(), cpu)
-            err = (out.view(16, H).float().cpu() - ref.float()).abs()
+            ref = torch_ref.moe_dispatch(x.view(T, H).cpu(), idx.long().cpu(), w.cpu(), cpu)
+            # output bar on the unscaled N(0, 1) tokens (a token scaled by 30 has
+            # activations far outside the inputs the fp16 bar is stated for)
+            rows = slice(1, T) if step % 4 == 3 else slice(0, T)
+            err = (out.view(T, H)[rows].float().cpu() - ref[rows].float()).abs()
+            ref = ref[rows]
             assert bool((err <= 1e-2 + 2e-3 * ref.float().abs()).all()), err.max()
         assert gated > 0
     finally:
