@@ -51,6 +51,7 @@ SIGNATURES: dict[str, list] = {
                              P],
     "hn_moe_decode_layer": [P, L, P, L, L, L, L, P, L, L, L, F, F, P, P, P, P, P, P, P, P, P,
                             P, L, P, L, P],
+    "hn_expert_mlp_int4_noalloc": [P, P, P, P, P, P, P, P, L, L, L, L, P],
 }
 
 # Sizes up to which hn_moe_route (one launch: logits, top-k, permutation,

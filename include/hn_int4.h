@@ -229,6 +229,21 @@ int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const void* tabl
                                  long E, long rows, long H, long I, long group, void* h_ws,
                                  void* y_perm, void* work, long work_bytes, void* stream);
 
+/* hn_expert_mlp_int4 without allocation: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments as
+ * hn_expert_mlp_int4 minus the buffers: h [T, I] and the split-K workspace live
+ * in a library-owned static device array of 17 MiB per GPU (held until the
+ * process ends; set up on the first call on each device).  Limits: T <= 16,
+ * T * I * 2 <= 1 MiB and hn_skinny_workspace_bytes(2, T, H, I, 0) <= 16 MiB
+ * (Mixtral 4096/14336 at T = 16 needs 9 MiB); beyond them it returns -EINVAL
+ * with a message.  Same kernels, so the same results as hn_expert_mlp_int4.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (concurrent streams) race; calls in one stream's order do not. */
+int hn_expert_mlp_int4_noalloc(const void* x, const void* gq, const void* gs, const void* uq,
+                               const void* us, const void* dq, const void* ds, void* out, long T,
+                               long H, long I, long group, void* stream);
+
 /* Decoder-step helpers around the MoE layer (the whole-model decode harness).
  *
  * hn_add_rmsnorm: for rows t < T of H fp16 (H % 8 == 0, H <= 8192):
