@@ -160,7 +160,8 @@ def _expert(seed, H, I, g=128):
     return out  # gp, gs, up, us, dp, ds (CPU)
 
 
-@pytest.mark.parametrize("T,H,I", [(1, 4096, 14336), (4, 4096, 1408), (16, 512, 1024),
+@pytest.mark.parametrize("T,H,I", [(1, 4096, 14336), (2, 4096, 14336), (4, 4096, 14336),
+                                   (4, 4096, 1408), (16, 512, 1024),
                                    (3, 256, 384), (5, 4096, 14336)])
 def test_expert_mlp_vs_torch_ref(T, H, I, decode_path):
     from hydranet_amd.kernels import expert_mlp_int4_fused
@@ -201,3 +202,4 @@ def test_int4linear_module():
         lin.bias.data.float().numpy()
     got = q(x.to(DEV))
     _close(got, torch.from_numpy(ref))
+
