@@ -1,19 +1,22 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X INT4 expert-MLP hot path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c3|c4|c5|c2phase] [--tokens T]
+    python bench.py [--steps K] [--warmup W] [--workload c1|c2|c3|c4|c5|...] [--tokens T]
 
 Prints ONE JSON line.  A "step" is one pass of the hot path over one batch of
 synthetic input already resident in HBM:
 
   c2  (default, the headline) one Mixtral MoE layer at decode, T = 1, 4, 16
-      (value: T = 16): route + grouped gate/up + down + unpermute; then the
-      c5 decoder run (decoder_tokens_per_s; --skip-c5 leaves it out)
+      (value: T = 16): route + grouped gate/up + down + unpermute.  The default
+      line also carries C1 ("c1": one expert at T = 1 against the 0.70 target),
+      C3 ("c3"), C4 ("c4", TFLOP/s with its own MFMA roofline) and the C5
+      decoder (decoder_tokens_per_s); --skip-c34 / --skip-c5 leave those out
   c1  one Mixtral expert SwiGLU (H 4096, I 14336, INT4 g128), T tokens (default 1)
   c3  one GLM-4.5-Air MoE layer at decode (T = 32, 128 experts, shared expert)
   c4  one Mixtral MoE layer at prefill (2048 tokens, Zipf-skewed routing)
   c5  the whole Mixtral-8x7B-shaped decoder: 64 x 512-token prompts, greedy
       decode (tokens/s over the decode forwards)
+  c1phase / c2phase / c4phase: only the kernels of a counter run (rocprofv3 --pmc)
 
 Weights are seeded N(0, 0.02) fp16 packed to INT4 by the GPU packer.  Steps
 rotate over enough distinct experts (>= 0.7 GB) that weights stream from HBM,
@@ -24,7 +27,8 @@ its average duration, timed with HIP events on the stream the kernel runs on
 (c2: around each launch of the routing + gate/up kernel inside eager layer
 sequences).
 cpu_baseline: the torch-CPU restatement of the reference's
-dequantise-then-matmul path (oracle/torch_ref.py) on this host.
+dequantise-then-matmul path (oracle/torch_ref.py) on this host: the headline
+C2 layer at T = 16 (value) and T = 1, 4 (per_T), and one C1 expert ("c1").
 """
 from __future__ import annotations
 
@@ -244,6 +248,8 @@ def bench_c2(args, T: int, n_layers: int = 4, phases: bool = False):
            / n_layers, "graph": gr is not None}
     if phases and args.decode_path == 0:
         res["phases"] = time_decode_phases(layers, x.view(T, H), T, H, I, g, E)
+    # for the CPU baseline and its parity check: layer 0's output on this input
+    res["_ctx"] = (layers[0], x.view(T, H), layers[0](x, top_k=2).view(T, H))
     return res
 
 
@@ -531,6 +537,104 @@ def cpu_baseline_c1(ctx, budget_s: float):
                                                      "ok": ok}
 
 
+def cpu_baseline_c2(ctxs, budget_s: float):
+    """The headline workload (C2: one Mixtral MoE layer at decode) through the
+    torch-CPU restatement of the reference's path (oracle/torch_ref.py:
+    TopKRouter.forward + MixtralMoELayer.forward's fp16 dequantise-then-F.linear
+    per expert + fp16 index_add_, model/router.py:96-120, model/mixtral.py:283-368),
+    on this host, for T = 1, 4, 16.  Per call every routed expert is dequantised
+    again (the reference clears its fp16 cache per layer, model/mixtral.py:583-584).
+    TEST INFRASTRUCTURE (oracle) used only as the reported baseline; its output is
+    also checked against the GPU layer's."""
+    from oracle import torch_ref
+    from hydranet_amd.preprocess.synthetic import slot_to_cpu
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    layer0 = ctxs["T16"][0]
+    experts = {e: slot_to_cpu(s) for e, s in enumerate(layer0.experts.table.slots)}
+    gate = layer0.router.gate.weight.detach().to(torch.float16).cpu()
+    blob = layer0.experts.table.slots[0].layout.total_size
+    E, H = gate.shape
+    per_t, worst = {}, 0.0
+    share = budget_s / len(ctxs)
+    for name, (layer, x, y_gpu) in ctxs.items():
+        xc = x.cpu()
+        T = xc.shape[0]
+        times, y = [], None
+        t_start = time.perf_counter()
+        for i in range(40):
+            t0 = time.perf_counter()
+            idx, w, _ = torch_ref.mixtral_router(xc, gate, 2)
+            y = torch_ref.moe_dispatch(xc, idx, w, experts, 128)
+            times.append(time.perf_counter() - t0)
+            if i >= 4 and time.perf_counter() - t_start > share:
+                break
+        runs = times[3:]
+        med = statistics.median(runs)
+        uniq = int(torch.unique(idx).numel())
+        nbytes = uniq * blob + E * H * 2 + 2 * T * H * 2
+        err = (y_gpu.cpu().float() - y.float()).abs()
+        ok = bool((err <= 1e-2 + 2e-3 * y.float().abs()).all())
+        worst = max(worst, float(err.max()))
+        per_t[name] = {"ms_per_step": round(med * 1e3, 2),
+                       "GB_s": round(nbytes / med / 1e9, 3), "unique_experts": uniq,
+                       "timed_calls": len(runs), "parity_ok": ok}
+    head = per_t["T16"]
+    return {"value": head["GB_s"], "unit": "GB/s", "ms_per_step": head["ms_per_step"],
+            "cores": torch.get_num_threads(), "kind": "port", "cpu": _cpu_model(),
+            "sample": "C2 (one Mixtral MoE layer at decode, layer 0 of the GPU run, same input) "
+                      "at T = 16 (value) and T = 1 / 4: per T at least 2 warm-up + 2 timed "
+                      "calls within " + f"{share:.0f} s, median; every routed expert dequantised "
+                      "per call", "per_T": per_t, "max_abs_err_vs_gpu": worst}
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def c1phase(args):
+    """Counter run: 20 launches each of the C1 gate/up+SiLU and down stream
+    kernels (one Mixtral expert, T = 1, rotating over 8 experts), then 20 copies
+    of 512 MiB (the copy calibrates FETCH_SIZE / WRITE_SIZE in bytes)."""
+    from hydranet_amd import _lib
+    from hydranet_amd.preprocess.synthetic import make_expert_slot, normal_f16, expert_seed
+    H, I, g, T = 4096, 14336, 128, 1
+    slots = [make_expert_slot(expert_seed(0, e), H, I, g, slot_idx=e) for e in range(8)]
+    x = normal_f16((T, H), 1234, std=1.0)
+    h = torch.empty(T, I, dtype=torch.float16, device="cuda")
+    y = torch.empty(T, H, dtype=torch.float16, device="cuda")
+    work = _lib.skinny_workspace(2, T, H, I, 0, "cuda")
+    for r in range(20):
+        sl = slots[r % 8]
+        _lib.call("hn_int4_gate_up_silu", _lib.ptr(x), H, _lib.ptr(sl.gate_packed),
+                  _lib.ptr(sl.gate_scales), _lib.ptr(sl.up_packed), _lib.ptr(sl.up_scales),
+                  H // 2, H // g, _lib.ptr(h), I, T, I, H, g, _lib.ptr(work), work.numel(),
+                  _lib.stream())
+    for r in range(20):
+        sl = slots[r % 8]
+        _lib.call("hn_int4_linear", _lib.ptr(h), I, _lib.ptr(sl.down_packed), I // 2,
+                  _lib.ptr(sl.down_scales), I // g, _lib.ptr(y), H, T, H, I, g, _lib.ptr(work),
+                  work.numel(), _lib.stream())
+    src = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    lay = slots[0].layout
+    print(json.dumps({"workload": "c1phase",
+                      "gate_up_bytes_per_launch": 2 * (lay.gate_packed_size + lay.gate_scales_size)
+                      + T * H * 2 + T * I * 2,
+                      "down_bytes_per_launch": lay.down_packed_size + lay.down_scales_size
+                      + T * I * 2 + T * H * 2, "copy_bytes": src.numel() * 2}), flush=True)
+
+
 def c2phase(args):
     """Counter run: 20 launches of the C2 T=16 routing + gate/up stream kernel (the
     roofline kernel), then 20 copies of 512 MiB (the copy calibrates FETCH_SIZE /
@@ -683,7 +787,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c5", "c2phase", "c4phase"],
+                    choices=["c1", "c2", "c3", "c4", "c5", "c1phase", "c2phase", "c4phase"],
                     help="c2phase: only the C2 T=16 routing + gate/up kernel and a 512 MiB copy "
                          "(the two kernels whose rocprofv3 counters give roofline.traffic); "
                          "c4phase: only the C4 grouped GEMM launches (MFMA counters)")
@@ -692,7 +796,10 @@ def main():
     ap.add_argument("--warmup-decode", type=int, default=3, help="c5: untimed decode forwards")
     ap.add_argument("--skip-c5", action="store_true",
                     help="c2: leave out the whole-decoder tokens/s run (workload c5)")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--skip-c34", action="store_true",
+                    help="c2: leave out the GLM layer (c3) and prefill (c4) lines")
+    ap.add_argument("--cpu-budget", type=float, default=24.0,
+                    help="seconds of CPU-baseline work (C2 at T = 1, 4, 16; C1 gets a quarter)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-path", type=int, default=0, choices=[0, 1],
                     help="0: streaming kernels where they apply (default); 1: split-K only")
@@ -710,6 +817,9 @@ def main():
     from hydranet_amd import _lib
     _lib.set_decode_path(args.decode_path)
     _log("workload", args.workload, "steps", args.steps, "warmup", args.warmup)
+    if args.workload == "c1phase":
+        c1phase(args)
+        return
     if args.workload == "c2phase":
         c2phase(args)
         return
@@ -742,16 +852,21 @@ def main():
         return
     res, ctx = bench_c1(args)
     _log("c1 done", res["value"], res["unit"])
-    c1 = {"GB_s": res["value"], "frac": res["roofline"]["expert_frac"],
-          "ms_per_step": res["ms_per_step"], "tokens_per_s": res["tokens_per_s"]}
+    c1 = {"GB_s": res["value"], "frac": res["roofline"]["expert_frac"], "target_frac": 0.70,
+          "us_per_expert": round(res["ms_per_step"] * 1e3, 2),
+          "tokens_per_s": res["tokens_per_s"],
+          "kernels": {"gate_up_silu_us": res["roofline"]["avg_us"],
+                      "down_us": res["roofline"]["down_avg_us"]}}
     cpu = None
+    cpu_c1 = None
     if not args.no_cpu:
-        cpu, parity = cpu_baseline_c1(ctx, args.cpu_budget)
+        cpu_c1, parity = cpu_baseline_c1(ctx, args.cpu_budget / 4)
         res["parity"] = parity
     if args.workload == "c2":
-        sweep = {}
+        sweep, ctxs = {}, {}
         for T in (1, 4, 16):
             sweep[f"T{T}"] = bench_c2(args, T, phases=(T == 16))
+            ctxs[f"T{T}"] = sweep[f"T{T}"].pop("_ctx")
             _log("c2", T, sweep[f"T{T}"])
         head = sweep["T16"]
         ph = head.pop("phases", None)
@@ -765,10 +880,20 @@ def main():
                 "kernel": "stream_kernel<grouped, gate+up+SiLU, routing in the prologue> (C2, T=16)",
                 "achieved": gu["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "traffic_source": None,
                 "bytes_per_launch": gu["bytes_per_launch"], "avg_us": gu["avg_us"],
                 "down": ph["down_4slices"], "active_experts": ph["active_experts"]}
             if ph["active_experts"] == 8:
                 res["roofline"]["traffic"] = ROUTE_GATE_UP_C2_T16_TRAFFIC
+                res["roofline"]["traffic_source"] = (
+                    "constant from profiles/route_gate_up_c2_t16_traffic.md (rocprofv3 "
+                    "FETCH_SIZE + WRITE_SIZE of bench.py --workload c2phase, scaled by a 512 MiB "
+                    "copy); not measured in this run")
+        if not args.no_cpu:
+            cpu = cpu_baseline_c2(ctxs, args.cpu_budget)
+            cpu["c1"] = cpu_c1
+            _log("cpu baseline", cpu)
+        del ctxs
         res["metric"] = METRIC
         res["value"] = head["GB_s"]
         res["ms_per_step"] = head["ms_per_step"]
@@ -779,6 +904,16 @@ def main():
                          "tokens": 16, "experts": 8, "top_k": 2, "layers_rotated": 4,
                          "sweep": sweep, "c1_single_expert_T1": c1,
                          "graph": head["graph"]}
+        res["c1"] = c1
+        if not args.skip_c34:
+            torch.cuda.empty_cache()
+            c3 = bench_c3(args)
+            _log("c3", c3)
+            res["c3"] = c3
+            torch.cuda.empty_cache()
+            c4 = bench_c4(args)
+            _log("c4", c4)
+            res["c4"] = c4
         if not args.skip_c5:
             # the metric's second half: whole-decoder decode tokens/s (workload c5)
             torch.cuda.empty_cache()
@@ -786,6 +921,8 @@ def main():
             _log("c5", c5)
             res["decoder_tokens_per_s"] = c5["tokens_per_s"]
             res["config"]["c5_decoder"] = c5
+    else:
+        cpu = cpu_c1
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
