@@ -132,15 +132,30 @@ class Attention(nn.Module):
         self.v_proj = nn.Linear(H, self.nkv * self.hd, bias=False)
         self.o_proj = nn.Linear(self.nh * self.hd, H, bias=False)
 
-    def _qkv_weight(self) -> torch.Tensor:
-        """q, k and v projection weights stacked into one matrix (one GEMM),
-        rebuilt when a weight is replaced or modified."""
-        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
-        key = tuple((w.data_ptr(), w._version) for w in ws)
-        if getattr(self, "_wqkv_key", None) != key:
-            self._wqkv = torch.cat([w.detach() for w in ws], 0)
-            self._wqkv_key = key
-        return self._wqkv
+    def _qkv(self, x2: torch.Tensor) -> torch.Tensor:
+        """q, k and v projections of x2 [rows, H] as one product: the fp16
+        weights stacked into one matrix (one GEMM), or, for Int4Linear
+        projections (convert_dense_to_int4), their packed weights and scales
+        stacked into one hn_int4_linear launch.  The stack is rebuilt when a
+        weight is replaced or modified."""
+        from ..kernels.int4_linear import Int4Linear, stacked_int4
+        projs = (self.q_proj, self.k_proj, self.v_proj)
+        int4 = all(isinstance(m, Int4Linear) for m in projs)
+        ts = [t for m in projs for t in ((m.weight_packed, m.weight_scale) if int4 else
+                                         (m.weight,))]
+        key = (int4,) + tuple((t.data_ptr(), t._version) for t in ts)
+        if getattr(self, "_qkv_key", None) != key:
+            if int4:
+                assert all(m.bias is None for m in projs), "q/k/v projections carry no bias"
+                self._qkv_w = stacked_int4(projs)
+            else:
+                self._qkv_w = torch.cat([m.weight.detach() for m in projs], 0)
+            self._qkv_key = key
+        if int4:
+            from ..kernels.int4_gemm import int4_linear
+            packed, scale, g = self._qkv_w
+            return int4_linear(x2, packed, scale, g)
+        return F.linear(x2, self._qkv_w)
 
     def forward(self, x: torch.Tensor, rope: "RotaryEmbedding", pos: torch.Tensor,
                 cache: KVCache, layer: int, kv_len: int,
@@ -162,7 +177,7 @@ class Attention(nn.Module):
             # the kernel reads fp32 tables (a module-wide .half() would have cast them)
             cos_t = rope.cos_cached.float().contiguous()
             sin_t = rope.sin_cached.float().contiguous()
-            qkv = F.linear(x.reshape(B * S, -1), self._qkv_weight())
+            qkv = self._qkv(x.reshape(B * S, -1))
             wq, wk = nh * hd, nkv * hd
             qg = torch.empty((B, nkv, rep * S, hd), dtype=x.dtype, device=x.device)
             ld = qkv.stride(0)
@@ -378,6 +393,17 @@ class GraphDecoder:
         g.replay()
         self.cache.advance(1)
         return self.tok
+
+
+def convert_dense_to_int4(model: nn.Module, group_size: int = 128) -> nn.Module:
+    """The reference's INT4 option for non-expert weights (test_glm4_generate.py:
+    262-280: convert_model_to_int4 with lm_head and the embeddings kept):
+    every attention projection and dense MLP linear becomes an Int4Linear
+    (kernels/int4_linear.py).  The MoE routers' gates stay fp16 (the routing
+    kernels read them as such), as does the LM head."""
+    from ..kernels.int4_linear import convert_model_to_int4
+    return convert_model_to_int4(model, skip_layers=["lm_head", "embed", "router"],
+                                 group_size=group_size)
 
 
 def build_synthetic_decoder(cfg: MixtralDecoderConfig, device="cuda", decode_top_k: int = 1,
