@@ -27,6 +27,14 @@ constexpr int kMaxDevices = 64;
 std::atomic<int> g_cus[kMaxDevices];
 }  // namespace
 
+// Launch tags of the last-arriver counters (hn_common.h, hn_arrive).
+extern "C" unsigned long long hn_next_tag(void) {
+  static std::atomic<unsigned long long> tag{0};
+  const unsigned long long t = (tag.fetch_add(1, std::memory_order_relaxed) + 1) &
+                               ((1ull << 48) - 1);
+  return t ? t : 1;
+}
+
 extern "C" int hn_device_cus(void) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;

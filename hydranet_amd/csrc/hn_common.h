@@ -29,6 +29,9 @@ void hn_set_error(const char* fmt, ...);
 int hn_device_cus(void);
 // Current device index, clamped to the per-device caches' range (0..63).
 int hn_current_device(void);
+// A fresh launch tag for the last-arriver counters (see hn_arrive): process-
+// wide, strictly increasing, in [1, 2^48).
+unsigned long long hn_next_tag(void);
 #ifdef __cplusplus
 }
 #endif
@@ -151,3 +154,49 @@ __device__ __forceinline__ float hn_silu(float g) {
 }
 
 static inline int hn_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------
+// Last-arriver counters of the split reductions (skinny split-K, GEMM
+// stream-K).  A counter is a 64-bit word: bits [63:16] the tag of the launch
+// that claimed it, bits [15:0] the arrivals counted under that tag.  Every
+// launch takes a fresh tag (hn_next_tag).  An arriving wave first claims the
+// word for its launch with an atomic max of tag << 16 — a word left by any
+// earlier launch, finished or stopped part-way, holds a smaller tag and so
+// becomes tag << 16, a count of zero — then adds 1.  The two atomics of one
+// wave to one address stay in program order, so the claim precedes the
+// count.  The last arrival resets the word to 0, which keeps replays of a
+// captured graph (whose tag is fixed at capture) counting from zero; a
+// replay stopped part-way is the one case not healed by the next launch.
+// Launches that share a workspace concurrently race (on the partials too).
+//
+// Ordering, with the wave's partial stores issued before the call:
+//   hn_publish_partials();  n = hn_arrive(c, tag) on one lane;  broadcast n;
+//   if last: hn_acquire_agent(), reset, read every split's partial.
+// The partials are agent-scope atomic stores and loads (sc1: performed where
+// every XCD sees them, past this XCD's L2).  Publishing waits until the
+// wave's stores are acknowledged (vmcnt counts stores on gfx9) and is a
+// compiler memory barrier, so "partials stored" precedes "counted in"; the
+// last arrival's agent-scope acquire fence (L2/L1 invalidate) precedes its
+// reads.  An agent-scope release fence in place of the wait would also write
+// back this XCD's L2 for plain stores (buffer_wbl2), which the partials are
+// not: measured on MI355X it made the split-K GEMV 2-4x and the stream-K GEMM
+// 3-14 % slower, with identical results.  Returns the arrival's index,
+// 0-based; the caller is last when it is n - 1 for n arrivals.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void hn_publish_partials() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void hn_acquire_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+__device__ __forceinline__ int hn_arrive(unsigned long long* c, unsigned long long tag) {
+  __hip_atomic_fetch_max(c, tag << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long old =
+      __hip_atomic_fetch_add(c, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return (int)(old & 0xffffu);
+}
+__device__ __forceinline__ void hn_counter_reset(unsigned long long* c) {
+  __hip_atomic_store(c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Arrivals per counter are below 2^16.
+constexpr long kHnMaxArrivals = 0xffff;

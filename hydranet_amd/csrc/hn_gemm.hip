@@ -11,13 +11,15 @@
 // This is the one place the path is a real dense contraction, so it is built
 // around the MFMA pipe (v_mfma_f32_32x32x16_f16, which one wave per SIMD can
 // keep busy back to back):
-//  * Tile = 128 tokens x 256 weight rows, one workgroup of four waves per CU;
-//    a wave owns 64 weight rows -- one 32-row block of gate and the same rows
-//    of up (so the SwiGLU epilogue has both values of an output in one lane),
-//    or two 32-row blocks of one matrix -- for all 128 tokens.  Waves split
-//    N, never M, so each weight is dequantised by exactly one wave.
+//  * Tile = up to 256 tokens (eight 32-token row blocks; a tile whose rows
+//    fit in 128 runs the four-block loop) x 256 weight rows, one workgroup of
+//    four waves per CU; a wave owns 64 weight rows -- one 32-row block of gate
+//    and the same rows of up (so the SwiGLU epilogue has both values of an
+//    output in one lane), or two 32-row blocks of one matrix -- for all the
+//    tile's tokens.  Waves split N, never M, so each weight is dequantised by
+//    exactly one wave per tile.
 //  * Every load of the K loop goes HBM -> LDS directly (buffer_load ... lds,
-//    issued from inline asm with explicit waits), three stages of 128 k deep:
+//    issued from inline asm with explicit waits), three LDS stages of 64 k:
 //    activations (XOR-swizzled rows so A-fragment reads are conflict-free),
 //    packed weights and the dwords holding the scales.
 //  * Each k-step's A fragments and unpacked weights are double-buffered: step
@@ -32,6 +34,10 @@
 //    super-blocks of up to 8 M-tiles x n-tiles, and workgroups on one XCD
 //    take consecutive numbers, so tiles running together on an XCD share
 //    activation and weight slices in its L2.
+//  * Single problems with a caller workspace run stream-K: the (tile, stage)
+//    iterations are split evenly over the grid, and a tile whose stages span
+//    several workgroups is summed by its last-arriving wave from fp32
+//    partials (tagged counters, agent-scope acquire, hn_arrive).
 #include "hn_common.h"
 
 namespace {
@@ -64,7 +70,8 @@ struct GemmArgs {
   // iterations evenly; a tile whose stages span several workgroups is summed
   // from fp32 partial slots by the last of them to arrive (per wave).
   float* part;      // [4 * grid][kWaves][kWaveSlot]
-  int* ctr;         // [tiles * kWaves], zero between launches
+  unsigned long long* ctr;  // [tiles * kWaves] tagged counters (hn_arrive), left zero
+  unsigned long long tag;   // this launch's counter tag (hn_next_tag)
   int sk_ch;        // stages per stream-K chunk (chunks start on whole scale groups)
 };
 
@@ -404,8 +411,8 @@ constexpr long kWaveSlot = (long)kRBMax * kBlk * 16 * 64;  // floats
 // so no range is empty and a tile's segments belong to consecutive ranks.
 // A tile whose stages belong to several ranks ("segments") is finished by the
 // wave that arrives last: every segment stores its fp32 partial (relaxed
-// agent-scope atomics: coherent across XCDs without L2 write-back), then
-// counts itself in; the last one sums all the partials from the slots in
+// agent-scope atomics), publishes them and counts itself in
+// (hn_arrive); the last one acquires, sums all the partials from the slots in
 // segment order (deterministic) and resets the counter.
 struct SkSeg {
   int wf, nseg;  // first rank of the tile's segments, their number
@@ -441,15 +448,15 @@ __device__ __forceinline__ bool streamk_arrive(const GemmArgs& A, const f32x16 (
         for (int r = 0; r < 16; ++r)
           __hip_atomic_store(mine + ((rb * kBlk + b) * 16 + r) * 64 + lane, acc[rb][b][r],
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
-  int* c = A.ctr + (long)ctile * kWaves + wave;
-  int last = 0;
-  if (lane == 0)
-    last = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           sgi.nseg - 1;
-  last = __builtin_amdgcn_readfirstlane(last);
-  if (last && lane == 0) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return last != 0;
+  hn_publish_partials();
+  unsigned long long* c = A.ctr + (long)ctile * kWaves + wave;
+  int n = 0;
+  if (lane == 0) n = hn_arrive(c, A.tag);
+  n = __builtin_amdgcn_readfirstlane(n);
+  if (n != sgi.nseg - 1) return false;
+  hn_acquire_agent();
+  if (lane == 0) hn_counter_reset(c);
+  return true;
 }
 
 // The sum over the tile's segments of one accumulator register r of block
@@ -765,8 +772,9 @@ int grid_for(long tiles_upper) {
 // Stream-K workspace: per-(tile, wave) counters, then four partial slots per
 // workgroup of the full grid (the first and last tile of each pass).
 constexpr long kSkCounters = 1L << 16;          // tiles * kWaves
-constexpr long kSkCtrBytes = kSkCounters * 4;
+constexpr long kSkCtrBytes = kSkCounters * 8;
 constexpr int kSkMaxGrid = 256;   // workgroups (one per CU on MI355X)
+static_assert(kSkMaxGrid <= kHnMaxArrivals, "segments per tile fit a counter");
 
 long sk_bytes() { return kSkCtrBytes + 4L * kSkMaxGrid * kWaves * kWaveSlot * 4; }
 
@@ -786,7 +794,8 @@ bool sk_setup(GemmArgs& A, void* work, long work_bytes, long tiles_upper, dim3& 
     if (T % c == 0 && (c * kKS) % (2 * A.group) == 0) { ch = c; break; }
   if (ch == 0) return false;
   A.sk_ch = ch;
-  A.ctr = (int*)work;
+  A.ctr = (unsigned long long*)work;
+  A.tag = hn_next_tag();
   A.part = (float*)((char*)work + kSkCtrBytes);
   grid = dim3(g);
   return true;

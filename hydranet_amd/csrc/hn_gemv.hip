@@ -22,8 +22,8 @@
 //    order) for the A operand.
 //  * Only when the activation chunk would not fit in LDS is K also split over
 //    workgroups (blockIdx.y): each split writes fp32 partials, the last split
-//    of a tile (atomic counter, reset to 0 by it) sums them in split order —
-//    deterministic — and runs the epilogue.
+//    of a tile (tagged counter, hn_arrive; acquire at agent scope)
+//    sums them in split order — deterministic — and runs the epilogue.
 //  * Tokens beyond 16 (up to 64) reuse the unpacked B operand with another
 //    MFMA per 16-token chunk.
 //  * Group scales multiply the fp32 MFMA partial of each 128-k group when
@@ -67,7 +67,8 @@ struct SkinnyArgs {
   int tg;          // tiles per workgroup
   int ldx;         // LDS row stride of the x chunk (halves)
   float* partial;  // [ks][MATS][part_rows][N] fp32 when ks > 1
-  int* counters;   // [E?][tiles] zero on entry, left zero on exit
+  unsigned long long* counters;  // [E?][tiles] tagged counters (hn_arrive), left zero
+  unsigned long long tag;        // this launch's counter tag (hn_next_tag)
   long part_rows;  // row capacity of one (split, mat) partial plane
   // grouped mode
   const ExpertW4* table;
@@ -83,7 +84,8 @@ struct SkinnyArgs {
 template <int MATS, int EPI, bool PREMUL, int NCH, int XR>
 __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __restrict__ x,
                                             int Mc, const W4Mat* mats, h16* __restrict__ out,
-                                            float* __restrict__ part, int* __restrict__ ctr,
+                                            float* __restrict__ part,
+                                            unsigned long long* __restrict__ ctr,
                                             unsigned char* smem) {
   constexpr int BATCH = kLoadsPerLane / MATS;  // loads per lane per matrix (even)
   static_assert(BATCH % 2 == 0, "groups are loaded in pairs");
@@ -327,9 +329,9 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
     return;
   }
   // split over workgroups: write partials, the last split of this tile reduces
-  // in split order.  Partials and counters are relaxed agent-scope atomics (sc1
-  // accesses, coherent across XCDs without writing back or invalidating the
-  // L2); the s_waitcnt orders "partials stored" before "counter incremented".
+  // in split order.  Partials are relaxed agent-scope atomics, published
+  // before the count; the last split acquires before reading them
+  // (hn_arrive).
   const long plane = A.part_rows * (long)N;
   if (row_ok) {
 #pragma unroll
@@ -344,14 +346,13 @@ __device__ __forceinline__ void skinny_unit(const SkinnyArgs& A, const h16* __re
                                acc[c][mt][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  int last = 0;
-  if (lane == 0)
-    last = __hip_atomic_fetch_add(ctr + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           A.ks - 1;
-  last = __shfl(last, 0, 64);
-  if (!last) return;
-  if (lane == 0) __hip_atomic_store(ctr + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  hn_publish_partials();
+  int n = 0;
+  if (lane == 0) n = hn_arrive(ctr + tile, A.tag);
+  n = __shfl(n, 0, 64);
+  if (n != A.ks - 1) return;
+  hn_acquire_agent();
+  if (lane == 0) hn_counter_reset(ctr + tile);
   // this wave now owns the tile's 16 rows x Mc tokens: lanes walk (token, row);
   // all partial loads of an element are issued together (one round trip)
   for (int e = lane; e < Mc * kTileN; e += 64) {
@@ -407,7 +408,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void grouped_kernel(SkinnyArgs A) {
   const ExpertW4 ew = A.table[e];
   const int H = A.H, I = A.I, g = A.group;
   const int tmax = max((H + kTileN - 1) / kTileN, (I + kTileN - 1) / kTileN);
-  int* ctr = A.counters + (long)e * tmax;
+  unsigned long long* ctr = A.counters + (long)e * tmax;
   float* part = A.partial + (long)t0 * A.N;  // row offset inside each plane
   if (PHASE == 0) {
     const W4Mat mats[2] = {{ew.gate_q, ew.gate_s, H / 2, H / g}, {ew.up_q, ew.up_s, H / 2, H / g}};
@@ -528,10 +529,11 @@ constexpr int kMaxRows = 64;  // tokens per weight matrix handled per launch
 // Workspace layout, the same for every call: [counters: a fixed 2 MiB region
 // at the start][partials].  One buffer serves calls of every kind and size
 // in turn; with the counter region fixed, no call's partials ever land on
-// another call's counters (which must read zero on entry; every launch
-// leaves its counters at zero).
+// another call's counters (64-bit tagged words, hn_arrive: zero when the
+// workspace is new; a launch leaves its counters at zero, and a counter left
+// by a launch stopped part-way is reclaimed by the next launch's tag).
 constexpr size_t kCtrRegion = 2u << 20;
-constexpr long kMaxCounters = (long)(kCtrRegion / 4);
+constexpr long kMaxCounters = (long)(kCtrRegion / 8);
 size_t ctr_bytes(long /*counters*/) { return kCtrRegion; }
 
 size_t part_bytes(int ks, int mats, long rows, long N) {
@@ -673,6 +675,7 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
     const size_t need = cb + part_bytes(p.ks, mats, rows, N);
     HN_ARG_CHECK(p.ks == 1 || (ws && (size_t)ws_size >= need),
                  "%s: workspace too small (%ld < %zu bytes)", who, ws_size, need);
+    HN_ARG_CHECK(p.ks <= kHnMaxArrivals, "%s: K=%ld splits into too many chunks", who, K);
     SkinnyArgs A = {};
     A.x = (const h16*)x + m0 * ld_x;
     A.ld_x = ld_x;
@@ -685,7 +688,8 @@ static int run_single(int mats, const void* x, long ld_x, W4Mat w0, W4Mat w1, vo
     A.K = (int)K;
     A.group = (int)group;
     apply_plan(A, p);
-    A.counters = (int*)ws;
+    A.counters = (unsigned long long*)ws;
+    A.tag = hn_next_tag();
     A.partial = ws ? (float*)((char*)ws + cb) : nullptr;
     A.part_rows = rows;
     if (mats == 2) {
@@ -818,13 +822,16 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
   A.H = (int)H;
   A.I = (int)I;
   A.group = (int)group;
-  A.counters = (int*)work;
+  A.counters = (unsigned long long*)work;
+  A.tag = hn_next_tag();
   A.part_rows = rows;
   A.M = rmax;
   const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
                                                             : hn_cdiv(H, kTileN);
   HN_ARG_CHECK(E * tmax <= kMaxCounters, "%s: E=%ld x %ld tiles exceed the counter region", who,
                E, tmax);
+  HN_ARG_CHECK(hn_cdiv(H, 128) <= kHnMaxArrivals && hn_cdiv(I, 128) <= kHnMaxArrivals,
+               "%s: H=%ld or I=%ld splits into too many chunks", who, H, I);
   float* partial = (float*)((char*)work + ctr_bytes(E * tmax));
   {
     const Plan p = make_plan(rmax, (int)H, 2);
@@ -844,6 +851,7 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
     A.out = (h16*)y_perm; A.ld_o = H;
     A.N = (int)H; A.K = (int)I;
     apply_plan(A, p);
+    A.tag = hn_next_tag();
     A.partial = partial;
     A.phase = 1;
     if (premul) launch_grouped<1, true>(A, p, (int)E, s);
