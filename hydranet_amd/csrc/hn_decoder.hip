@@ -20,12 +20,20 @@ namespace {
 
 constexpr int kNormThreads = 256;
 
-// One workgroup per row; 8 fp16 per vector access.
+constexpr int kMaxGate = 16;  // router experts the norm kernel can score
+
+// One workgroup per row; 8 fp16 per vector access.  LOGITS: also the router
+// logits of the normalised row, logits[row, e] = fp16(sum_k out[k] gate[e, k])
+// (fp32 sums: per thread, then the wave, then the waves in order) stored as
+// fp32 -- the fp16 Linear of TopKRouter (model/router.py:102) on this row.
+template <bool LOGITS>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     const h16* __restrict__ x, long ld_x, const h16* __restrict__ res, long ld_r,
     h16* __restrict__ x_out, long ld_xo, const h16* __restrict__ w, h16* __restrict__ out,
-    long ld_o, int H, float eps) {
+    long ld_o, int H, float eps, const h16* __restrict__ gate, long ld_g, int E,
+    float* __restrict__ logits) {
   __shared__ float s_part[kNormThreads / 64];
+  __shared__ float s_lg[kNormThreads / 64][kMaxGate];
   const int row = blockIdx.x, tid = threadIdx.x;
   const half8_t* xr = reinterpret_cast<const half8_t*>(x + (long)row * ld_x);
   const half8_t* rr = res ? reinterpret_cast<const half8_t*>(res + (long)row * ld_r) : nullptr;
@@ -72,6 +80,33 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
         o[e] = (h16)((float)wv[e] * t);
       }
       orow[j] = o;
+      if constexpr (LOGITS) v[i] = o;
+    }
+  }
+  if constexpr (LOGITS) {
+    const int lane = tid & 63, wave = tid >> 6;
+    for (int e = 0; e < E; ++e) {  // uniform
+      const half8_t* gr = reinterpret_cast<const half8_t*>(gate + (long)e * ld_g);
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = tid + i * kNormThreads;
+        if (j < nv) {
+          const half8_t gv = gr[j];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) d = __builtin_fmaf((float)v[i][q], (float)gv[q], d);
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
+      if (lane == 0) s_lg[wave][e] = d;
+    }
+    __syncthreads();
+    if (tid < E) {
+      float d = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < kNormThreads / 64; ++wv) d += s_lg[wv][tid];
+      logits[(long)row * E + tid] = (float)(h16)d;
     }
   }
 }
@@ -134,10 +169,35 @@ extern "C" int hn_add_rmsnorm(const void* x, long ld_x, const void* res, long ld
                    (!x_out || (al16(x_out) && ld_xo % 8 == 0)),
                "hn_add_rmsnorm: rows must be 16-byte aligned");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)T), dim3(kNormThreads), 0,
+  hipLaunchKernelGGL(add_rmsnorm_kernel<false>, dim3((unsigned)T), dim3(kNormThreads), 0,
                      (hipStream_t)stream, (const h16*)x, ld_x, (const h16*)res, ld_r,
-                     (h16*)x_out, ld_xo, (const h16*)w, (h16*)out, ld_o, (int)H, eps);
+                     (h16*)x_out, ld_xo, (const h16*)w, (h16*)out, ld_o, (int)H, eps,
+                     (const h16*)nullptr, 0L, 0, (float*)nullptr);
   HN_LAUNCH_CHECK("hn_add_rmsnorm");
+  return 0;
+}
+
+// hn_add_rmsnorm, then the router logits of each normalised row against an
+// fp16 gate [E, H] (E <= 16): logits [T, E] fp32 holding fp16-rounded values.
+// See include/hn_int4.h.
+extern "C" int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, long ld_r,
+                                     void* x_out, long ld_xo, const void* w, void* out,
+                                     long ld_o, long T, long H, float eps, const void* gate,
+                                     long ld_g, long E, float* logits, void* stream) {
+  HN_ARG_CHECK(T >= 0 && H > 0 && H % 8 == 0 && H <= 8 * kNormThreads * 4,
+               "hn_add_rmsnorm_router: need 0 < H <= %d, H %% 8 == 0", 8 * kNormThreads * 4);
+  HN_ARG_CHECK(E > 0 && E <= kMaxGate, "hn_add_rmsnorm_router: need 0 < E <= %d", kMaxGate);
+  HN_ARG_CHECK(al16(x) && ld_x % 8 == 0 && al16(w) && al16(out) && ld_o % 8 == 0 &&
+                   (!res || (al16(res) && ld_r % 8 == 0)) &&
+                   (!x_out || (al16(x_out) && ld_xo % 8 == 0)) && gate && al16(gate) &&
+                   ld_g % 8 == 0 && ld_g >= H && logits,
+               "hn_add_rmsnorm_router: rows must be 16-byte aligned (gate and logits given)");
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(add_rmsnorm_kernel<true>, dim3((unsigned)T), dim3(kNormThreads), 0,
+                     (hipStream_t)stream, (const h16*)x, ld_x, (const h16*)res, ld_r,
+                     (h16*)x_out, ld_xo, (const h16*)w, (h16*)out, ld_o, (int)H, eps,
+                     (const h16*)gate, ld_g, (int)E, logits);
+  HN_LAUNCH_CHECK("hn_add_rmsnorm_router");
   return 0;
 }
 

@@ -203,14 +203,20 @@ class Attention(nn.Module):
         return self.o_proj(o.transpose(1, 2).reshape(B, S, nh * hd))
 
 
-def add_rmsnorm(x: torch.Tensor, res: Optional[torch.Tensor], norm: RMSNorm):
+def add_rmsnorm(x: torch.Tensor, res: Optional[torch.Tensor], norm: RMSNorm,
+                gate: Optional[torch.Tensor] = None):
     """(x + res, norm(x + res)); res None: (x, norm(x)).  On the GPU one
     kernel (hn_add_rmsnorm) with the torch formulation's fp16 add and fp32
-    normalisation."""
+    normalisation.  gate: an fp16 router gate [E, H]; then a third result,
+    the router logits [T, E] of the normalised rows (hn_add_rmsnorm_router)."""
     if not x.is_cuda:
         if res is not None:
             x = x + res
-        return x, norm(x)
+        h = norm(x)
+        if gate is None:
+            return x, h
+        lg = F.linear(h, gate).float()
+        return x, h, lg.reshape(-1, gate.shape[0])
     from .. import _lib
     H = x.shape[-1]
     assert norm.weight.dtype == torch.float16 and x.dtype == torch.float16
@@ -221,10 +227,19 @@ def add_rmsnorm(x: torch.Tensor, res: Optional[torch.Tensor], norm: RMSNorm):
     if res is not None:
         r2 = res.reshape(-1, H).contiguous()
         xo = torch.empty_like(x2)
-    _lib.call("hn_add_rmsnorm", _lib.ptr(x2), H, _lib.ptr(r2), H,
+    if gate is None:
+        _lib.call("hn_add_rmsnorm", _lib.ptr(x2), H, _lib.ptr(r2), H,
+                  _lib.ptr(xo) if res is not None else None, H, _lib.ptr(norm.weight),
+                  _lib.ptr(out), H, T, H, norm.eps, _lib.stream(x.device))
+        return xo.view(x.shape), out.view(x.shape)
+    assert gate.dtype == torch.float16 and gate.shape[1] == H and gate.stride(1) == 1
+    E = gate.shape[0]
+    lg = torch.empty((T, E), dtype=torch.float32, device=x.device)
+    _lib.call("hn_add_rmsnorm_router", _lib.ptr(x2), H, _lib.ptr(r2), H,
               _lib.ptr(xo) if res is not None else None, H, _lib.ptr(norm.weight), _lib.ptr(out),
-              H, T, H, norm.eps, _lib.stream(x.device))
-    return xo.view(x.shape), out.view(x.shape)
+              H, T, H, norm.eps, _lib.ptr(gate), gate.stride(0), E, _lib.ptr(lg),
+              _lib.stream(x.device))
+    return xo.view(x.shape), out.view(x.shape), lg
 
 
 def causal_mask(start: int, S: int, device, dtype=torch.float16) -> torch.Tensor:
@@ -251,6 +266,13 @@ class DecoderBlock(nn.Module):
         previous block's MoE output, added to x first."""
         x, h = add_rmsnorm(x, pending, self.input_layernorm)
         a = self.self_attn(h, rope, pos, cache, self.layer_idx, kv_len, mask)
+        T = h.shape[0] * h.shape[1]
+        gw = self.moe.router.gate.weight
+        if x.is_cuda and gw.dtype == torch.float16 and self.moe.takes_logits(T, top_k):
+            # the router logits come out of the norm kernel (no gate product
+            # in the routing launch)
+            x, h, lg = add_rmsnorm(x, a, self.post_attention_layernorm, gate=gw)
+            return x, self.moe(h, top_k=top_k, logits=lg)
         x, h = add_rmsnorm(x, a, self.post_attention_layernorm)
         return x, self.moe(h, top_k=top_k)
 

@@ -331,15 +331,35 @@ class MixtralMoELayer(nn.Module):
         # (idx [T, k] int32, w [T, k] fp16) of the last forward, on the device
         self.last_routing = None
 
-    def forward(self, hidden_states: torch.Tensor, top_k: int = 2) -> torch.Tensor:
+    def takes_logits(self, T: int, top_k: int) -> bool:
+        """Whether a forward of T tokens routes through hn_moe_route, whose
+        gate product a caller can save by passing the router logits (e.g. from
+        hn_add_rmsnorm_router); False where the fused decode layer computes
+        them inside its gate/up kernel, or the batch is past the one-launch
+        routing."""
+        E, gw = self.num_experts, self.router.gate.weight
+        if not route_fits(T, E, top_k) or E > 16 or not gw.is_cuda:
+            return False
+        rt = self.router
+        if rt.enable_affinity_bonus and rt._is_cached_fn is not None:
+            return True
+        table = self.experts.static_table(gw.device)
+        return not (table is not None and decode_layer_fits(T, E, top_k, table, gw))
+
+    def forward(self, hidden_states: torch.Tensor, top_k: int = 2,
+                logits: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """logits: optional router logits [T, E] of hidden_states (fp16 values
+        in fp32, as TopKRouter's gate Linear gives), used in place of the gate
+        product where the routing takes them (takes_logits)."""
         B, S, H = hidden_states.shape
         T = B * S
         flat = hidden_states.reshape(T, H)
         rt = self.router
         if route_fits(T, self.num_experts, top_k):
-            logits = None
             if rt.enable_affinity_bonus and rt._is_cached_fn is not None:
-                logits = rt._affinity(router_logits(flat, rt.gate.weight.to(torch.float16)))
+                if logits is None:
+                    logits = router_logits(flat, rt.gate.weight.to(torch.float16))
+                logits = rt._affinity(logits)
             table = self.experts.static_table(flat.device) if logits is None else None
             if table is not None and decode_layer_fits(T, self.num_experts, top_k, table,
                                                        rt.gate.weight):

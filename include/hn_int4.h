@@ -264,6 +264,17 @@ int hn_expert_mlp_int4_noalloc(const void* x, const void* gq, const void* gs, co
 int hn_add_rmsnorm(const void* x, long ld_x, const void* res, long ld_r, void* x_out,
                    long ld_xo, const void* w, void* out, long ld_o, long T, long H, float eps,
                    void* stream);
+/* hn_add_rmsnorm_router: hn_add_rmsnorm, then the router logits of each
+ *   normalised row against an fp16 gate [E, H] (row stride ld_g, E <= 16):
+ *   logits[t, e] = fp16(sum_k out[t, k] * gate[e, k]) with fp32 sums, stored as
+ *   fp32 [T, E].  The post-attention RMSNorm (model/mixtral.py:423-425) fused
+ *   with TopKRouter's fp16 gate Linear (model/router.py:102); the logits feed
+ *   hn_moe_route's logits_in.  The sum's order is its own: a logit may differ
+ *   from a GEMM's by an fp16 ulp. */
+int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, long ld_r, void* x_out,
+                          long ld_xo, const void* w, void* out, long ld_o, long T, long H,
+                          float eps, const void* gate, long ld_g, long E, float* logits,
+                          void* stream);
 int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k, const void* v, long ld_v,
                    const float* cos_t, const float* sin_t, const long* pos, long B, long S,
                    long nh, long nkv, long hd, void* q_out, void* kt, void* vc, long max_len,

@@ -42,6 +42,43 @@ def test_add_rmsnorm(T, H):
         assert (out != ref).float().mean().item() < 0.02
 
 
+@pytest.mark.parametrize("T,H,E", [(1, 4096, 8), (64, 4096, 8), (5, 512, 16), (3, 1024, 3)])
+def test_add_rmsnorm_router(T, H, E):
+    """The norm output equals hn_add_rmsnorm's bit for bit; the logits are the
+    fp16 gate product of that output: fp16 values within one fp16 ulp of the
+    float64 product rounded to fp16 (the fp32 sum's order is the kernel's)."""
+    g = torch.Generator(device=DEV).manual_seed(T * 31 + E)
+    x = torch.randn(T, H, generator=g, device=DEV).half()
+    r = (torch.randn(T, H, generator=g, device=DEV) * 0.5).half()
+    w = (1 + 0.1 * torch.randn(H, generator=g, device=DEV)).half()
+    gate = (torch.randn(E, H, generator=g, device=DEV) * 0.02).half()
+    st = _lib.stream()
+    out0, xo0 = torch.empty_like(x), torch.empty_like(x)
+    _lib.call("hn_add_rmsnorm", _lib.ptr(x), H, _lib.ptr(r), H, _lib.ptr(xo0), H, _lib.ptr(w),
+              _lib.ptr(out0), H, T, H, 1e-5, st)
+    out1, xo1 = torch.empty_like(x), torch.empty_like(x)
+    lg = torch.full((T, E), float("nan"), device=DEV)
+    _lib.call("hn_add_rmsnorm_router", _lib.ptr(x), H, _lib.ptr(r), H, _lib.ptr(xo1), H,
+              _lib.ptr(w), _lib.ptr(out1), H, T, H, 1e-5, _lib.ptr(gate), H, E, _lib.ptr(lg), st)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out0) and torch.equal(xo1, xo0)
+    assert torch.equal(lg, lg.half().float()), "logits hold fp16 values"
+    ref = (out0.double().cpu() @ gate.double().cpu().t()).half().double()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - 10)
+    assert bool(((lg.double().cpu() - ref).abs() <= ulp).all())
+
+
+def test_add_rmsnorm_router_rejects_bad_arguments():
+    x = torch.zeros(2, 512, device=DEV).half()
+    w = torch.ones(512, device=DEV).half()
+    gate = torch.zeros(17, 512, device=DEV).half()
+    lg = torch.zeros(2, 17, device=DEV)
+    with pytest.raises(RuntimeError, match="E <= 16"):
+        _lib.call("hn_add_rmsnorm_router", _lib.ptr(x), 512, None, 512, None, 512, _lib.ptr(w),
+                  _lib.ptr(x), 512, 2, 512, 1e-5, _lib.ptr(gate), 512, 17, _lib.ptr(lg),
+                  _lib.stream())
+
+
 def test_add_rmsnorm_in_place_residual():
     """x_out may alias x (the residual stream updated in place)."""
     H, T = 1024, 4
