@@ -36,9 +36,11 @@ unsigned long long hn_next_tag(void);
 }
 #endif
 
-// Per-device flag that a kernel's dynamic-LDS limit was raised to the CU's
-// 160 KiB (hipFuncSetAttribute is per device): 0 unknown, 1 raised, 2 refused.
-struct HnLdsAttr {
+// One int per device index (0 = not yet known), for per-kernel facts that
+// are set or queried once per device: whether its dynamic-LDS limit was
+// raised to the CU's 160 KiB (1 raised, 2 refused), how many of its
+// workgroups its registers let one CU hold.
+struct HnPerDevice {
   std::atomic<int> state[64] = {};
 };
 

@@ -578,8 +578,8 @@ extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const v
                                      long group, void* stream);
 extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const void* table,
                                       const int* active, const int* n_active, const int* offsets,
-                                      long E, long max_rows, long H, long I, long group, void* out,
-                                      long ld_o, void* stream, int dry_run);
+                                      long E, long max_rows, long rows, long H, long I, long group,
+                                      void* out, long ld_o, void* stream, int dry_run);
 extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const int* active,
                                          const int* n_active, const int* offsets, long E,
                                          long max_rows, long rows_cap, long H, long I,
@@ -804,14 +804,14 @@ extern "C" int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table,
   const bool premul = (group % 128) != 0;
   if (g_decode_path == 0 && !premul && stream_rows_ok(max_rows_per_expert, rows, E) &&
       hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
-                             max_rows_per_expert, H, I, group, h_ws, I, s, 1) == 0 &&
+                             max_rows_per_expert, rows, H, I, group, h_ws, I, s, 1) == 0 &&
       hn_stream_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E,
-                             max_rows_per_expert, H, I, group, y_perm, H, s, 1) == 0) {
+                             max_rows_per_expert, rows, H, I, group, y_perm, H, s, 1) == 0) {
     int rc = hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
-                                    max_rows_per_expert, H, I, group, h_ws, I, s, 0);
+                                    max_rows_per_expert, rows, H, I, group, h_ws, I, s, 0);
     if (rc) return rc;
     return hn_stream_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E,
-                                  max_rows_per_expert, H, I, group, y_perm, H, s, 0);
+                                  max_rows_per_expert, rows, H, I, group, y_perm, H, s, 0);
   }
   const int rmax = (int)max_rows_per_expert;
   SkinnyArgs A = {};
@@ -912,7 +912,7 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
       g_decode_path == 0 && !premul && H % 128 == 0 && I % 128 == 0 && aligned16(x_perm) &&
       aligned16(h_ws) &&
       hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
-                             max_rows_per_expert, H, I, group, h_ws, I, s, 1) == 0 &&
+                             max_rows_per_expert, rows, H, I, group, h_ws, I, s, 1) == 0 &&
       hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, max_rows_per_expert,
                                 rows, H, I, group, nullptr, s, 1) == 0) {
     const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
@@ -922,7 +922,7 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
                  work_bytes, need);
     float* part = (float*)((char*)work + ctr_bytes(E * tmax));
     int rc = hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
-                                    max_rows_per_expert, H, I, group, h_ws, I, s, 0);
+                                    max_rows_per_expert, rows, H, I, group, h_ws, I, s, 0);
     if (rc == 0)
       rc = hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E,
                                      max_rows_per_expert, rows, H, I, group, part, s, 0);
@@ -1042,7 +1042,7 @@ extern "C" int hn_grouped_decode_phase_int4(int phase, const void* x, const void
   int rc;
   if (phase == 0) {
     rc = hn_stream_grouped_impl(0, x, H, table, active, n_active, offsets, E,
-                                max_rows_per_expert, H, I, group, h_ws, I, s, 0);
+                                max_rows_per_expert, rows, H, I, group, h_ws, I, s, 0);
   } else {
     const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
                                                               : hn_cdiv(H, kTileN);

@@ -180,15 +180,31 @@ __device__ int route_prologue(const StreamArgs& A, float* part, int* s_act, int*
 // slice (one staging); each column's wave-reduced partial is written in fp32
 // and the caller sums the KS slices in order.  A slice keeps the workgroup's
 // activations and the pipeline short where K is long (the down projection).
+// Waves per SIMD the register budget must allow: single-matrix launches of
+// 8-token chunks and four groups per wave run two 7- or 8-wave workgroups
+// per CU (four waves per SIMD, so at most 128 VGPRs); the others one
+// workgroup (their plans may still ask for two; launch_one then checks what
+// the registers allow).
+template <int MATS, int TH, int LPW>
+constexpr int stream_waves_per_eu() { return MATS == 1 && TH == 1 && LPW <= 4 ? 4 : 1; }
+
 template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS,
-          bool ROUTE = false>
-__global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
+          bool ROUTE = false, int TH = 1>
+__global__ __launch_bounds__(512)
+__attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void stream_kernel(
+    StreamArgs A,
                                                      const SExpert* __restrict__ table,
                                                      const int* __restrict__ active,
                                                      const int* __restrict__ n_active,
                                                      const int* __restrict__ offsets) {
   constexpr int PAIRS = LPW / 2;
   static_assert(NBUF == 2 || NBUF == 3, "two or three column buffers");
+  static_assert(TH == 1 || TH == 2, "8 or 16 tokens per chunk");
+  static_assert(!(ROUTE && TH == 2), "the routing prologue takes 8-token chunks");
+  // reduction buffers: parity-double-buffered (one barrier per column) unless
+  // that no longer fits beside 16 tokens of gate/up activations; then one
+  // buffer and a second barrier per column
+  constexpr int NRB = (TH == 2 && MATS == 2) ? 1 : 2;
   extern __shared__ __align__(16) unsigned char smem[];
   Meta meta = {nullptr, nullptr, nullptr};
   __shared__ int chunk_off[kMaxActive + 1];
@@ -207,8 +223,8 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
   const int pb0 = g0 >> 1;                     // its first group pair
   h16* xs = reinterpret_cast<h16*>(smem);
   float* cs = reinterpret_cast<float*>(smem + (size_t)TC * 2 * A.ldx * 2);
-  float2* red = reinterpret_cast<float2*>(cs + A.npair * 16);
-  constexpr int kRedSlots = (kMaxWaves - 1) * MATS * 64;  // per parity
+  float2* red = reinterpret_cast<float2*>(cs + A.npair * kCsw);
+  constexpr int kRedSlots = (kMaxWaves - 1) * TH * MATS * 64;  // per buffer
   HnUnpackRegs ur;
   ur.m_lo = A.m_lo;
   ur.m_hi = A.m_hi;
@@ -221,7 +237,7 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     // one round of independent loads: active list, offsets, weight pointers
     // (ROUTE: the pointers only; the active list and offsets are computed)
     const int E = A.E;
-    int* s_act = reinterpret_cast<int*>(red + 2 * kRedSlots);
+    int* s_act = reinterpret_cast<int*>(red + NRB * kRedSlots);
     int* s_off = s_act + ((E + 1) & ~1);
     uint64_t* s_ptr = reinterpret_cast<uint64_t*>(s_off + ((E + 2) & ~1));
     const uint64_t* tw = reinterpret_cast<const uint64_t*>(table);
@@ -278,8 +294,8 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     chunk_off[1] = (A.M + TC - 1) / TC;
   }
   // reduction slots of waves this workgroup does not have stay zero
-  for (int i = tid; i < 2 * kRedSlots; i += blockDim.x) {
-    const int slot = (i / (MATS * 64)) % (kMaxWaves - 1);
+  for (int i = tid; i < NRB * kRedSlots; i += blockDim.x) {
+    const int slot = (i / (TH * MATS * 64)) % (kMaxWaves - 1);
     if (slot >= KW - 1) red[i] = float2{0.f, 0.f};
   }
   __syncthreads();
@@ -378,69 +394,88 @@ __global__ __launch_bounds__(512) void stream_kernel(StreamArgs A,
     issue_next(nxt);
     if (c < ce) {
       const int Mc = sg.Mc;
-      const int arow_i = 2 * min(col >> 1, Mc - 1) + (col & 1);
-      float4_t acc_lo[MATS], acc_hi[MATS];
-      compute<MATS, PAIRS, WIDE>(cur, xs, cs, A.ldx, pb0, gw, arow_i, q, col >= 8 ? 16 : 0, ur,
-                                 acc_lo, acc_hi);
-      // lane (col, q): row n0 + col, tokens 2q, 2q + 1 (both group parities)
-      float2 v[MATS];
+      int arow_i[TH];
+#pragma unroll
+      for (int h = 0; h < TH; ++h) arow_i[h] = 2 * min(8 * h + (col >> 1), Mc - 1) + (col & 1);
+      float4_t acc_lo[TH][MATS], acc_hi[TH][MATS];
+      compute<MATS, PAIRS, WIDE, TH>(cur, xs, cs, A.ldx, pb0, gw, arow_i, q, col >= 8 ? 16 : 0,
+                                     ur, acc_lo, acc_hi);
+      // lane (col, q): row n0 + col, tokens 8h + 2q, 8h + 2q + 1 (both group parities)
+      float2 v[TH][MATS];
       const bool low = col < 8;
 #pragma unroll
-      for (int mt = 0; mt < MATS; ++mt) {
-        const float e0 = low ? acc_lo[mt][0] : acc_hi[mt][1];
-        const float u0 = low ? acc_hi[mt][0] : acc_lo[mt][1];
-        const float e1 = low ? acc_lo[mt][2] : acc_hi[mt][3];
-        const float u1 = low ? acc_hi[mt][2] : acc_lo[mt][3];
-        v[mt] = float2{e0 + xor8(u0), e1 + xor8(u1)};
-      }
+      for (int h = 0; h < TH; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MATS; ++mt) {
+          const float e0 = low ? acc_lo[h][mt][0] : acc_hi[h][mt][1];
+          const float u0 = low ? acc_hi[h][mt][0] : acc_lo[h][mt][1];
+          const float e1 = low ? acc_lo[h][mt][2] : acc_hi[h][mt][3];
+          const float u1 = low ? acc_hi[h][mt][2] : acc_lo[h][mt][3];
+          v[h][mt] = float2{e0 + xor8(u0), e1 + xor8(u1)};
+        }
       // KW-wave reduction through LDS (parity-buffered: one barrier per
-      // column), summed in wave order by wave 0, which writes the tile
-      float2* rb = red + parity * kRedSlots;
+      // column; single-buffered: a second barrier first, after which wave 0
+      // has read the previous column's partials), summed in wave order by
+      // wave 0, which writes the tile
+      float2* rb = red + (NRB == 2 ? parity * kRedSlots : 0);
+      if (NRB == 1) __syncthreads();
       if (wave > 0) {
 #pragma unroll
-        for (int mt = 0; mt < MATS; ++mt) rb[((wave - 1) * MATS + mt) * 64 + lane] = v[mt];
+        for (int h = 0; h < TH; ++h)
+#pragma unroll
+          for (int mt = 0; mt < MATS; ++mt)
+            rb[(((wave - 1) * TH + h) * MATS + mt) * 64 + lane] = v[h][mt];
       }
       __syncthreads();
       if (wave == 0) {
-        float2 o[kMaxWaves - 1][MATS];
+        float2 o[kMaxWaves - 1][TH][MATS];
 #pragma unroll
         for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
 #pragma unroll
-          for (int mt = 0; mt < MATS; ++mt) o[w2][mt] = rb[(w2 * MATS + mt) * 64 + lane];
+          for (int h = 0; h < TH; ++h)
+#pragma unroll
+            for (int mt = 0; mt < MATS; ++mt)
+              o[w2][h][mt] = rb[((w2 * TH + h) * MATS + mt) * 64 + lane];
 #pragma unroll
         for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
 #pragma unroll
-          for (int mt = 0; mt < MATS; ++mt) {
-            v[mt].x += o[w2][mt].x;
-            v[mt].y += o[w2][mt].y;
-          }
+          for (int h = 0; h < TH; ++h)
+#pragma unroll
+            for (int mt = 0; mt < MATS; ++mt) {
+              v[h][mt].x += o[w2][h][mt].x;
+              v[h][mt].y += o[w2][h][mt].y;
+            }
         const int row = (t - st_kj * tiles_n) * kTileN + col;
         if (KS > 1) {
           if (row < N) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const int m = 2 * q + j;
-              if (m < Mc)
-                A.out32[st_kj * A.ks_stride + (long)(st_pr.t0 + sg.m0 + m) * N + row] =
-                    j ? v[0].y : v[0].x;
-            }
+            for (int h = 0; h < TH; ++h)
+#pragma unroll
+              for (int j = 0; j < 2; ++j) {
+                const int m = 8 * h + 2 * q + j;
+                if (m < Mc)
+                  A.out32[st_kj * A.ks_stride + (long)(st_pr.t0 + sg.m0 + m) * N + row] =
+                      j ? v[h][0].y : v[h][0].x;
+              }
           }
         } else if (row < N) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int m = 2 * q + j;
-            if (m < Mc) {
-              const float g = j ? v[0].y : v[0].x;
-              h16 o16;
-              if (EPI == 1) {
-                const float u = j ? v[MATS - 1].y : v[MATS - 1].x;
-                o16 = (h16)(hn_silu((float)(h16)g) * (float)(h16)u);
-              } else {
-                o16 = (h16)g;
+          for (int h = 0; h < TH; ++h)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const int m = 8 * h + 2 * q + j;
+              if (m < Mc) {
+                const float g = j ? v[h][0].y : v[h][0].x;
+                h16 o16;
+                if (EPI == 1) {
+                  const float u = j ? v[h][MATS - 1].y : v[h][MATS - 1].x;
+                  o16 = (h16)(hn_silu((float)(h16)g) * (float)(h16)u);
+                } else {
+                  o16 = (h16)g;
+                }
+                st_pr.out[(long)(sg.m0 + m) * A.ld_o + row] = o16;
               }
-              st_pr.out[(long)(sg.m0 + m) * A.ld_o + row] = o16;
             }
-          }
         }
       }
       parity ^= 1;
@@ -480,19 +515,28 @@ struct StreamPlan {
   bool ok;
   bool wide;  // vector scale loads (set by the caller after its alignment checks)
   int lpw, nbuf, kw, tc, ldx, npair;
+  int th;     // token halves of 8 per chunk (2: up to 16 tokens per pass)
   int lds;  // dynamic LDS bytes per workgroup
   int occ;  // workgroups per CU
 };
 
 // One workgroup per CU of KW <= 8 waves; LPW (2..16) groups of 128 k per wave
 // per column, the smallest that covers K with 8 waves; three column buffers
-// when they fit the register budget, else two.  tc <= 8 tokens per chunk,
-// limited by the LDS left after the corrections and the reduction buffers.
+// when they fit the register budget, else two.  tc tokens per chunk: up to 8,
+// or up to 16 (two token halves per weight operand) when want16 and an
+// instantiation exists, limited by the LDS left after the corrections and the
+// reduction buffers.
 // LDS scratch of the routing prologue (ROUTE), in front of the metadata:
 // 16 slice partials of 16 x 16 logits, the logits, the selection.
 constexpr int kRouteScratch = 16 * 16 * 16 * 4 + 256 * 4 + 64 * 4 + 64 * 2 + 16;
 
-StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = false) {
+// Shapes with a 16-token instantiation (launch_lpw): four groups per wave
+// (grouped gate/up and the down K slices, one expert's gate/up).  Sixteen
+// groups per wave (one expert's 14336-long down projection) would spill.
+bool th2_instantiated(bool /*grouped*/, int /*mats*/, int lpw) { return lpw == 4; }
+
+StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = false,
+                       bool want16 = false, bool grouped = true) {
   StreamPlan p{};
   const long G = K / 128;
   int lpw = 2;
@@ -504,36 +548,47 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   p.kw = (int)kw;
   p.npair = (int)(kw * lpw / 2);
   p.ldx = p.npair * 128 + 8;  // row stride = 16 B mod 256 B: conflict-free A reads
-  const int red = 2 * (kMaxWaves - 1) * mats * 64 * 8;
-  const int cs = p.npair * 16 * 4;
-  const int per_tok = 2 * p.ldx * 2;
-  const int want = (int)(rows < kMaxTc ? rows : kMaxTc);
   // grouped metadata copy: active [E], offsets [E + 1] (each padded to even), pointers [E][4]
   // (ROUTE: and the permuted-row map, 64 entries)
   const int meta = (int)(((E + 1) & ~1L) * 4 + ((E + 2) & ~1L) * 4 + E * 32) + (route ? 256 : 0);
-  const int tcmax = (kLdsPerCu - kStaticLds - red - cs - meta) / per_tok;
-  p.tc = tcmax < want ? tcmax : want;
-  if (p.tc < 1) return p;
-  p.lds = p.tc * per_tok + cs + red + meta;
-  if (route && p.tc * per_tok + cs + red < kRouteScratch) return p;
-  // single-matrix (down) launches of 4 or more rows per matrix: two
-  // workgroups per CU when their LDS and waves fit, for more loads in flight
-  // where a column has little work (measured: gate/up launches and 1-row
-  // launches are faster with one)
-  p.occ = (mats == 1 && !route && rows >= 4 && 2 * (p.lds + kStaticLds) <= kLdsPerCu &&
-           2 * kw <= 16) ? 2 : 1;
-  p.ok = true;
+  const int cs = p.npair * kCsw * 4;
+  const int per_tok = 2 * p.ldx * 2;
+  for (int th = (want16 && !route && rows > 8 && th2_instantiated(grouped, mats, lpw)) ? 2 : 1;
+       th >= 1; --th) {
+    const int nrb = (th == 2 && mats == 2) ? 1 : 2;  // the kernel's reduction buffers
+    const int red = nrb * (kMaxWaves - 1) * th * mats * 64 * 8;
+    const int want = (int)(rows < 8 * th ? rows : 8 * th);
+    const int tcmax = (kLdsPerCu - kStaticLds - red - cs - meta) / per_tok;
+    const int tc = tcmax < want ? tcmax : want;
+    if (th == 2 && tc <= 8) continue;  // no room for a second token half
+    p.th = th;
+    p.tc = tc;
+    if (p.tc < 1) return p;
+    p.lds = p.tc * per_tok + cs + red + meta;
+    if (route && p.tc * per_tok + cs + red < kRouteScratch) return p;
+    // single-matrix (down) launches of 4 or more rows per matrix: two
+    // workgroups per CU when their LDS and waves fit, for more loads in flight
+    // where a column has little work (measured: gate/up launches and 1-row
+    // launches are faster with one)
+    p.occ = (mats == 1 && !route && rows >= 4 && 2 * (p.lds + kStaticLds) <= kLdsPerCu &&
+             2 * kw <= 16) ? 2 : 1;
+    p.ok = true;
+    return p;
+  }
   return p;
 }
 
 int num_cus() { return hn_device_cus(); }
 
 template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS = 1,
-          bool ROUTE = false>
+          bool ROUTE = false, int TH = 1>
 int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
-  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS, ROUTE>;
-  static HnLdsAttr attr;  // per instantiation and device
-  std::atomic<int>& sa = attr.state[hn_current_device()];
+  if (p.th != TH) return HN_NOT_HANDLED;  // the plan was sized for the other chunking
+  auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS, ROUTE, TH>;
+  static HnPerDevice attr;  // per instantiation and device
+  static HnPerDevice fit;   // workgroups per CU the registers allow
+  const int dev = hn_current_device();
+  std::atomic<int>& sa = attr.state[dev];
   int st = sa.load(std::memory_order_relaxed);
   if (st == 0) {
     st = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -542,13 +597,33 @@ int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, h
     sa.store(st, std::memory_order_relaxed);
   }
   if (st != 1 && p.lds > 64 * 1024 - kStaticLds) return HN_NOT_HANDLED;
-  hipLaunchKernelGGL(kern, dim3(num_cus() * p.occ), dim3(p.kw * 64), (size_t)p.lds, s, A, g.table,
+  int occ = p.occ;
+  if (occ > 1) {
+    // the plan checked LDS and waves; the registers decide too (a kernel
+    // over 128 VGPRs holds three waves per SIMD: one 7-wave workgroup per CU)
+    std::atomic<int>& sf = fit.state[dev];
+    int n = sf.load(std::memory_order_relaxed);
+    if (n == 0) {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)kern, p.kw * 64, 0) !=
+              hipSuccess || n < 1) {
+        (void)hipGetLastError();
+        n = 1;
+      }
+      sf.store(n, std::memory_order_relaxed);
+    }
+    occ = occ < n ? occ : n;
+  }
+  hipLaunchKernelGGL(kern, dim3(num_cus() * occ), dim3(p.kw * 64), (size_t)p.lds, s, A, g.table,
                      g.active, g.n_active, g.offsets);
   return 0;
 }
 
 template <bool GROUPED, int MATS, int EPI, bool WIDE>
 int launch_lpw(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
+  if (p.th == 2) {  // the shapes th2_instantiated() names
+    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 2, WIDE, 1, false, 2>(A, g, p, s);
+    return HN_NOT_HANDLED;
+  }
   if constexpr (MATS == 2) {
     if (p.lpw == 2) return launch_one<GROUPED, MATS, EPI, 2, 3, WIDE>(A, g, p, s);
     // one expert's gate/up (a few columns per workgroup): two columns in
@@ -577,6 +652,11 @@ int launch_stream(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p
 // groups, 7 waves x 4 groups with three column buffers.
 constexpr int kDownSplit = 4;
 
+// 16-token chunks for a grouped launch when its rows average 5 or more per
+// expert (e.g. 64 decode tokens at top-1 over 8 experts): an expert's rows
+// then mostly exceed 8, and one pass over its weights replaces two.
+bool want16_grouped(long rows, long E) { return E > 0 && rows >= 5 * E; }
+
 // Vector scale loads need the wave's LPW groups inside the scale row and
 // 16-byte aligned scale rows.
 bool wide_scales_ok(const StreamPlan& p, long K, long ld_s) {
@@ -604,7 +684,7 @@ extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const v
                                      const void* s0, const void* q1, const void* s1, long ld_q,
                                      long ld_s, void* out, long ld_o, long M, long N, long K,
                                      long group, void* stream) {
-  const StreamPlan p = stream_plan(K, mats, M);
+  const StreamPlan p = stream_plan(K, mats, M, 0, false, true, false);
   if (!p.ok || group != 128 || M > p.tc) return HN_NOT_HANDLED;
   if (mats == 2 && p.lpw > 8) return HN_NOT_HANDLED;
   if (N * ld_q >= (long)kOOB || N * ld_s * 2 >= (long)kOOB || ld_x >= (1L << 31) ||
@@ -637,12 +717,12 @@ extern "C" int hn_stream_linear_impl(int mats, const void* x, long ld_x, const v
 // whether the shape is handled (0) or not (HN_NOT_HANDLED).
 extern "C" int hn_stream_grouped_impl(int phase, const void* x, long ld_x, const void* table,
                                       const int* active, const int* n_active, const int* offsets,
-                                      long E, long max_rows, long H, long I, long group, void* out,
-                                      long ld_o, void* stream, int dry_run) {
+                                      long E, long max_rows, long rows, long H, long I, long group,
+                                      void* out, long ld_o, void* stream, int dry_run) {
   const int mats = phase == 0 ? 2 : 1;
   const long K = phase == 0 ? H : I, N = phase == 0 ? I : H;
   if (E > kMaxActive) return HN_NOT_HANDLED;
-  const StreamPlan p = stream_plan(K, mats, max_rows, E);
+  const StreamPlan p = stream_plan(K, mats, max_rows, E, false, want16_grouped(rows, E));
   if (!p.ok || group != 128) return HN_NOT_HANDLED;
   if (mats == 2 && p.lpw > 8) return HN_NOT_HANDLED;
   if (N * (K / 2) >= (long)kOOB || N * (K / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
@@ -680,7 +760,7 @@ extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const
                                          int dry_run) {
   const long K = I / kDownSplit, N = H;
   if (I % (kDownSplit * 128) != 0 || group != 128 || E > kMaxActive) return HN_NOT_HANDLED;
-  const StreamPlan p = stream_plan(K, 1, max_rows, E);
+  const StreamPlan p = stream_plan(K, 1, max_rows, E, false, want16_grouped(rows_cap, E));
   if (!p.ok || p.lpw != 4 || !wide_scales_ok(p, K, I / group)) return HN_NOT_HANDLED;
   if (N * (I / 2) >= (long)kOOB || N * (I / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
   if (dry_run) return 0;
@@ -697,7 +777,9 @@ extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const
   StreamPlan pw = p;
   pw.wide = true;
   const GroupedPtrs g = {(const SExpert*)table, active, n_active, offsets};
-  const int rc = launch_one<true, 1, 0, 4, 3, true, kDownSplit>(A, g, pw, (hipStream_t)stream);
+  const int rc = pw.th == 2
+      ? launch_one<true, 1, 0, 4, 3, true, kDownSplit, false, 2>(A, g, pw, (hipStream_t)stream)
+      : launch_one<true, 1, 0, 4, 3, true, kDownSplit>(A, g, pw, (hipStream_t)stream);
   if (rc) return rc;
   HN_LAUNCH_CHECK("hn_stream_down_split");
   return 0;

@@ -13,7 +13,8 @@ constexpr int kTileN = 16;
 constexpr uint32_t kOOB = 0x7ffffff0u;
 constexpr int kMaxActive = 256;
 constexpr int kMaxWaves = 8;  // per workgroup, one workgroup per CU: 2 per SIMD
-constexpr int kMaxTc = 8;     // tokens per chunk (two MFMA rows each)
+constexpr int kMaxTc = 16;    // tokens per chunk (two MFMA rows each; 8 per MFMA)
+constexpr int kCsw = 2 * kMaxTc;  // corrections per group pair: (token, parity)
 
 struct SExpert {
   const uint8_t* gate_q; const h16* gate_s;
@@ -207,66 +208,100 @@ __device__ __forceinline__ half8_t unpack_biased(uint32_t w, const HnUnpackRegs&
   return __builtin_bit_cast(half8_t, r);
 }
 
-// Unpack + MFMA of one column for this wave.  acc_lo / acc_hi: D rows 4q + r
-// (token 2q + r/2, group parity r%2) of the lo / hi chains.
+// Unpack + MFMA of one column for this wave.  acc_lo / acc_hi[h]: D rows
+// 4q + r (token 8h + 2q + r/2, group parity r%2) of the lo / hi chains; TH
+// token halves of 8 share each unpacked weight operand.
 // FULL: every pair of the wave lies inside K (the common case): no per-pair
 // guard, so the pairs' loads from LDS and MFMA chains form one basic block
 // that the scheduler can interleave.  The arithmetic is the same either way.
-template <int MATS, int PAIRS, bool WIDE, bool FULL>
+template <int MATS, int PAIRS, bool WIDE, bool FULL, int TH>
 __device__ __forceinline__ void compute_pairs(const WBuf<MATS, PAIRS, WIDE>& b, const h16* xs,
                                               const float* cs, int ldx, int pb0, int gw,
-                                              int arow_i, int q, int sshift,
-                                              const HnUnpackRegs& ur, float4_t acc_lo[MATS],
-                                              float4_t acc_hi[MATS]) {
+                                              const int (&arow_i)[TH], int q, int sshift,
+                                              const HnUnpackRegs& ur, float4_t (&acc_lo)[TH][MATS],
+                                              float4_t (&acc_hi)[TH][MATS]) {
 #pragma unroll
-  for (int mt = 0; mt < MATS; ++mt) {
-    acc_lo[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    acc_hi[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int h = 0; h < TH; ++h)
+#pragma unroll
+    for (int mt = 0; mt < MATS; ++mt) {
+      acc_lo[h][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      acc_hi[h][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
   for (int pi = 0; pi < PAIRS; ++pi) {
     if (FULL || 2 * pi < gw) {  // uniform
-      const h16* arow = xs + arow_i * ldx + (pb0 + pi) * 128 + 32 * q;
-      half8_t a[4];
+      half8_t a[TH][4];
+      float4_t negc[TH];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) a[t] = *reinterpret_cast<const half8_t*>(arow + 8 * t);
-      const float4_t negc = *reinterpret_cast<const float4_t*>(cs + (pb0 + pi) * 16 + 4 * q);
+      for (int h = 0; h < TH; ++h) {
+        const h16* arow = xs + arow_i[h] * ldx + (pb0 + pi) * 128 + 32 * q;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[h][t] = *reinterpret_cast<const half8_t*>(arow + 8 * t);
+        negc[h] = *reinterpret_cast<const float4_t*>(cs + (pb0 + pi) * kCsw + 16 * h + 4 * q);
+      }
 #pragma unroll
       for (int mt = 0; mt < MATS; ++mt) {
-        float4_t cl = negc, ch = negc;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], unpack_biased(b.lo[mt][pi][t], ur),
-                                                      cl, 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], unpack_biased(b.hi[mt][pi][t], ur),
-                                                      ch, 0, 0, 0);
         // WIDE: the lane's group parity picks the half of the pair's dword
         const int sft = WIDE ? sshift : 0;
-        const float sl = (float)__builtin_bit_cast(h16, (uint16_t)(b.slo[mt][pi] >> sft));
-        const float sh = (float)__builtin_bit_cast(h16, (uint16_t)(b.shi[mt][pi] >> sft));
+        if constexpr (TH == 1) {
+          float4_t cl = negc[0], ch = negc[0];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          acc_lo[mt][r] = __builtin_fmaf(sl, cl[r], acc_lo[mt][r]);
-          acc_hi[mt][r] = __builtin_fmaf(sh, ch[r], acc_hi[mt][r]);
+          for (int t = 0; t < 4; ++t)
+            cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][t], unpack_biased(b.lo[mt][pi][t], ur),
+                                                        cl, 0, 0, 0);
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][t], unpack_biased(b.hi[mt][pi][t], ur),
+                                                        ch, 0, 0, 0);
+          const float sl = (float)__builtin_bit_cast(h16, (uint16_t)(b.slo[mt][pi] >> sft));
+          const float sh = (float)__builtin_bit_cast(h16, (uint16_t)(b.shi[mt][pi] >> sft));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc_lo[0][mt][r] = __builtin_fmaf(sl, cl[r], acc_lo[0][mt][r]);
+            acc_hi[0][mt][r] = __builtin_fmaf(sh, ch[r], acc_hi[0][mt][r]);
+          }
+        } else {
+          const float sl = (float)__builtin_bit_cast(h16, (uint16_t)(b.slo[mt][pi] >> sft));
+          const float sh = (float)__builtin_bit_cast(h16, (uint16_t)(b.shi[mt][pi] >> sft));
+          half8_t wl[4], wh[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            wl[t] = unpack_biased(b.lo[mt][pi][t], ur);
+            wh[t] = unpack_biased(b.hi[mt][pi][t], ur);
+          }
+#pragma unroll
+          for (int h = 0; h < TH; ++h) {
+            float4_t cl = negc[h], ch = negc[h];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h][t], wl[t], cl, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h][t], wh[t], ch, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              acc_lo[h][mt][r] = __builtin_fmaf(sl, cl[r], acc_lo[h][mt][r]);
+              acc_hi[h][mt][r] = __builtin_fmaf(sh, ch[r], acc_hi[h][mt][r]);
+            }
+          }
         }
       }
     }
   }
 }
 
-template <int MATS, int PAIRS, bool WIDE>
+template <int MATS, int PAIRS, bool WIDE, int TH>
 __device__ __forceinline__ void compute(const WBuf<MATS, PAIRS, WIDE>& b, const h16* xs,
-                                        const float* cs, int ldx, int pb0, int gw, int arow_i,
-                                        int q, int sshift, const HnUnpackRegs& ur,
-                                        float4_t acc_lo[MATS], float4_t acc_hi[MATS]) {
+                                        const float* cs, int ldx, int pb0, int gw,
+                                        const int (&arow_i)[TH], int q, int sshift,
+                                        const HnUnpackRegs& ur, float4_t (&acc_lo)[TH][MATS],
+                                        float4_t (&acc_hi)[TH][MATS]) {
   if (gw >= 2 * PAIRS)  // uniform
-    compute_pairs<MATS, PAIRS, WIDE, true>(b, xs, cs, ldx, pb0, gw, arow_i, q, sshift, ur, acc_lo,
-                                           acc_hi);
+    compute_pairs<MATS, PAIRS, WIDE, true, TH>(b, xs, cs, ldx, pb0, gw, arow_i, q, sshift, ur,
+                                               acc_lo, acc_hi);
   else
-    compute_pairs<MATS, PAIRS, WIDE, false>(b, xs, cs, ldx, pb0, gw, arow_i, q, sshift, ur,
-                                            acc_lo, acc_hi);
+    compute_pairs<MATS, PAIRS, WIDE, false, TH>(b, xs, cs, ldx, pb0, gw, arow_i, q, sshift, ur,
+                                                acc_lo, acc_hi);
 }
 
 __device__ __forceinline__ float xor8(float v) {  // lane col ^ 8 of the same 16-lane row
@@ -303,8 +338,8 @@ __device__ __forceinline__ void stage_load(const StreamArgs& A, const h16* x,
 // Also the bias corrections: the 16 blocks of one (token, group) sit in 16
 // consecutive lanes (block index = base + tid + j * nthr, blk_per_tok a
 // multiple of 16), so each lane's 8-term dot product is summed across its
-// 16-lane DPP row and the row's first lane writes cs[pair * 16 + 2 t + parity]
-// = -C.  Lanes whose block is a repeat of the last one (past the chunk) skip
+// 16-lane DPP row and the row's first lane writes cs[pair * kCsw + 2 t +
+// parity] = -C.  Lanes whose block is a repeat of the last one (past the chunk) skip
 // the write; so does the whole row, as the chunk ends on a group boundary.
 __device__ __forceinline__ void stage_store(const StreamArgs& A, const StageGeom& sg, int base,
                                             const half8_t v[4], h16* xs, float* cs) {
@@ -334,15 +369,15 @@ __device__ __forceinline__ void stage_store(const StreamArgs& A, const StageGeom
     c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x124, 0xf, 0xf, false));
     c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x122, 0xf, 0xf, false));
     c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x121, 0xf, 0xf, false));
-    if ((tid & 15) == 0 && ir < sg.nblk) cs[(g >> 1) * 16 + 2 * t + (g & 1)] = -c;
+    if ((tid & 15) == 0 && ir < sg.nblk) cs[(g >> 1) * kCsw + 2 * t + (g & 1)] = -c;
   }
 }
 
 // Corrections of MFMA rows past the chunk's tokens are zero (their outputs
 // are never stored; the rows read a clamped token).
 __device__ __forceinline__ void stage_zero_rows(const StreamArgs& A, int Mc, float* cs) {
-  for (int i = threadIdx.x; i < A.npair * 16; i += blockDim.x)
-    if (((i & 15) >> 1) >= Mc) cs[i] = 0.f;
+  for (int i = threadIdx.x; i < A.npair * kCsw; i += blockDim.x)
+    if (((i % kCsw) >> 1) >= Mc) cs[i] = 0.f;
 }
 
 // Whole staging of one chunk (used when the staged chunk changes mid-stream).

@@ -95,7 +95,9 @@ def test_quantize_bit_exact_random_large():
                                      (4, 1408, 4096, 128), (16, 272, 1024, 128),
                                      (17, 96, 384, 128), (33, 48, 256, 128), (3, 64, 256, 64),
                                      (5, 48, 256, 32), (1, 4096, 1408, 128), (8, 32, 160, 32),
-                                     (2, 40, 384, 128), (7, 24, 128, 128)])
+                                     (2, 40, 384, 128), (7, 24, 128, 128),
+                                     (12, 336, 4096, 128), (16, 64, 4096, 128),
+                                     (9, 48, 3584, 128)])
 def test_int4_linear_vs_oracle(M, N, K, g, decode_path):
     from hydranet_amd.kernels.int4_gemm import int4_linear
     w = _rand_f16(M * 7 + N, (N, K), 0.02)
@@ -162,7 +164,8 @@ def _expert(seed, H, I, g=128):
 
 @pytest.mark.parametrize("T,H,I", [(1, 4096, 14336), (2, 4096, 14336), (4, 4096, 14336),
                                    (4, 4096, 1408), (16, 512, 1024),
-                                   (3, 256, 384), (5, 4096, 14336)])
+                                   (3, 256, 384), (5, 4096, 14336), (12, 4096, 1408),
+                                   (16, 4096, 14336)])
 def test_expert_mlp_vs_torch_ref(T, H, I, decode_path):
     from hydranet_amd.kernels import expert_mlp_int4_fused
     from hydranet_amd.kernels.int4_expert_mlp import expert_mlp_int4_from_slot
