@@ -278,7 +278,7 @@ def time_decode_phases(layers, x, T, H, I, g, E, reps: int = 12):
 
     def route_gate_up(li):
         r, tb = rts[li], layers[li].experts.table
-        _lib.call("hn_moe_route_gate_up", _lib.ptr(xx), H, _lib.ptr(gates[li]), H, T, E, k,
+        _lib.call("hn_moe_route_gate_up", _lib.ptr(xx), H, _lib.ptr(gates[li]), H, None, T, E, k,
                   _lib.ptr(tb.dev), H, I, g, 1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w),
                   _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active),
                   _lib.ptr(r.n_active), _lib.ptr(h_ws), sp)
@@ -651,7 +651,7 @@ def c2phase(args):
     n = T * k
     h_ws = torch.empty(n, I, dtype=torch.float16, device="cuda")
     for _ in range(20):
-        _lib.call("hn_moe_route_gate_up", _lib.ptr(x), H, _lib.ptr(gate), H, T, E, k,
+        _lib.call("hn_moe_route_gate_up", _lib.ptr(x), H, _lib.ptr(gate), H, None, T, E, k,
                   _lib.ptr(table.dev), H, I, g, 1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w),
                   _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active),
                   _lib.ptr(r.n_active), _lib.ptr(h_ws), _lib.stream())

@@ -589,8 +589,8 @@ extern "C" int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, c
                                 void* out, long ld_o, long H, void* stream);
 // Unpermute (hn_route.hip) from the four fp32 slices of the split down projection.
 extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const void* gate,
-                                            long ld_gate, long T, long E, long k,
-                                            const void* table, long H, long I, long group,
+                                            long ld_gate, const float* logits_in, long T, long E,
+                                            long k, const void* table, long H, long I, long group,
                                             float eps, float scaling, float* logits_out,
                                             int* idx, void* w, int* offsets, int* perm,
                                             int* inv, int* active, int* n_active, void* h_ws,
@@ -942,72 +942,80 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
 // The first launch of hn_moe_decode_layer on its own: routing computed in the
 // grouped gate/up streaming kernel, h_ws = SwiGLU gate/up of the routed rows.
 extern "C" int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w, long ld_w,
-                                    long T, long E, long k, const void* table, long H, long I,
-                                    long group, float eps, float scaling, void* logits_out,
-                                    int* idx, void* w, int* offsets, int* perm, int* inv,
-                                    int* active, int* n_active, void* h_ws, void* stream) {
+                                    const float* logits_in, long T, long E, long k,
+                                    const void* table, long H, long I, long group, float eps,
+                                    float scaling, void* logits_out, int* idx, void* w,
+                                    int* offsets, int* perm, int* inv, int* active,
+                                    int* n_active, void* h_ws, void* stream) {
   const char* who = "hn_moe_route_gate_up";
-  HN_ARG_CHECK(aligned16(h) && aligned16(gate_w) && aligned16(h_ws),
+  HN_ARG_CHECK(aligned16(h) && (logits_in || aligned16(gate_w)) && aligned16(h_ws),
                "%s: h, gate and h_ws rows must be 16-byte aligned", who);
   HN_ARG_CHECK(g_decode_path == 0, "%s: needs the streaming kernels (decode path 0)", who);
-  const int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, T, E, k, table, H, I, group,
-                                              eps, scaling, (float*)logits_out, idx, w, offsets,
-                                              perm, inv, active, n_active, h_ws,
+  const int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, logits_in, T, E, k, table,
+                                              H, I, group, eps, scaling, (float*)logits_out, idx,
+                                              w, offsets, perm, inv, active, n_active, h_ws,
                                               (hipStream_t)stream, 0);
-  HN_ARG_CHECK(rc != HN_NOT_HANDLED, "%s: shape not covered (T <= 16, E <= 8, k == 2, H %% 512 "
-               "== 0, group 128; T=%ld E=%ld k=%ld H=%ld group=%ld)", who, T, E, k, H, group);
+  HN_ARG_CHECK(rc != HN_NOT_HANDLED, "%s: shape not covered (E <= 8, k 1 or 2, T k <= 64, T <= "
+               "16 without logits_in, H %% 512 == 0, group 128; T=%ld E=%ld k=%ld H=%ld "
+               "group=%ld)", who, T, E, k, H, group);
   return rc;
 }
 
 // 0 when hn_moe_decode_layer covers the shape (decode path 0 included),
-// otherwise HN_NOT_HANDLED; sets no error.
-extern "C" int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group) {
+// otherwise HN_NOT_HANDLED; sets no error.  has_logits: the caller passes
+// logits_in.
+extern "C" int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group,
+                                         int has_logits) {
   if (g_decode_path != 0) return HN_NOT_HANDLED;
-  // dry runs: shapes only (no pointer is read)
-  const int a = hn_stream_route_gate_up_impl(nullptr, H, nullptr, H, T, E, k, nullptr, H, I,
-                                             group, 0.f, 1.f, nullptr, nullptr, nullptr, nullptr,
+  // dry runs: shapes only (no pointer is read; a non-null logits_in stands
+  // for the caller's)
+  static const float dummy = 0.f;
+  const int a = hn_stream_route_gate_up_impl(nullptr, H, nullptr, H, has_logits ? &dummy : nullptr,
+                                             T, E, k, nullptr, H, I, group, 0.f, 1.f, nullptr,
                                              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                             1);
+                                             nullptr, nullptr, nullptr, 1);
   const int b = hn_stream_down_split_impl(nullptr, nullptr, nullptr, nullptr, nullptr, E, T,
                                           T * k, H, I, group, nullptr, nullptr, 1);
   return a == 0 && b == 0 ? 0 : HN_NOT_HANDLED;
 }
 
-// One Mixtral MoE layer at decode in three launches: the routing (logits,
-// softmax top-2, permutation) computed inside the gate/up streaming kernel,
-// the down projection in four K slices, the ordered weighted unpermute.
-// Same results as hn_moe_route followed by hn_moe_experts_decode.
+// One Mixtral MoE layer at decode in three launches: the routing (logits
+// unless given, softmax top-k, permutation) computed inside the gate/up
+// streaming kernel, the down projection in four K slices, the ordered
+// weighted unpermute.  Same results as hn_moe_route followed by
+// hn_moe_experts_decode.
 extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
-                                   long T, long E, long k, const void* table, long H, long I,
-                                   long group, float eps, float scaling, void* logits_out,
-                                   int* idx, void* w, int* offsets, int* perm, int* inv,
-                                   int* active, int* n_active, void* h_ws, void* out, long ld_o,
-                                   void* work, long work_bytes, void* stream) {
+                                   const float* logits_in, long T, long E, long k,
+                                   const void* table, long H, long I, long group, float eps,
+                                   float scaling, void* logits_out, int* idx, void* w,
+                                   int* offsets, int* perm, int* inv, int* active, int* n_active,
+                                   void* h_ws, void* out, long ld_o, void* work, long work_bytes,
+                                   void* stream) {
   const char* who = "hn_moe_decode_layer";
-  HN_ARG_CHECK(aligned16(h) && aligned16(gate_w) && aligned16(h_ws) && aligned16(out) &&
-                   ld_o % 8 == 0,
+  HN_ARG_CHECK(aligned16(h) && (logits_in || aligned16(gate_w)) && aligned16(h_ws) &&
+                   aligned16(out) && ld_o % 8 == 0,
                "%s: h, gate, h_ws and out rows must be 16-byte aligned", who);
   HN_ARG_CHECK(g_decode_path == 0, "%s: needs the streaming kernels (decode path 0)", who);
   hipStream_t s = (hipStream_t)stream;
   const long rows = T * k;
   const bool ok =
-      hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, T, E, k, table, H, I, group, eps,
-                                   scaling, (float*)logits_out, idx, w, offsets, perm, inv,
+      hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, logits_in, T, E, k, table, H, I, group,
+                                   eps, scaling, (float*)logits_out, idx, w, offsets, perm, inv,
                                    active, n_active, h_ws, s, 1) == 0 &&
       hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H, I, group,
                                 nullptr, s, 1) == 0;
-  HN_ARG_CHECK(ok, "%s: shape not covered (T <= 16, E <= 8, k == 2, H %% 512 == 0, I %% 512 "
-               "== 0, group 128; T=%ld E=%ld k=%ld H=%ld I=%ld group=%ld)", who, T, E, k, H, I,
-               group);
+  HN_ARG_CHECK(ok, "%s: shape not covered (E <= 8, k 1 or 2, T k <= 64, T <= 16 without "
+               "logits_in, H %% 512 == 0, I %% 512 == 0, group 128; T=%ld E=%ld k=%ld H=%ld "
+               "I=%ld group=%ld)", who, T, E, k, H, I, group);
   const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
                                                             : hn_cdiv(H, kTileN);
   const long need = hn_skinny_workspace_bytes(3, rows, H, I, E);
   HN_ARG_CHECK(work && work_bytes >= need, "%s: workspace too small (%ld < %ld)", who,
                work_bytes, need);
   float* part = (float*)((char*)work + ctr_bytes(E * tmax));
-  int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, T, E, k, table, H, I, group, eps,
-                                        scaling, (float*)logits_out, idx, w, offsets, perm, inv,
-                                        active, n_active, h_ws, s, 0);
+  int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, logits_in, T, E, k, table, H, I,
+                                        group, eps, scaling, (float*)logits_out, idx, w, offsets,
+                                        perm, inv, active, n_active, h_ws, s, 0);
   if (rc == 0)
     rc = hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H, I,
                                    group, part, s, 0);

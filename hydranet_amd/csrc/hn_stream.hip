@@ -48,25 +48,29 @@
 
 namespace {
 // Decode routing in the gate/up kernel's prologue (ROUTE): Mixtral softmax
-// top-2 of E <= 8 experts over T <= 16 tokens, fp16 gate.  The arithmetic is
-// moe_route_kernel's (hn_route.hip): logits by MFMA over 16 slices of H, the
-// slice partials summed in slice order and rounded to fp16 (the fp16 Linear
-// of TopKRouter, model/router.py:102); top-k and weights by topk_small; the
-// stable order by expert from ballots (torch.where order, model/mixtral.py:
-// 333).  Every workgroup computes it into LDS (part: 16 KiB scratch, reused by
-// the staging afterwards); workgroup 0 also writes the routing outputs.
+// top-k (k = 1 or 2) of E <= 8 experts over T tokens, T k <= 64.  The
+// arithmetic is moe_route_kernel's (hn_route.hip): logits (T <= 16, fp16
+// gate) by MFMA over 16 slices of H, the slice partials summed in slice order
+// and rounded to fp16 (the fp16 Linear of TopKRouter, model/router.py:102),
+// or read from logits_in; top-k and weights by topk_small; the stable order
+// by expert from ballots (torch.where order, model/mixtral.py:333).  Every
+// workgroup computes it into LDS (part: 16 KiB scratch, reused by the
+// staging afterwards); workgroup 0 also writes the routing outputs.
 // Returns the number of active experts (uniform).
 __device__ int route_prologue(const StreamArgs& A, float* part, int* s_act, int* s_off,
                               int* rperm, int wave, int lane) {
   const int tid = threadIdx.x, KW = blockDim.x >> 6;
   const int T = A.T, E = A.E, H = A.K, k = A.topk, n = T * k;
   const bool lead = blockIdx.x == 0;
-  float* s_lg = part + 16 * 16 * 16;           // [T * E]
-  int* s_sel = reinterpret_cast<int*>(s_lg + 16 * 16);
+  float* s_lg = part + 16 * 16 * 16;           // [T * E] <= 512
+  int* s_sel = reinterpret_cast<int*>(s_lg + 512);
   h16* s_w = reinterpret_cast<h16*>(s_sel + 64);
   int* s_na = reinterpret_cast<int*>(s_w + 64);
-  // 1. logits: slice sl of H/16 by wave sl % KW; lane (expert tl, tokens 4 (lane >> 4) + r)
-  {
+  // 1. logits: given, or slice sl of H/16 by wave sl % KW; lane (expert tl,
+  //    tokens 4 (lane >> 4) + r)
+  if (A.logits_in) {
+    for (int i = tid; i < T * E; i += blockDim.x) s_lg[i] = A.logits_in[i];
+  } else {
     const int ksl = H >> 4, steps = ksl >> 5;
     const int tl = lane & 15, kq = (lane >> 4) * 8;
     const h16* ap = A.hx + (long)min(tl, T - 1) * A.ld_hx + kq;
@@ -105,21 +109,26 @@ __device__ int route_prologue(const StreamArgs& A, float* part, int* s_act, int*
         if (has1) part[(sl1 * 16 + 4 * (lane >> 4) + r) * 16 + tl] = acc1[r];
       }
     }
-  }
-  __syncthreads();
-  for (int i = tid; i < T * E; i += blockDim.x) {
-    const int t = i / E, e = i - t * E;
-    float v = 0.f;
+    __syncthreads();
+    for (int i = tid; i < T * E; i += blockDim.x) {
+      const int t = i / E, e = i - t * E;
+      float v = 0.f;
 #pragma unroll
-    for (int sl = 0; sl < 16; ++sl) v += part[(sl * 16 + t) * 16 + e];
-    s_lg[i] = (float)(h16)v;
-    if (lead && A.logits_out) A.logits_out[i] = s_lg[i];
+      for (int sl = 0; sl < 16; ++sl) v += part[(sl * 16 + t) * 16 + e];
+      s_lg[i] = (float)(h16)v;
+    }
   }
   __syncthreads();
-  // 2. top-2 and weights, one thread per token
-  for (int t = tid; t < T; t += blockDim.x)
-    topk_small<8, 2, 0>(s_lg + t * E, nullptr, E, 2, 0, A.eps, A.scaling, s_sel + t * 2,
-                        s_w + t * 2);
+  if (lead && A.logits_out)
+    for (int i = tid; i < T * E; i += blockDim.x) A.logits_out[i] = s_lg[i];
+  // 2. top-k and weights, one thread per token
+  for (int t = tid; t < T; t += blockDim.x) {
+    if (k == 2)
+      topk_small<8, 2, 0>(s_lg + t * E, nullptr, E, 2, 0, A.eps, A.scaling, s_sel + t * 2,
+                          s_w + t * 2);
+    else
+      topk_small<8, 1, 0>(s_lg + t * E, nullptr, E, 1, 0, A.eps, A.scaling, s_sel + t, s_w + t);
+  }
   __syncthreads();
   // 3. stable order by expert (n <= 64: wave 0, one lane per assignment).
   //    Rank among equal experts from ballots over the bits of e (E <= 8:
@@ -200,7 +209,6 @@ __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void 
   constexpr int PAIRS = LPW / 2;
   static_assert(NBUF == 2 || NBUF == 3, "two or three column buffers");
   static_assert(TH == 1 || TH == 2, "8 or 16 tokens per chunk");
-  static_assert(!(ROUTE && TH == 2), "the routing prologue takes 8-token chunks");
   // reduction buffers: parity-double-buffered (one barrier per column) unless
   // that no longer fits beside 16 tokens of gate/up activations; then one
   // buffer and a second barrier per column
@@ -527,8 +535,8 @@ struct StreamPlan {
 // instantiation exists, limited by the LDS left after the corrections and the
 // reduction buffers.
 // LDS scratch of the routing prologue (ROUTE), in front of the metadata:
-// 16 slice partials of 16 x 16 logits, the logits, the selection.
-constexpr int kRouteScratch = 16 * 16 * 16 * 4 + 256 * 4 + 64 * 4 + 64 * 2 + 16;
+// 16 slice partials of 16 x 16 logits, the logits (T E <= 512), the selection.
+constexpr int kRouteScratch = 16 * 16 * 16 * 4 + 512 * 4 + 64 * 4 + 64 * 2 + 16;
 
 // Shapes with a 16-token instantiation (launch_lpw): four groups per wave
 // (grouped gate/up and the down K slices, one expert's gate/up).  Sixteen
@@ -553,7 +561,7 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   const int meta = (int)(((E + 1) & ~1L) * 4 + ((E + 2) & ~1L) * 4 + E * 32) + (route ? 256 : 0);
   const int cs = p.npair * kCsw * 4;
   const int per_tok = 2 * p.ldx * 2;
-  for (int th = (want16 && !route && rows > 8 && th2_instantiated(grouped, mats, lpw)) ? 2 : 1;
+  for (int th = (want16 && rows > 8 && th2_instantiated(grouped, mats, lpw)) ? 2 : 1;
        th >= 1; --th) {
     const int nrb = (th == 2 && mats == 2) ? 1 : 2;  // the kernel's reduction buffers
     const int red = nrb * (kMaxWaves - 1) * th * mats * 64 * 8;
@@ -785,24 +793,26 @@ extern "C" int hn_stream_down_split_impl(const void* h, const void* table, const
   return 0;
 }
 
-// Decode routing fused into the grouped gate/up launch: Mixtral softmax top-2
-// over E <= 8 experts, T <= 16 tokens, fp16 gate [E, H] (the arithmetic of
-// hn_moe_route), then h_ws = SwiGLU gate/up of the routed rows, staged from
-// hx directly (no x_perm).  Workgroup 0 writes logits_out (optional), idx, w,
+// Decode routing fused into the grouped gate/up launch: Mixtral softmax top-k
+// (k = 1 or 2, T k <= 64) over E <= 8 experts, logits from the fp16 gate
+// [E, H] (T <= 16; the arithmetic of hn_moe_route) or given in logits_in
+// [T, E], then h_ws = SwiGLU gate/up of the routed rows, staged from hx
+// directly (no x_perm).  Workgroup 0 writes logits_out (optional), idx, w,
 // offsets, perm, inv, active and n_active for the down projection and the
 // unpermute.  Returns HN_NOT_HANDLED when the shape is not covered.
 extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const void* gate,
-                                            long ld_gate, long T, long E, long k,
-                                            const void* table, long H, long I, long group,
+                                            long ld_gate, const float* logits_in, long T, long E,
+                                            long k, const void* table, long H, long I, long group,
                                             float eps, float scaling, float* logits_out,
                                             int* idx, void* w, int* offsets, int* perm,
                                             int* inv, int* active, int* n_active, void* h_ws,
                                             void* stream, int dry_run) {
-  if (T < 1 || T > 16 || E < 1 || E > 8 || k != 2 || H % 512 != 0 || group != 128 ||
-      I % 128 != 0 || ld_hx % 8 != 0 || ld_gate % 8 != 0 || ld_hx >= (1L << 31) ||
+  if (T < 1 || E < 1 || E > 8 || (k != 1 && k != 2) || T * k > 64 ||
+      (!logits_in && T > 16) || H % 512 != 0 || group != 128 || I % 128 != 0 ||
+      ld_hx % 8 != 0 || (!logits_in && ld_gate % 8 != 0) || ld_hx >= (1L << 31) ||
       ld_gate >= (1L << 31))
     return HN_NOT_HANDLED;
-  const StreamPlan p = stream_plan(H, 2, T, E, true);
+  const StreamPlan p = stream_plan(H, 2, T, E, true, want16_grouped(T * k, E));
   if (!p.ok || p.lpw > 8 || !wide_scales_ok(p, H, H / group)) return HN_NOT_HANDLED;
   if (I * (H / 2) >= (long)kOOB || I * (H / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
   if (dry_run) return 0;
@@ -822,6 +832,7 @@ extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const vo
   A.ld_hx = (int)ld_hx;
   A.gate = (const h16*)gate;
   A.ld_gate = (int)ld_gate;
+  A.logits_in = logits_in;
   A.T = (int)T;
   A.topk = (int)k;
   A.eps = eps;
@@ -837,7 +848,8 @@ extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const vo
   const GroupedPtrs g = {(const SExpert*)table, nullptr, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
   int rc = HN_NOT_HANDLED;
-  if (p.lpw == 2) rc = launch_one<true, 2, 1, 2, 3, true, 1, true>(A, g, pw, s);
+  if (p.th == 2) rc = launch_one<true, 2, 1, 4, 2, true, 1, true, 2>(A, g, pw, s);
+  else if (p.lpw == 2) rc = launch_one<true, 2, 1, 2, 3, true, 1, true>(A, g, pw, s);
   else if (p.lpw == 4) rc = launch_one<true, 2, 1, 4, 3, true, 1, true>(A, g, pw, s);
   else if (p.lpw == 8) rc = launch_one<true, 2, 1, 8, 2, true, 1, true>(A, g, pw, s);
   if (rc) return rc;

@@ -43,10 +43,12 @@ struct StreamArgs {
   float* out32;
   long ks_stride;
   // ROUTE (grouped gate/up only): the routing of hx computed in the kernel.
-  // hx [T, H] fp16 hidden rows, gate [E, H] fp16; the permuted rows are
-  // staged from hx directly; workgroup 0 writes the routing outputs.
+  // hx [T, H] fp16 hidden rows, gate [E, H] fp16 (or logits_in [T, E] fp32,
+  // the router logits computed elsewhere); the permuted rows are staged from
+  // hx directly; workgroup 0 writes the routing outputs.
   const h16* hx; int ld_hx;
   const h16* gate; int ld_gate;
+  const float* logits_in;
   int T, topk;
   float eps, scaling;
   float* logits_out;

@@ -125,22 +125,25 @@ def moe_route(hidden: torch.Tensor, k: int, mode: int, gate_w: Optional[torch.Te
     return r
 
 
-def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torch.Tensor) -> bool:
+def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torch.Tensor,
+                      has_logits: bool = False) -> bool:
     """Whether hn_moe_decode_layer (routing fused into the gate/up kernel)
-    covers this Mixtral layer call."""
+    covers this Mixtral layer call; has_logits: the router logits are given
+    (then up to 64 routed rows, else up to 16 tokens)."""
     H, I, g = table.dims
     if table.num_experts != E or tuple(gate_w.shape) != (E, H):
         return False
-    return _lib.lib().hn_moe_decode_layer_check(T, E, k, H, I, g) == 0
+    return _lib.lib().hn_moe_decode_layer_check(T, E, k, H, I, g, int(has_logits)) == 0
 
 
 def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: "ExpertTable",
-                     want_logits: bool = False):
+                     want_logits: bool = False, logits: Optional[torch.Tensor] = None):
     """One Mixtral MoE layer at decode in three launches (hn_moe_decode_layer):
-    fp16 gate logits, softmax top-k and the stable permutation computed in the
-    gate/up kernel, the down projection, the ordered weighted unpermute.
-    Returns (out [T, H] fp16, Routed) with the same routing outputs as
-    moe_route (x_perm is not written)."""
+    softmax top-k and the stable permutation computed in the gate/up kernel
+    (with the fp16 gate logits, unless ``logits`` [T, E] are given), the down
+    projection, the ordered weighted unpermute.  Returns (out [T, H] fp16,
+    Routed) with the same routing outputs as moe_route (x_perm is not
+    written)."""
     T, H = hidden.shape
     _lib.require_gpu(hidden)
     dev = hidden.device
@@ -150,14 +153,20 @@ def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: 
     x = _lib.aligned_rows(hidden.to(torch.float16))
     ww = _lib.aligned_rows(gate_w.to(torch.float16))
     r = Routed(T, k, E, 0, dev)
-    if want_logits:
+    lg_in = None
+    if logits is not None:
+        assert tuple(logits.shape) == (T, E), f"logits {tuple(logits.shape)} vs ({T}, {E})"
+        lg_in = logits.to(torch.float32).contiguous()
+        r.logits = lg_in
+    elif want_logits:
         r.logits = torch.empty((T, E), dtype=torch.float32, device=dev)
     n = T * k
     h_ws = torch.empty((n, I), dtype=torch.float16, device=dev)
     out = torch.empty((T, H), dtype=torch.float16, device=dev)
     work = _lib.skinny_workspace(3, n, H, I, E, dev)
-    _lib.call("hn_moe_decode_layer", _lib.ptr(x), x.stride(0), _lib.ptr(ww), ww.stride(0), T, E,
-              k, _lib.ptr(table.dev), H, I, g, 1e-9, 1.0, _lib.ptr(r.logits), _lib.ptr(r.idx),
+    _lib.call("hn_moe_decode_layer", _lib.ptr(x), x.stride(0), _lib.ptr(ww), ww.stride(0),
+              _lib.ptr(lg_in), T, E, k, _lib.ptr(table.dev), H, I, g, 1e-9, 1.0,
+              _lib.ptr(r.logits if lg_in is None else None), _lib.ptr(r.idx),
               _lib.ptr(r.w), _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv),
               _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(h_ws), _lib.ptr(out), H,
               _lib.ptr(work), work.numel(), _lib.stream(dev))
@@ -332,19 +341,12 @@ class MixtralMoELayer(nn.Module):
         self.last_routing = None
 
     def takes_logits(self, T: int, top_k: int) -> bool:
-        """Whether a forward of T tokens routes through hn_moe_route, whose
-        gate product a caller can save by passing the router logits (e.g. from
-        hn_add_rmsnorm_router); False where the fused decode layer computes
-        them inside its gate/up kernel, or the batch is past the one-launch
-        routing."""
+        """Whether a forward of T tokens can take its router logits from the
+        caller (e.g. hn_add_rmsnorm_router), saving the gate product: the
+        one-launch routing and the decode layer with routing in its gate/up
+        kernel both take them; past those sizes the router runs alone."""
         E, gw = self.num_experts, self.router.gate.weight
-        if not route_fits(T, E, top_k) or E > 16 or not gw.is_cuda:
-            return False
-        rt = self.router
-        if rt.enable_affinity_bonus and rt._is_cached_fn is not None:
-            return True
-        table = self.experts.static_table(gw.device)
-        return not (table is not None and decode_layer_fits(T, E, top_k, table, gw))
+        return route_fits(T, E, top_k) and E <= 16 and gw.is_cuda
 
     def forward(self, hidden_states: torch.Tensor, top_k: int = 2,
                 logits: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -360,11 +362,11 @@ class MixtralMoELayer(nn.Module):
                 if logits is None:
                     logits = router_logits(flat, rt.gate.weight.to(torch.float16))
                 logits = rt._affinity(logits)
-            table = self.experts.static_table(flat.device) if logits is None else None
+            table = self.experts.static_table(flat.device)
             if table is not None and decode_layer_fits(T, self.num_experts, top_k, table,
-                                                       rt.gate.weight):
+                                                       rt.gate.weight, logits is not None):
                 # decode, resident experts: routing inside the gate/up kernel
-                out, r = moe_decode_layer(flat, rt.gate.weight, top_k, table)
+                out, r = moe_decode_layer(flat, rt.gate.weight, top_k, table, logits=logits)
             else:
                 # decode: routing, permutation and gather in one launch
                 r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits)

@@ -174,32 +174,38 @@ int hn_moe_experts_decode(const void* x_perm, const void* table, const int* acti
  * * fp16(x Wu^T)) for the routed rows (same arguments; for per-kernel timing
  * and counter runs).  Replaces TopKRouter.forward and the gate/up half of the
  * per-expert loop (model/router.py:96-120, model/mixtral.py:327-354). */
-int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w, long ld_w, long T, long E,
-                         long k, const void* table, long H, long I, long group, float eps,
-                         float scaling, void* logits_out, int* idx, void* w, int* offsets,
-                         int* perm, int* inv, int* active, int* n_active, void* h_ws,
-                         void* stream);
+int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w, long ld_w,
+                         const float* logits_in, long T, long E, long k, const void* table,
+                         long H, long I, long group, float eps, float scaling, void* logits_out,
+                         int* idx, void* w, int* offsets, int* perm, int* inv, int* active,
+                         int* n_active, void* h_ws, void* stream);
 
 /* 0 when hn_moe_decode_layer covers (T, E, k, H, I, group) with the current
- * decode kernel family, else a nonzero code (no error message is set). */
-int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group);
+ * decode kernel family, else a nonzero code (no error message is set).
+ * has_logits: whether the call will pass logits_in. */
+int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group,
+                              int has_logits);
 
-/* One Mixtral MoE layer at decode (T <= 16 tokens, E <= 8 experts, top-2
- * softmax, fp16 gate [E, H], group 128, H and I multiples of 512) in three
- * launches: the routing (logits, top-k, stable permutation) computed inside
- * the gate/up streaming kernel from h [T, H] directly (no x_perm), the down
- * projection in four K slices, the ordered weighted unpermute into out
- * [T, H].  Results equal hn_moe_route + hn_moe_experts_decode; the routing
- * outputs (logits_out may be NULL, idx, w, offsets [E + 1], perm, inv, active,
- * n_active) are written as hn_moe_route writes them.  h_ws [T k, I] fp16;
- * work: hn_skinny_workspace_bytes(3, T k, H, I, E).  Replaces
+/* One Mixtral MoE layer at decode (E <= 8 experts, softmax top-k with k 1 or
+ * 2 and T k <= 64, group 128, H and I multiples of 512) in three launches:
+ * the routing (top-k, stable permutation) computed inside the gate/up
+ * streaming kernel from h [T, H] directly (no x_perm), the down projection in
+ * four K slices, the ordered weighted unpermute into out [T, H].  The router
+ * logits are either computed there from the fp16 gate [E, H] (T <= 16) or
+ * given in logits_in [T, E] fp32 (fp16 values, e.g. from
+ * hn_add_rmsnorm_router; gate_w may then be NULL).  Results equal
+ * hn_moe_route + hn_moe_experts_decode; the routing outputs (logits_out may be
+ * NULL, idx, w, offsets [E + 1], perm, inv, active, n_active) are written as
+ * hn_moe_route writes them.  h_ws [T k, I] fp16; work:
+ * hn_skinny_workspace_bytes(3, T k, H, I, E).  Replaces
  * MixtralMoELayer.forward's router call, per-expert loop and index_add_
  * (model/mixtral.py:283-368) at decode sizes. */
-int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w, long T, long E,
-                        long k, const void* table, long H, long I, long group, float eps,
-                        float scaling, void* logits_out, int* idx, void* w, int* offsets,
-                        int* perm, int* inv, int* active, int* n_active, void* h_ws, void* out,
-                        long ld_o, void* work, long work_bytes, void* stream);
+int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
+                        const float* logits_in, long T, long E, long k, const void* table,
+                        long H, long I, long group, float eps, float scaling, void* logits_out,
+                        int* idx, void* w, int* offsets, int* perm, int* inv, int* active,
+                        int* n_active, void* h_ws, void* out, long ld_o, void* work,
+                        long work_bytes, void* stream);
 
 /* One phase of hn_moe_experts_decode's streaming path on its own (<= 16 rows per
  * expert, group 128): phase 0 reads x [rows, H] (sorted by expert) and writes

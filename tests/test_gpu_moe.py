@@ -472,6 +472,42 @@ def test_decode_layer_fused_routing_matches_route_then_experts(T, mixtral_expert
     assert torch.equal(out2, moe_dispatch(moe_route(x2, 2, 0, gate_w=gw), table))
 
 
+@pytest.mark.parametrize("T,k", [(1, 1), (4, 1), (16, 2), (20, 1), (32, 2), (64, 1)])
+def test_decode_layer_with_given_logits_matches_route_then_experts(T, k, mixtral_experts):
+    """hn_moe_decode_layer fed the router logits (as the decoder's norm kernel
+    gives them; up to 64 routed rows, top-1 or top-2) vs hn_moe_route with the
+    same logits followed by hn_moe_experts_decode: routing outputs and the
+    layer output bit for bit (at 5+ rows per expert both run 16-token
+    chunks).  Logits are fp16 values, with a few exact ties (the lower
+    expert wins in both)."""
+    from hydranet_amd.model.moe import ExpertTable, moe_decode_layer, moe_dispatch, moe_route
+    slots, _ = mixtral_experts
+    table = ExpertTable.from_slots(slots)
+    g = torch.Generator().manual_seed(90 + T * k)
+    x = torch.randn(T, 4096, generator=g).half().to(DEV)
+    gw = (torch.randn(8, 4096, generator=g) * 0.02).half().to(DEV)
+    lg = (torch.randn(T, 8, generator=g) * 2).half().float()
+    lg[::5, 3] = lg[::5, 5]  # exact ties
+    lg = lg.to(DEV)
+    print(f"[case] decode layer with logits T={T} k={k}", flush=True)
+    r0 = moe_route(x, k, 0, logits=lg)
+    ref = moe_dispatch(r0, table)
+    out, r1 = moe_decode_layer(x, gw, k, table, logits=lg)
+    torch.cuda.synchronize()
+    assert torch.equal(r1.idx, r0.idx)
+    assert torch.equal(r1.w, r0.w)
+    na = int(r0.n_active.item())
+    assert int(r1.n_active.item()) == na
+    assert torch.equal(r1.offsets, r0.offsets)
+    assert torch.equal(r1.active[:na], r0.active[:na])
+    assert torch.equal(r1.perm, r0.perm)
+    assert torch.equal(r1.inv, r0.inv)
+    assert torch.equal(out, ref)
+    # idx against a brute-force top-k of the logits (ties -> lower expert)
+    keys = lg.double() - torch.arange(8, device=DEV).double() * 1e-9
+    assert torch.equal(r1.idx.long(), keys.topk(k, dim=-1).indices)
+
+
 @pytest.mark.parametrize("T", [0, 1])
 def test_moe_layers_empty_and_single_token_batches(T, mixtral_experts):
     """An empty batch gives an empty output (no launch reads or writes rows);
