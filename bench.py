@@ -716,7 +716,9 @@ def bench_c5(args):
     ones; tokens/s = 64 x timed forwards / time.  bytes_per_step counts
     every expert of every layer once (64 tokens at top-1 leave an expert of a
     layer unused with probability (7/8)^64), the dense weights, the LM head and
-    the KV cache read at the step's context length."""
+    the KV cache read at the step's context length.  "top2": the same decode
+    with top-2 routing (the reference's FORCED_TOP2 mode, config.py:15-19),
+    from a second prefill, over min(64, --decode-tokens) tokens."""
     from hydranet_amd.model.decoder import (GraphDecoder, MixtralDecoderConfig,
                                             build_synthetic_decoder)
 
@@ -761,6 +763,24 @@ def bench_c5(args):
                       + kv_per_pos * (ctx0 + i + 1) for i in range(n))
     gbs = total_bytes / dt / 1e9
     toks = out
+    # the same decode at top-2 (FORCED_TOP2): fresh cache and prefill
+    del gd, cache
+    N2 = min(64, N)
+    cache2 = model.new_cache(B, P + N2)
+    tok2 = model(ids, cache2)[:, -1].argmax(-1, keepdim=True)
+    model.decode_top_k = 2
+    gd2 = GraphDecoder(model, cache2, tok2)
+    for _ in range(min(W, N2 - 2)):
+        gd2.step()
+    torch.cuda.synchronize()
+    n2 = N2 - 1 - min(W, N2 - 2)
+    t0 = time.perf_counter()
+    for i in range(n2):
+        gd2.step()
+    torch.cuda.synchronize()
+    dt2 = time.perf_counter() - t0
+    model.decode_top_k = 1
+    del gd2, cache2
     return {"workload": "C5: Mixtral-8x7B-shaped decoder (32 layers, H 4096, 32/8 heads, "
                         "head_dim 128, vocab 32000, 8 INT4 g128 experts per layer resident), "
                         "64 x 512-token random prompts, greedy decode (top-1 routing)",
@@ -770,7 +790,10 @@ def bench_c5(args):
             "prefill_tokens_per_s": round(B * P / prefill_s, 1),
             "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
             "bytes_per_step_avg": int(total_bytes / n),
-            "distinct_last_tokens": int(torch.unique(toks[:, -1]).numel())}
+            "distinct_last_tokens": int(torch.unique(toks[:, -1]).numel()),
+            "top2": {"routing": "top-2 at decode (FORCED_TOP2)", "decode_tokens": N2,
+                     "timed_forwards": n2, "ms_per_step": round(dt2 * 1e3 / n2, 4),
+                     "tokens_per_s": round(B * n2 / dt2, 1)}}
 
 
 # HBM bytes per launch of the roofline kernel (routing + grouped gate/up stream
@@ -920,6 +943,7 @@ def main():
             c5 = bench_c5(args)
             _log("c5", c5)
             res["decoder_tokens_per_s"] = c5["tokens_per_s"]
+            res["decoder_tokens_per_s_top2"] = c5["top2"]["tokens_per_s"]
             res["config"]["c5_decoder"] = c5
     else:
         cpu = cpu_c1

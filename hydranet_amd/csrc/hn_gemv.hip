@@ -623,8 +623,11 @@ constexpr long kStreamMaxRows = 16;
 // or up to 64 when the average over the experts is at most 8 (few rows per
 // expert: GLM-4.5-Air's 128 experts x top-8; 64 tokens over 8 experts at top-1
 // pass over each expert's weights about 1.4 times on average).
+// The streaming kernels take a grouped launch when every expert's rows fit
+// one pass (<= 16), or when the rows average at most 16 per expert (passes
+// of 8 or 16 tokens; the decoder's 64-token batches at top-1 and top-2).
 static bool stream_rows_ok(long max_rows, long rows, long E) {
-  return max_rows <= kStreamMaxRows || (max_rows <= kMaxRows && rows <= 8 * E);
+  return max_rows <= kStreamMaxRows || (max_rows <= kMaxRows && rows <= 16 * E);
 }
 
 extern "C" int hn_set_decode_path(int path) {

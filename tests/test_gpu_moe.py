@@ -233,7 +233,7 @@ def mixtral_experts():
     return slots, {e: slot_to_cpu(s) for e, s in enumerate(slots)}
 
 
-@pytest.mark.parametrize("T,k", [(1, 2), (4, 2), (16, 2), (32, 2), (64, 1)])
+@pytest.mark.parametrize("T,k", [(1, 2), (4, 2), (16, 2), (32, 2), (64, 1), (64, 2)])
 def test_mixtral_moe_layer_c2(T, k, mixtral_experts, decode_path):
     """Config C2: 8 Mixtral experts, softmax top-2, T tokens of decode; and
     the whole decoder's decode batch (64 tokens at top-1)."""
