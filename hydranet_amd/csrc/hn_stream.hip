@@ -232,7 +232,10 @@ __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void 
   h16* xs = reinterpret_cast<h16*>(smem);
   float* cs = reinterpret_cast<float*>(smem + (size_t)TC * 2 * A.ldx * 2);
   float2* red = reinterpret_cast<float2*>(cs + A.npair * kCsw);
-  constexpr int kRedSlots = (kMaxWaves - 1) * TH * MATS * 64;  // per buffer
+  // reduction slots per buffer: waves 1.. (TH 1: wave 0 reduces) or every
+  // wave (TH 2: wave h reduces token half h)
+  constexpr int kRedWaves = TH == 1 ? kMaxWaves - 1 : kMaxWaves;
+  constexpr int kRedSlots = kRedWaves * TH * MATS * 64;
   HnUnpackRegs ur;
   ur.m_lo = A.m_lo;
   ur.m_hi = A.m_hi;
@@ -303,8 +306,8 @@ __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void 
   }
   // reduction slots of waves this workgroup does not have stay zero
   for (int i = tid; i < NRB * kRedSlots; i += blockDim.x) {
-    const int slot = (i / (TH * MATS * 64)) % (kMaxWaves - 1);
-    if (slot >= KW - 1) red[i] = float2{0.f, 0.f};
+    const int slot = (i / (TH * MATS * 64)) % kRedWaves;
+    if (slot >= KW - (TH == 1 ? 1 : 0)) red[i] = float2{0.f, 0.f};
   }
   __syncthreads();
   if (nprob <= 0) return;
@@ -421,69 +424,83 @@ __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void 
           const float u1 = low ? acc_hi[h][mt][2] : acc_lo[h][mt][3];
           v[h][mt] = float2{e0 + xor8(u0), e1 + xor8(u1)};
         }
+      // the tile's outputs of token half h from the wave-summed partials
+      auto emit = [&](int h, const float2 (&vv)[MATS]) {
+        const int row = (t - st_kj * tiles_n) * kTileN + col;
+        if (row >= N) return;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int m = 8 * h + 2 * q + j;
+          if (m >= Mc) continue;
+          const float g = j ? vv[0].y : vv[0].x;
+          if (KS > 1) {
+            A.out32[st_kj * A.ks_stride + (long)(st_pr.t0 + sg.m0 + m) * N + row] = g;
+          } else {
+            h16 o16;
+            if (EPI == 1) {
+              const float u = j ? vv[MATS - 1].y : vv[MATS - 1].x;
+              o16 = (h16)(hn_silu((float)(h16)g) * (float)(h16)u);
+            } else {
+              o16 = (h16)g;
+            }
+            st_pr.out[(long)(sg.m0 + m) * A.ld_o + row] = o16;
+          }
+        }
+      };
       // KW-wave reduction through LDS (parity-buffered: one barrier per
-      // column; single-buffered: a second barrier first, after which wave 0
-      // has read the previous column's partials), summed in wave order by
-      // wave 0, which writes the tile
+      // column; single-buffered: a second barrier first, after which the
+      // previous column's partials have been read), summed in wave order
       float2* rb = red + (NRB == 2 ? parity * kRedSlots : 0);
       if (NRB == 1) __syncthreads();
-      if (wave > 0) {
+      if constexpr (TH == 1) {
+        // waves 1.. store; wave 0 adds them to its own and writes the tile
+        if (wave > 0) {
+#pragma unroll
+          for (int mt = 0; mt < MATS; ++mt) rb[((wave - 1) * MATS + mt) * 64 + lane] = v[0][mt];
+        }
+        __syncthreads();
+        if (wave == 0) {
+          float2 o[kMaxWaves - 1][MATS];
+#pragma unroll
+          for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
+#pragma unroll
+            for (int mt = 0; mt < MATS; ++mt) o[w2][mt] = rb[(w2 * MATS + mt) * 64 + lane];
+#pragma unroll
+          for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
+#pragma unroll
+            for (int mt = 0; mt < MATS; ++mt) {
+              v[0][mt].x += o[w2][mt].x;
+              v[0][mt].y += o[w2][mt].y;
+            }
+          emit(0, v[0]);
+        }
+      } else {
+        // every wave stores both halves; wave h sums half h over the waves in
+        // wave order (slots of absent waves hold zeros) and writes its tokens
 #pragma unroll
         for (int h = 0; h < TH; ++h)
 #pragma unroll
           for (int mt = 0; mt < MATS; ++mt)
-            rb[(((wave - 1) * TH + h) * MATS + mt) * 64 + lane] = v[h][mt];
-      }
-      __syncthreads();
-      if (wave == 0) {
-        float2 o[kMaxWaves - 1][TH][MATS];
+            rb[((wave * TH + h) * MATS + mt) * 64 + lane] = v[h][mt];
+        __syncthreads();
+        if (wave < TH) {
+          const int h = wave;
+          float2 o[kMaxWaves][MATS];
 #pragma unroll
-        for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
+          for (int w2 = 0; w2 < kMaxWaves; ++w2)
 #pragma unroll
-          for (int h = 0; h < TH; ++h)
+            for (int mt = 0; mt < MATS; ++mt) o[w2][mt] = rb[((w2 * TH + h) * MATS + mt) * 64 + lane];
+          float2 sum[MATS];
 #pragma unroll
-            for (int mt = 0; mt < MATS; ++mt)
-              o[w2][h][mt] = rb[((w2 * TH + h) * MATS + mt) * 64 + lane];
+          for (int mt = 0; mt < MATS; ++mt) sum[mt] = o[0][mt];
 #pragma unroll
-        for (int w2 = 0; w2 < kMaxWaves - 1; ++w2)
-#pragma unroll
-          for (int h = 0; h < TH; ++h)
+          for (int w2 = 1; w2 < kMaxWaves; ++w2)
 #pragma unroll
             for (int mt = 0; mt < MATS; ++mt) {
-              v[h][mt].x += o[w2][h][mt].x;
-              v[h][mt].y += o[w2][h][mt].y;
+              sum[mt].x += o[w2][mt].x;
+              sum[mt].y += o[w2][mt].y;
             }
-        const int row = (t - st_kj * tiles_n) * kTileN + col;
-        if (KS > 1) {
-          if (row < N) {
-#pragma unroll
-            for (int h = 0; h < TH; ++h)
-#pragma unroll
-              for (int j = 0; j < 2; ++j) {
-                const int m = 8 * h + 2 * q + j;
-                if (m < Mc)
-                  A.out32[st_kj * A.ks_stride + (long)(st_pr.t0 + sg.m0 + m) * N + row] =
-                      j ? v[h][0].y : v[h][0].x;
-              }
-          }
-        } else if (row < N) {
-#pragma unroll
-          for (int h = 0; h < TH; ++h)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const int m = 8 * h + 2 * q + j;
-              if (m < Mc) {
-                const float g = j ? v[h][0].y : v[h][0].x;
-                h16 o16;
-                if (EPI == 1) {
-                  const float u = j ? v[h][MATS - 1].y : v[h][MATS - 1].x;
-                  o16 = (h16)(hn_silu((float)(h16)g) * (float)(h16)u);
-                } else {
-                  o16 = (h16)g;
-                }
-                st_pr.out[(long)(sg.m0 + m) * A.ld_o + row] = o16;
-              }
-            }
+          emit(h, sum);
         }
       }
       parity ^= 1;
@@ -564,7 +581,7 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   for (int th = (want16 && rows > 8 && th2_instantiated(grouped, mats, lpw)) ? 2 : 1;
        th >= 1; --th) {
     const int nrb = (th == 2 && mats == 2) ? 1 : 2;  // the kernel's reduction buffers
-    const int red = nrb * (kMaxWaves - 1) * th * mats * 64 * 8;
+    const int red = nrb * (th == 1 ? kMaxWaves - 1 : kMaxWaves) * th * mats * 64 * 8;
     const int want = (int)(rows < 8 * th ? rows : 8 * th);
     const int tcmax = (kLdsPerCu - kStaticLds - red - cs - meta) / per_tok;
     const int tc = tcmax < want ? tcmax : want;
@@ -629,7 +646,9 @@ int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, h
 template <bool GROUPED, int MATS, int EPI, bool WIDE>
 int launch_lpw(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
   if (p.th == 2) {  // the shapes th2_instantiated() names
-    if (p.lpw == 4) return launch_one<GROUPED, MATS, EPI, 4, 2, WIDE, 1, false, 2>(A, g, p, s);
+    // gate/up: two column buffers (a third spills); one matrix: three
+    if (p.lpw == 4)
+      return launch_one<GROUPED, MATS, EPI, 4, MATS == 2 ? 2 : 3, WIDE, 1, false, 2>(A, g, p, s);
     return HN_NOT_HANDLED;
   }
   if constexpr (MATS == 2) {
