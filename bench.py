@@ -281,7 +281,7 @@ def time_decode_phases(layers, x, T, H, I, g, E, reps: int = 12):
         _lib.call("hn_moe_route_gate_up", _lib.ptr(xx), H, _lib.ptr(gates[li]), H, None, T, E, k,
                   _lib.ptr(tb.dev), H, I, g, 1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w),
                   _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active),
-                  _lib.ptr(r.n_active), _lib.ptr(h_ws), sp)
+                  _lib.ptr(r.n_active), None, _lib.ptr(h_ws), sp)
 
     def down(li):
         r, tb = rts[li], layers[li].experts.table
@@ -654,7 +654,7 @@ def c2phase(args):
         _lib.call("hn_moe_route_gate_up", _lib.ptr(x), H, _lib.ptr(gate), H, None, T, E, k,
                   _lib.ptr(table.dev), H, I, g, 1e-9, 1.0, None, _lib.ptr(r.idx), _lib.ptr(r.w),
                   _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active),
-                  _lib.ptr(r.n_active), _lib.ptr(h_ws), _lib.stream())
+                  _lib.ptr(r.n_active), None, _lib.ptr(h_ws), _lib.stream())
     src = torch.empty(256 << 20, dtype=torch.float16, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(20):

@@ -42,16 +42,16 @@ SIGNATURES: dict[str, list] = {
     "hn_set_decode_path": [I],
     "hn_gemm_workspace_bytes": [],
     "hn_grouped_expert_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, P, P, P, L, P],
-    "hn_moe_route": [P, L, P, L, I, P, P, L, L, L, L, I, F, F, P, P, P, P, P, P, P, P, P, L,
-                     P],
+    "hn_moe_route": [P, L, P, L, I, P, P, L, L, L, L, I, F, F, P, P, P, P, P, P, P, P, P, P,
+                     L, P],
     "hn_moe_experts_decode": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, P, P, L, L, P, L, P, L,
                               P, L, P],
     "hn_grouped_decode_phase_int4": [I, P, P, P, P, P, L, L, L, L, L, L, P, P, L, P],
     "hn_moe_decode_layer_check": [L, L, L, L, L, L, I],
     "hn_moe_route_gate_up": [P, L, P, L, P, L, L, L, P, L, L, L, F, F, P, P, P, P, P, P, P, P,
-                             P, P],
+                             P, P, P],
     "hn_moe_decode_layer": [P, L, P, L, P, L, L, L, P, L, L, L, F, F, P, P, P, P, P, P, P, P,
-                            P, P, L, P, L, P],
+                            P, P, P, L, P, L, P],
     "hn_expert_mlp_int4_noalloc": [P, P, P, P, P, P, P, P, L, L, L, L, P],
 }
 

@@ -22,11 +22,13 @@ constexpr int kNormThreads = 256;
 
 constexpr int kMaxGate = 16;  // router experts the norm kernel can score
 
-// One workgroup per row; 8 fp16 per vector access.  LOGITS: also the router
-// logits of the normalised row, logits[row, e] = fp16(sum_k out[k] gate[e, k])
-// (fp32 sums: per thread, then the wave, then the waves in order) stored as
-// fp32 -- the fp16 Linear of TopKRouter (model/router.py:102) on this row.
-template <bool LOGITS>
+// One workgroup per row; 8 fp16 per vector access.  LG > 0: also the router
+// logits of the normalised row against E <= LG gate rows, logits[row, e] =
+// fp16(sum_k out[k] gate[e, k]) (fp32 sums: per thread, then the wave, then
+// the waves in order) stored as fp32 -- the fp16 Linear of TopKRouter
+// (model/router.py:102) on this row.  Every expert's gate loads of a thread
+// go out together and the E wave reductions are interleaved.
+template <int LG>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     const h16* __restrict__ x, long ld_x, const h16* __restrict__ res, long ld_r,
     h16* __restrict__ x_out, long ld_xo, const h16* __restrict__ w, h16* __restrict__ out,
@@ -80,33 +82,43 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
         o[e] = (h16)((float)wv[e] * t);
       }
       orow[j] = o;
-      if constexpr (LOGITS) v[i] = o;
+      if constexpr (LG > 0) v[i] = o;
     }
   }
-  if constexpr (LOGITS) {
+  if constexpr (LG > 0) {
     const int lane = tid & 63, wave = tid >> 6;
-    for (int e = 0; e < E; ++e) {  // uniform
-      const half8_t* gr = reinterpret_cast<const half8_t*>(gate + (long)e * ld_g);
-      float d = 0.f;
+    float d[LG];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = tid + i * kNormThreads;
-        if (j < nv) {
-          const half8_t gv = gr[j];
+    for (int e = 0; e < LG; ++e) d[e] = 0.f;
 #pragma unroll
-          for (int q = 0; q < 8; ++q) d = __builtin_fmaf((float)v[i][q], (float)gv[q], d);
-        }
+    for (int i = 0; i < 4; ++i) {
+      const int j = tid + i * kNormThreads;
+      if (j < nv) {
+        half8_t gv[LG];
+#pragma unroll
+        for (int e = 0; e < LG; ++e)
+          if (e < E) gv[e] = reinterpret_cast<const half8_t*>(gate + (long)e * ld_g)[j];
+#pragma unroll
+        for (int e = 0; e < LG; ++e)
+          if (e < E)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) d[e] = __builtin_fmaf((float)v[i][q], (float)gv[e][q], d[e]);
       }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
-      if (lane == 0) s_lg[wave][e] = d;
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+      for (int e = 0; e < LG; ++e) d[e] += __shfl_xor(d[e], off, 64);
+    if (lane == 0)
+#pragma unroll
+      for (int e = 0; e < LG; ++e)
+        if (e < E) s_lg[wave][e] = d[e];
     __syncthreads();
     if (tid < E) {
-      float d = 0.f;
+      float t = 0.f;
 #pragma unroll
-      for (int wv = 0; wv < kNormThreads / 64; ++wv) d += s_lg[wv][tid];
-      logits[(long)row * E + tid] = (float)(h16)d;
+      for (int wv = 0; wv < kNormThreads / 64; ++wv) t += s_lg[wv][tid];
+      logits[(long)row * E + tid] = (float)(h16)t;
     }
   }
 }
@@ -169,7 +181,7 @@ extern "C" int hn_add_rmsnorm(const void* x, long ld_x, const void* res, long ld
                    (!x_out || (al16(x_out) && ld_xo % 8 == 0)),
                "hn_add_rmsnorm: rows must be 16-byte aligned");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(add_rmsnorm_kernel<false>, dim3((unsigned)T), dim3(kNormThreads), 0,
+  hipLaunchKernelGGL(add_rmsnorm_kernel<0>, dim3((unsigned)T), dim3(kNormThreads), 0,
                      (hipStream_t)stream, (const h16*)x, ld_x, (const h16*)res, ld_r,
                      (h16*)x_out, ld_xo, (const h16*)w, (h16*)out, ld_o, (int)H, eps,
                      (const h16*)nullptr, 0L, 0, (float*)nullptr);
@@ -193,10 +205,11 @@ extern "C" int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, 
                    ld_g % 8 == 0 && ld_g >= H && logits,
                "hn_add_rmsnorm_router: rows must be 16-byte aligned (gate and logits given)");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(add_rmsnorm_kernel<true>, dim3((unsigned)T), dim3(kNormThreads), 0,
-                     (hipStream_t)stream, (const h16*)x, ld_x, (const h16*)res, ld_r,
-                     (h16*)x_out, ld_xo, (const h16*)w, (h16*)out, ld_o, (int)H, eps,
-                     (const h16*)gate, ld_g, (int)E, logits);
+  auto kern = E <= 8 ? add_rmsnorm_kernel<8> : add_rmsnorm_kernel<kMaxGate>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)T), dim3(kNormThreads), 0, (hipStream_t)stream,
+                     (const h16*)x, ld_x, (const h16*)res, ld_r, (h16*)x_out, ld_xo,
+                     (const h16*)w, (h16*)out, ld_o, (int)H, eps, (const h16*)gate, ld_g, (int)E,
+                     logits);
   HN_LAUNCH_CHECK("hn_add_rmsnorm_router");
   return 0;
 }

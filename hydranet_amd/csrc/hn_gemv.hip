@@ -593,8 +593,9 @@ extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const vo
                                             long k, const void* table, long H, long I, long group,
                                             float eps, float scaling, float* logits_out,
                                             int* idx, void* w, int* offsets, int* perm,
-                                            int* inv, int* active, int* n_active, void* h_ws,
-                                            void* stream, int dry_run);
+                                            int* inv, int* active, int* n_active,
+                                            long long* usage, void* h_ws, void* stream,
+                                            int dry_run);
 extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, const int* inv,
                                             const int* idx, const void* w, long T, long k,
                                             const void* shared, long ld_sh, void* out,
@@ -949,15 +950,15 @@ extern "C" int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w
                                     const void* table, long H, long I, long group, float eps,
                                     float scaling, void* logits_out, int* idx, void* w,
                                     int* offsets, int* perm, int* inv, int* active,
-                                    int* n_active, void* h_ws, void* stream) {
+                                    int* n_active, long long* usage, void* h_ws, void* stream) {
   const char* who = "hn_moe_route_gate_up";
   HN_ARG_CHECK(aligned16(h) && (logits_in || aligned16(gate_w)) && aligned16(h_ws),
                "%s: h, gate and h_ws rows must be 16-byte aligned", who);
   HN_ARG_CHECK(g_decode_path == 0, "%s: needs the streaming kernels (decode path 0)", who);
   const int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, logits_in, T, E, k, table,
                                               H, I, group, eps, scaling, (float*)logits_out, idx,
-                                              w, offsets, perm, inv, active, n_active, h_ws,
-                                              (hipStream_t)stream, 0);
+                                              w, offsets, perm, inv, active, n_active, usage,
+                                              h_ws, (hipStream_t)stream, 0);
   HN_ARG_CHECK(rc != HN_NOT_HANDLED, "%s: shape not covered (E <= 8, k 1 or 2, T k <= 64, T <= "
                "16 without logits_in, H %% 512 == 0, group 128; T=%ld E=%ld k=%ld H=%ld "
                "group=%ld)", who, T, E, k, H, group);
@@ -976,7 +977,7 @@ extern "C" int hn_moe_decode_layer_check(long T, long E, long k, long H, long I,
   const int a = hn_stream_route_gate_up_impl(nullptr, H, nullptr, H, has_logits ? &dummy : nullptr,
                                              T, E, k, nullptr, H, I, group, 0.f, 1.f, nullptr,
                                              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                             nullptr, nullptr, nullptr, 1);
+                                             nullptr, nullptr, nullptr, nullptr, 1);
   const int b = hn_stream_down_split_impl(nullptr, nullptr, nullptr, nullptr, nullptr, E, T,
                                           T * k, H, I, group, nullptr, nullptr, 1);
   return a == 0 && b == 0 ? 0 : HN_NOT_HANDLED;
@@ -992,8 +993,8 @@ extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w,
                                    const void* table, long H, long I, long group, float eps,
                                    float scaling, void* logits_out, int* idx, void* w,
                                    int* offsets, int* perm, int* inv, int* active, int* n_active,
-                                   void* h_ws, void* out, long ld_o, void* work, long work_bytes,
-                                   void* stream) {
+                                   long long* usage, void* h_ws, void* out, long ld_o, void* work,
+                                   long work_bytes, void* stream) {
   const char* who = "hn_moe_decode_layer";
   HN_ARG_CHECK(aligned16(h) && (logits_in || aligned16(gate_w)) && aligned16(h_ws) &&
                    aligned16(out) && ld_o % 8 == 0,
@@ -1004,7 +1005,7 @@ extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w,
   const bool ok =
       hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, logits_in, T, E, k, table, H, I, group,
                                    eps, scaling, (float*)logits_out, idx, w, offsets, perm, inv,
-                                   active, n_active, h_ws, s, 1) == 0 &&
+                                   active, n_active, usage, h_ws, s, 1) == 0 &&
       hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H, I, group,
                                 nullptr, s, 1) == 0;
   HN_ARG_CHECK(ok, "%s: shape not covered (E <= 8, k 1 or 2, T k <= 64, T <= 16 without "
@@ -1018,7 +1019,7 @@ extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w,
   float* part = (float*)((char*)work + ctr_bytes(E * tmax));
   int rc = hn_stream_route_gate_up_impl(h, ld_h, gate_w, ld_w, logits_in, T, E, k, table, H, I,
                                         group, eps, scaling, (float*)logits_out, idx, w, offsets,
-                                        perm, inv, active, n_active, h_ws, s, 0);
+                                        perm, inv, active, n_active, usage, h_ws, s, 0);
   if (rc == 0)
     rc = hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H, I,
                                    group, part, s, 0);

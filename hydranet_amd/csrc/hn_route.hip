@@ -294,7 +294,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     int k, int mode, float eps, float scaling, float* __restrict__ logits_out,
     int* __restrict__ idx_out, h16* __restrict__ w_out, int* __restrict__ offsets,
     int* __restrict__ perm, int* __restrict__ inv, int* __restrict__ active,
-    int* __restrict__ n_active, h16* __restrict__ x_perm, long ld_p) {
+    int* __restrict__ n_active, long long* __restrict__ usage, h16* __restrict__ x_perm,
+    long ld_p) {
   // logits, or the MFMA partial tiles (16 waves x 16 LG tokens x 16 experts)
   __shared__ float s_buf[LG == 4 ? 16 * 64 * 16 : kRouteMaxLogits];
   __shared__ float s_lg[512];               // MFMA logits (T * E <= 512)
@@ -433,6 +434,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         if (lead) {
           offsets[ex] = co;
           if (f[q]) active[fo] = ex;
+          if (usage && c[q]) usage[ex] += c[q];
         }
       }
       co += c[q];
@@ -587,7 +589,8 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
                             const void* logits_in, const void* bias, long T, long E, long H,
                             long k, int mode, float eps, float scaling, void* logits_out,
                             int* idx_out, void* w_out, int* offsets, int* perm, int* inv,
-                            int* active, int* n_active, void* x_perm, long ld_p, void* stream) {
+                            int* active, int* n_active, long long* usage, void* x_perm,
+                            long ld_p, void* stream) {
   const char* who = "hn_moe_route";
   HN_ARG_CHECK(T >= 0 && E > 0 && E <= kMaxExperts && H > 0,
                "%s: need 0 < E <= %d", who, kMaxExperts);
@@ -614,7 +617,7 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
                      (const h16*)h, ld_h, (const TW*)w, ld_w, (const float*)logits_in,           \
                      (const float*)bias, (int)T, (int)E, (int)H, (int)k, mode, eps, scaling,      \
                      (float*)logits_out, idx_out, (h16*)w_out, offsets, perm, inv, active,        \
-                     n_active, (h16*)x_perm, ld_p)
+                     n_active, usage, (h16*)x_perm, ld_p)
   if (w_dtype == 0) {
     if (lgv == 1 && mix) HN_ROUTE_LAUNCH(h16, true, 1, 1);
     else if (lgv == 2 && mix) HN_ROUTE_LAUNCH(h16, true, 2, 1);

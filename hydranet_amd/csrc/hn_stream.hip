@@ -156,6 +156,7 @@ __device__ int route_prologue(const StreamArgs& A, float* part, int* s_act, int*
         if (lead) {
           A.offsets_out[x] = run;
           if (c > 0) A.active_out[nact] = x;
+          if (A.usage && c > 0) A.usage[x] += c;
         }
       }
       nact += c > 0 ? 1 : 0;
@@ -824,8 +825,9 @@ extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const vo
                                             long k, const void* table, long H, long I, long group,
                                             float eps, float scaling, float* logits_out,
                                             int* idx, void* w, int* offsets, int* perm,
-                                            int* inv, int* active, int* n_active, void* h_ws,
-                                            void* stream, int dry_run) {
+                                            int* inv, int* active, int* n_active,
+                                            long long* usage, void* h_ws, void* stream,
+                                            int dry_run) {
   if (T < 1 || E < 1 || E > 8 || (k != 1 && k != 2) || T * k > 64 ||
       (!logits_in && T > 16) || H % 512 != 0 || group != 128 || I % 128 != 0 ||
       ld_hx % 8 != 0 || (!logits_in && ld_gate % 8 != 0) || ld_hx >= (1L << 31) ||
@@ -864,6 +866,7 @@ extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const vo
   A.inv_out = inv;
   A.active_out = active;
   A.n_active_out = n_active;
+  A.usage = usage;
   const GroupedPtrs g = {(const SExpert*)table, nullptr, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
   int rc = HN_NOT_HANDLED;

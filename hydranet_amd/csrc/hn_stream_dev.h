@@ -54,6 +54,7 @@ struct StreamArgs {
   float* logits_out;
   int* idx_out; h16* w_out;
   int* offsets_out; int* perm_out; int* inv_out; int* active_out; int* n_active_out;
+  long long* usage;  // optional [E]: += the routed rows per expert (workgroup 0)
 };
 
 // Weights and scales of one column for one wave.  Scales: with WIDE, dword

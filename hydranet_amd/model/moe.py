@@ -93,10 +93,13 @@ def route_fits(T: int, E: int, k: int) -> bool:
 
 def moe_route(hidden: torch.Tensor, k: int, mode: int, gate_w: Optional[torch.Tensor] = None,
               logits: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
-              eps: float = 1e-9, scaling: float = 1.0, want_logits: bool = True) -> Routed:
+              eps: float = 1e-9, scaling: float = 1.0, want_logits: bool = True,
+              usage: Optional[torch.Tensor] = None) -> Routed:
     """Logits (from gate_w, unless ``logits`` is given), top-k, permutation and
     gather in one launch (hn_moe_route).  mode 0: Mixtral softmax top-k over
-    fp16-rounded logits of an fp16 gate; mode 1: GLM sigmoid top-k (fp32 gate)."""
+    fp16-rounded logits of an fp16 gate; mode 1: GLM sigmoid top-k (fp32 gate).
+    usage: optional int64 [E] counters; the launch adds each expert's routed
+    rows (TopKRouter's usage counts)."""
     T, H = hidden.shape
     _lib.require_gpu(hidden)
     dev = hidden.device
@@ -121,8 +124,16 @@ def moe_route(hidden: torch.Tensor, k: int, mode: int, gate_w: Optional[torch.Te
               _lib.ptr(lg_in), _lib.ptr(b), T, E, H, k, mode, eps, scaling,
               _lib.ptr(out_logits), _lib.ptr(r.idx), _lib.ptr(r.w), _lib.ptr(r.offsets),
               _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active), _lib.ptr(r.n_active),
-              _lib.ptr(r.x_perm), H, _lib.stream(dev))
+              _lib.ptr(_usage_ptr(usage, E, dev)), _lib.ptr(r.x_perm), H, _lib.stream(dev))
     return r
+
+
+def _usage_ptr(usage: Optional[torch.Tensor], E: int, dev) -> Optional[torch.Tensor]:
+    if usage is None:
+        return None
+    assert usage.dtype == torch.int64 and usage.is_contiguous() and usage.numel() == E \
+        and usage.device == torch.device(dev), "usage: contiguous int64 [E] on the layer's device"
+    return usage
 
 
 def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torch.Tensor,
@@ -137,7 +148,8 @@ def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torc
 
 
 def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: "ExpertTable",
-                     want_logits: bool = False, logits: Optional[torch.Tensor] = None):
+                     want_logits: bool = False, logits: Optional[torch.Tensor] = None,
+                     usage: Optional[torch.Tensor] = None):
     """One Mixtral MoE layer at decode in three launches (hn_moe_decode_layer):
     softmax top-k and the stable permutation computed in the gate/up kernel
     (with the fp16 gate logits, unless ``logits`` [T, E] are given), the down
@@ -168,7 +180,8 @@ def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: 
               _lib.ptr(lg_in), T, E, k, _lib.ptr(table.dev), H, I, g, 1e-9, 1.0,
               _lib.ptr(r.logits if lg_in is None else None), _lib.ptr(r.idx),
               _lib.ptr(r.w), _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv),
-              _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(h_ws), _lib.ptr(out), H,
+              _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(_usage_ptr(usage, E, dev)),
+              _lib.ptr(h_ws), _lib.ptr(out), H,
               _lib.ptr(work), work.numel(), _lib.stream(dev))
     return out, r
 
@@ -363,17 +376,18 @@ class MixtralMoELayer(nn.Module):
                     logits = router_logits(flat, rt.gate.weight.to(torch.float16))
                 logits = rt._affinity(logits)
             table = self.experts.static_table(flat.device)
+            # the routing launch adds to the usage counts (no host sync:
+            # graph-capturable)
+            usage = None if rt.training else rt.usage_counts
             if table is not None and decode_layer_fits(T, self.num_experts, top_k, table,
                                                        rt.gate.weight, logits is not None):
                 # decode, resident experts: routing inside the gate/up kernel
-                out, r = moe_decode_layer(flat, rt.gate.weight, top_k, table, logits=logits)
+                out, r = moe_decode_layer(flat, rt.gate.weight, top_k, table, logits=logits,
+                                          usage=usage)
             else:
                 # decode: routing, permutation and gather in one launch
-                r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits)
+                r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits, usage=usage)
                 out = moe_dispatch(r, self.experts.table_for(r.idx))
-            if not rt.training:
-                sel = r.idx.view(-1).long()  # no host sync: graph-capturable
-                rt.usage_counts.scatter_add_(0, sel, rt._one.expand_as(sel))
             self.last_routing = (r.idx, r.w)
             return out.view(B, S, H)
         ro = rt(hidden_states, top_k_override=top_k)

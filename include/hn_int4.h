@@ -118,7 +118,9 @@ int hn_moe_gather(const void* x, long ld_x, const int* perm, long k, const int* 
  * x_perm [T*k, H] (as hn_moe_gather); logits_out may be NULL.  Every
  * workgroup repeats the routing of all T tokens and copies a share of the
  * rows, so the outputs equal those of the four separate kernels.
- * T*E <= 8192, T*k <= 1024, E <= 256.  Replaces TopKRouter.forward
+ * T*E <= 8192, T*k <= 1024, E <= 256.  usage (may be NULL): int64 [E]
+ * counters to which the call adds each expert's routed rows (TopKRouter's
+ * usage counts, model/router.py:123-124).  Replaces TopKRouter.forward
  * (model/router.py:96-120) or GLM4SigmoidRouter.forward (model/glm4.py:275-309)
  * plus the unique()/where()/gather steps of MixtralMoELayer.forward
  * (model/mixtral.py:296-338) at decode sizes. */
@@ -126,7 +128,7 @@ int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, int w_dtype
                  const void* logits_in, const void* bias, long T, long E, long H, long k,
                  int mode, float eps, float scaling, void* logits_out, int* idx_out,
                  void* w_out, int* offsets, int* perm, int* inv, int* active, int* n_active,
-                 void* x_perm, long ld_p, void* stream);
+                 long long* usage, void* x_perm, long ld_p, void* stream);
 
 /* out[T, H] = (shared +) sum over the token's experts (ascending id) of
  * fp16(y_perm[inv[t*k+s]] * w[t, s]) with fp16 accumulation: output.index_add_
@@ -178,7 +180,7 @@ int hn_moe_route_gate_up(const void* h, long ld_h, const void* gate_w, long ld_w
                          const float* logits_in, long T, long E, long k, const void* table,
                          long H, long I, long group, float eps, float scaling, void* logits_out,
                          int* idx, void* w, int* offsets, int* perm, int* inv, int* active,
-                         int* n_active, void* h_ws, void* stream);
+                         int* n_active, long long* usage, void* h_ws, void* stream);
 
 /* 0 when hn_moe_decode_layer covers (T, E, k, H, I, group) with the current
  * decode kernel family, else a nonzero code (no error message is set).
@@ -195,8 +197,8 @@ int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group
  * given in logits_in [T, E] fp32 (fp16 values, e.g. from
  * hn_add_rmsnorm_router; gate_w may then be NULL).  Results equal
  * hn_moe_route + hn_moe_experts_decode; the routing outputs (logits_out may be
- * NULL, idx, w, offsets [E + 1], perm, inv, active, n_active) are written as
- * hn_moe_route writes them.  h_ws [T k, I] fp16; work:
+ * NULL, idx, w, offsets [E + 1], perm, inv, active, n_active, usage) are
+ * written as hn_moe_route writes them.  h_ws [T k, I] fp16; work:
  * hn_skinny_workspace_bytes(3, T k, H, I, E).  Replaces
  * MixtralMoELayer.forward's router call, per-expert loop and index_add_
  * (model/mixtral.py:283-368) at decode sizes. */
@@ -204,8 +206,8 @@ int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
                         const float* logits_in, long T, long E, long k, const void* table,
                         long H, long I, long group, float eps, float scaling, void* logits_out,
                         int* idx, void* w, int* offsets, int* perm, int* inv, int* active,
-                        int* n_active, void* h_ws, void* out, long ld_o, void* work,
-                        long work_bytes, void* stream);
+                        int* n_active, long long* usage, void* h_ws, void* out, long ld_o,
+                        void* work, long work_bytes, void* stream);
 
 /* One phase of hn_moe_experts_decode's streaming path on its own (<= 16 rows per
  * expert, group 128): phase 0 reads x [rows, H] (sorted by expert) and writes

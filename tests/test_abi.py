@@ -64,7 +64,7 @@ def test_argument_errors_raise_without_gpu():
     with pytest.raises(RuntimeError, match="decode sizes"):
         _lib.call("hn_moe_route", None, 4096, None, 4096, 0, None, None, 2048, 8, 4096, 2, 0,
                   ctypes.c_float(0), ctypes.c_float(1), None, None, None, None, None, None, None,
-                  None, None, 4096, None)
+                  None, None, None, 4096, None)
 
 
 def test_growing_a_workspace_keeps_the_old_buffer_allocated():

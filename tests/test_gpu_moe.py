@@ -508,6 +508,32 @@ def test_decode_layer_with_given_logits_matches_route_then_experts(T, k, mixtral
     assert torch.equal(r1.idx.long(), keys.topk(k, dim=-1).indices)
 
 
+@pytest.mark.parametrize("T,k,given", [(4, 2, False), (16, 2, False), (20, 2, False),
+                                       (64, 1, True), (64, 2, True), (4, 1, True)])
+def test_usage_counts_follow_the_routing(T, k, given, mixtral_experts):
+    """TopKRouter's usage counts (model/router.py:123-124), updated by the
+    routing launch itself (the fused gate/up routing or hn_moe_route): after
+    three calls in eval mode they equal the histogram of the experts the
+    layer selected, summed over the calls; in training mode they stay put
+    (counted at inference only, as the reference's)."""
+    from hydranet_amd.model.moe import MixtralMoELayer
+    slots, _ = mixtral_experts
+    layer = MixtralMoELayer(4096, 8, 2, slots=slots).to(DEV).eval()
+    layer.router.gate.weight.data = _randn(8, (8, 4096), 0.02).to(DEV)
+    want = torch.zeros(8, dtype=torch.long)
+    for call in range(3):
+        h = _randn(300 + 10 * T + call, (1, T, 4096)).to(DEV)
+        lg = None
+        if given:
+            lg = (h.view(T, 4096).float() @ layer.router.gate.weight.float().t()).half().float()
+        layer(h, top_k=k, logits=lg)
+        want += torch.bincount(layer.last_routing[0].view(-1).long().cpu(), minlength=8)
+    assert torch.equal(layer.router.usage_counts.cpu(), want), (layer.router.usage_counts, want)
+    layer.router.train()
+    layer(h, top_k=k, logits=lg)
+    assert torch.equal(layer.router.usage_counts.cpu(), want)
+
+
 @pytest.mark.parametrize("T", [0, 1])
 def test_moe_layers_empty_and_single_token_batches(T, mixtral_experts):
     """An empty batch gives an empty output (no launch reads or writes rows);
