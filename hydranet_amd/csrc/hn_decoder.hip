@@ -123,6 +123,63 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
   }
 }
 
+// Attention probabilities of a decode step, one wave per row of scores:
+//   a = fp16(float(s) * inv_scale);  a = fp16(float(a) + float(mask))  (mask given)
+//   p = fp16(exp(a - max) / sum exp(a - max))   (fp32)
+// The torch formulation's steps (model/mixtral.py:193-203): a Half tensor
+// divided by a Python scalar is multiplied by the fp32 reciprocal
+// (div_true_kernel_cuda's scalar path) and rounded; the mask add rounds;
+// F.softmax(dtype=float32) of a row of L <= 1024 runs softmax_warp_forward,
+// whose element order this kernel keeps: ws = min(2^ceil(log2 L), 64) lanes,
+// lane l holding elements l + ws * it, each lane's exps summed in it order,
+// then butterflies from ws / 2 down (max, then sum), exp by the same libm
+// expf; the .to(fp16) rounds the fp32 quotient.  Rows (b, g, r, s) take mask
+// row s = row % mask_rows.
+template <int IT>
+__global__ __launch_bounds__(256) void attn_softmax_kernel(const h16* __restrict__ s, long ld_s,
+                                                           const h16* __restrict__ mask,
+                                                           long ld_m, int mask_rows, int rows,
+                                                           int L, int ws, float inv_scale,
+                                                           h16* __restrict__ out, long ld_o) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wave
+  const h16* sr = s + (long)row * ld_s;
+  const h16* mr = mask ? mask + (long)(row % mask_rows) * ld_m : nullptr;
+  float x[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = it * ws + lane;
+    if (lane < ws && i < L) {
+      h16 a = (h16)((float)sr[i] * inv_scale);
+      if (mr) a = (h16)((float)a + (float)mr[i]);
+      x[it] = (float)a;
+    } else {
+      x[it] = -__builtin_inff();
+    }
+  }
+  float mx = x[0];
+#pragma unroll
+  for (int it = 1; it < IT; ++it) mx = mx > x[it] ? mx : x[it];
+  for (int off = ws >> 1; off > 0; off >>= 1) {
+    const float o = __shfl_xor(mx, off, 64);
+    mx = mx < o ? o : mx;
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    x[it] = expf(x[it] - mx);
+    sum += x[it];
+  }
+  for (int off = ws >> 1; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, 64);
+  h16* orow = out + (long)row * ld_o;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = it * ws + lane;
+    if (lane < ws && i < L) orow[i] = (h16)(x[it] / sum);
+  }
+}
+
 // Grid (rows = B * S, nh + nkv): one workgroup of hd threads per (token,
 // head).  Heads below nh are query heads, written rotated to
 // q_out[b][h / rep][h % rep][s][:]; the others are KV heads g: the rotated
@@ -211,6 +268,38 @@ extern "C" int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, 
                      (const h16*)w, (h16*)out, ld_o, (int)H, eps, (const h16*)gate, ld_g, (int)E,
                      logits);
   HN_LAUNCH_CHECK("hn_add_rmsnorm_router");
+  return 0;
+}
+
+// Scale, mask, fp32 softmax and fp16 cast of attention scores in one
+// launch.  See include/hn_int4.h.
+extern "C" int hn_attn_softmax(const void* scores, long ld_s, const void* mask, long ld_m,
+                               long mask_rows, long rows, long L, float inv_scale, void* out,
+                               long ld_o, void* stream) {
+  HN_ARG_CHECK(rows >= 0 && L >= 1 && L <= 1024 && (!mask || mask_rows >= 1),
+               "hn_attn_softmax: need 1 <= L <= 1024 (L=%ld) and mask_rows >= 1 with a mask", L);
+  HN_ARG_CHECK(ld_s >= L && ld_o >= L && (!mask || ld_m >= L),
+               "hn_attn_softmax: row strides below L");
+  if (rows == 0) return 0;
+  int p2 = 1;
+  while (p2 < L) p2 <<= 1;
+  const int ws = p2 < 64 ? p2 : 64;
+  const int it = p2 / ws;
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+#define HN_SOFTMAX(N)                                                                          \
+  hipLaunchKernelGGL(attn_softmax_kernel<N>, grid, block, 0, st, (const h16*)scores, ld_s,     \
+                     (const h16*)mask, ld_m, (int)(mask ? mask_rows : 1), (int)rows, (int)L,   \
+                     ws, inv_scale, (h16*)out, ld_o)
+  switch (it) {
+    case 1: HN_SOFTMAX(1); break;
+    case 2: HN_SOFTMAX(2); break;
+    case 4: HN_SOFTMAX(4); break;
+    case 8: HN_SOFTMAX(8); break;
+    default: HN_SOFTMAX(16); break;
+  }
+#undef HN_SOFTMAX
+  HN_LAUNCH_CHECK("hn_attn_softmax");
   return 0;
 }
 

@@ -21,6 +21,7 @@ import math
 from dataclasses import dataclass
 from typing import List, Optional
 
+import numpy as np
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -195,12 +196,42 @@ class Attention(nn.Module):
             cache.update(layer, k, v, pos)
             qg = q.reshape(B, nkv, rep * S, hd)  # rows: (head within the group, token)
         kt, vv = cache.get(layer, kv_len)
-        scores = torch.matmul(qg, kt) / math.sqrt(hd)  # [B, nkv, rep * S, kv_len]
-        if mask is not None:
-            scores = (scores.view(B, nkv, rep, S, kv_len) + mask).view(B, nkv, rep * S, kv_len)
-        p = F.softmax(scores, dim=-1, dtype=torch.float32).to(qg.dtype)
+        scores = torch.matmul(qg, kt)  # [B, nkv, rep * S, kv_len]
+        if x.is_cuda and kv_len <= 1024 and (mask is None or mask.dtype == torch.float16):
+            p = attn_softmax(scores, mask, hd)
+        else:
+            scores = scores / math.sqrt(hd)
+            if mask is not None:
+                scores = (scores.view(B, nkv, rep, S, kv_len) + mask).view(B, nkv, rep * S,
+                                                                           kv_len)
+            p = F.softmax(scores, dim=-1, dtype=torch.float32).to(qg.dtype)
         o = torch.matmul(p, vv).view(B, nh, S, hd)
         return self.o_proj(o.transpose(1, 2).reshape(B, S, nh * hd))
+
+
+def attn_softmax(scores: torch.Tensor, mask: Optional[torch.Tensor], head_dim: int) -> torch.Tensor:
+    """fp16(softmax_fp32(fp16(scores / sqrt(head_dim)) + mask)) over the last
+    dim (<= 1024), one launch (hn_attn_softmax): the torch formulation's
+    rounding steps and reduction order.  scores [..., rows, L] fp16 with the
+    mask's S rows fastest among the rows; mask [S, L] fp16 or None."""
+    from .. import _lib
+    L = scores.shape[-1]
+    s2 = scores.reshape(-1, L)
+    if s2.stride(-1) != 1 or s2.stride(0) < L:
+        s2 = s2.contiguous()
+    out = torch.empty((s2.shape[0], L), dtype=torch.float16, device=scores.device)
+    # torch divides a Half tensor by a Python scalar as a multiply by the fp32
+    # reciprocal of the fp32-rounded scalar
+    inv = float(np.float32(1.0) / np.float32(math.sqrt(head_dim)))
+    m2 = None
+    if mask is not None:
+        m2 = mask.reshape(-1, L)
+        if m2.stride(-1) != 1:
+            m2 = m2.contiguous()
+    _lib.call("hn_attn_softmax", _lib.ptr(s2), s2.stride(0), _lib.ptr(m2),
+              L if m2 is None else m2.stride(0), 1 if m2 is None else m2.shape[0], s2.shape[0],
+              L, inv, _lib.ptr(out), L, _lib.stream(scores.device))
+    return out.view(scores.shape)
 
 
 def add_rmsnorm(x: torch.Tensor, res: Optional[torch.Tensor], norm: RMSNorm,

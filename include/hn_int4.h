@@ -283,6 +283,17 @@ int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, long ld_r, 
                           long ld_xo, const void* w, void* out, long ld_o, long T, long H,
                           float eps, const void* gate, long ld_g, long E, float* logits,
                           void* stream);
+/* hn_attn_softmax: attention probabilities from fp16 scores [rows, L] (row
+ *   stride ld_s, 1 <= L <= 1024): a = fp16(s * inv_scale), a = fp16(a +
+ *   mask[row % mask_rows]) when mask [mask_rows, L] fp16 (0 / -inf) is given,
+ *   out[row] = fp16(softmax_fp32(a)).  The scale, mask add, F.softmax(dtype=
+ *   float32) and .to(fp16) of the reference's attention (model/mixtral.py:
+ *   193-203) in one launch; inv_scale is the fp32 reciprocal torch multiplies
+ *   by for a division by the Python scalar sqrt(head_dim); the softmax keeps
+ *   the element-to-lane layout and reduction order of torch's warp softmax
+ *   for rows of up to 1024. */
+int hn_attn_softmax(const void* scores, long ld_s, const void* mask, long ld_m, long mask_rows,
+                    long rows, long L, float inv_scale, void* out, long ld_o, void* stream);
 int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k, const void* v, long ld_v,
                    const float* cos_t, const float* sin_t, const long* pos, long B, long S,
                    long nh, long nkv, long hd, void* q_out, void* kt, void* vc, long max_len,

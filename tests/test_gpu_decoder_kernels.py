@@ -92,6 +92,37 @@ def test_add_rmsnorm_in_place_residual():
     assert torch.equal(x, want)
 
 
+@pytest.mark.parametrize("rows,L,S", [(2048, 576, 1), (64, 1, 1), (128, 7, 1), (256, 64, 1),
+                                      (256, 65, 1), (512, 1000, 1), (96, 1024, 1),
+                                      (4 * 2 * 12, 12, 12), (2 * 4 * 40, 200, 40)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_attn_softmax_matches_torch_formulation(rows, L, S, masked):
+    """hn_attn_softmax against the reference's steps run by torch on the same
+    GPU (scores / sqrt(head_dim), + mask, F.softmax(dtype=float32), .to(fp16)):
+    bit for bit.  Masks: the decode graph's tail of -inf (S = 1) or a causal
+    mask (S > 1); one row of large scores exercises the max subtraction."""
+    import math
+    from hydranet_amd.model.decoder import attn_softmax, causal_mask
+    g = torch.Generator(device=DEV).manual_seed(rows + L)
+    sc = (torch.randn(rows // S, S, L, generator=g, device=DEV) * 6).half()
+    sc[0, 0, : min(L, 5)] = 300.0
+    mask = None
+    if masked:
+        if S == 1:
+            mask = torch.zeros((1, L), dtype=torch.float16, device=DEV)
+            mask[:, L - L // 5:] = float("-inf") if L > 1 else 0.0
+        else:
+            mask = causal_mask(L - S, S, DEV)
+    got = attn_softmax(sc, mask, 128)
+    ref = sc / math.sqrt(128)
+    if mask is not None:
+        ref = ref + mask
+    ref = torch.softmax(ref, dim=-1, dtype=torch.float32).to(torch.float16)
+    torch.cuda.synchronize()
+    diff = (got != ref)
+    assert not bool(diff.any()), (int(diff.sum()), float((got.float() - ref.float()).abs().max()))
+
+
 def _rotate_half(x):
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
