@@ -103,8 +103,11 @@ __device__ __forceinline__ void hn_unpack8_centered(uint32_t w, half2_t out[4]) 
 // Same unpack, producing the MFMA operand directly.  gfx9 VOP3/VOP3P
 // encodings take no literal constants and at most one SGPR, so the masks live
 // in SGPRs and the magic number and the fp16 constants in VGPRs (made opaque
-// once per kernel with hn_vgpr); v_and_or_b32 is written out because the
-// compiler otherwise splits it into v_and + v_or.
+// once per kernel with hn_vgpr).  (w & m) | magic is written as the bit-field
+// insert (w & m) | (magic & ~m) -- equal, since the magic has no bit under
+// either mask -- which the compiler emits as one v_bfi_b32 (written as
+// v_and + v_or, it is two).  It is plain C, not inline asm: the compiler's
+// hazard checks between MFMAs and later VALU writes see through it.
 struct HnUnpackRegs {
   uint32_t m_lo, m_hi;                       // SGPR: 0x000F000F, 0x00F000F0
   uint32_t magic;                            // VGPR: 0x64006400
@@ -118,9 +121,7 @@ __device__ __forceinline__ uint32_t hn_vgpr(uint32_t v) {
 }
 
 __device__ __forceinline__ uint32_t hn_and_or(uint32_t w, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(m), "v"(o));
-  return r;
+  return (w & m) | (o & ~m);
 }
 
 __device__ __forceinline__ half8_t hn_unpack8_regs(uint32_t w, const HnUnpackRegs& c) {

@@ -154,23 +154,29 @@ __device__ __forceinline__ void issue(WBuf<MATS, PAIRS, WIDE>& b, const Problem&
   if constexpr (WIDE) {
 #pragma unroll
     for (int mt = 0; mt < MATS; ++mt) {
+      // lo rows' scales, then hi rows' (stored by name: no pointer into the
+      // buffer, which keeps every element a plain register)
+      if constexpr (PAIRS == 1) {
+        b.slo[mt][0] = __builtin_amdgcn_raw_buffer_load_b32(rs[mt], vslo, 0, 0);
+        b.shi[mt][0] = __builtin_amdgcn_raw_buffer_load_b32(rs[mt], vshi, 0, 0);
+      } else if constexpr (PAIRS == 2) {
+        const auto vl = __builtin_amdgcn_raw_buffer_load_b64(rs[mt], vslo, 0, 0);
+        const auto vh = __builtin_amdgcn_raw_buffer_load_b64(rs[mt], vshi, 0, 0);
+        b.slo[mt][0] = vl[0];
+        b.slo[mt][1] = vl[1];
+        b.shi[mt][0] = vh[0];
+        b.shi[mt][1] = vh[1];
+      } else {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t vo = h ? vshi : vslo;
-        uint32_t* dst = h ? b.shi[mt] : b.slo[mt];
-        if constexpr (PAIRS == 1) {
-          dst[0] = __builtin_amdgcn_raw_buffer_load_b32(rs[mt], vo, 0, 0);
-        } else if constexpr (PAIRS == 2) {
-          const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs[mt], vo, 0, 0);
-          dst[0] = v[0];
-          dst[1] = v[1];
-        } else {
+        for (int j = 0; j < PAIRS / 4; ++j) {
+          const u32x4 vl = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[mt], vslo + 16 * j, 0, 0));
+          const u32x4 vh = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[mt], vshi + 16 * j, 0, 0));
 #pragma unroll
-          for (int j = 0; j < PAIRS / 4; ++j) {
-            const u32x4 v = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[mt], vo + 16 * j, 0, 0));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dst[4 * j + e] = v[e];
+          for (int e = 0; e < 4; ++e) {
+            b.slo[mt][4 * j + e] = vl[e];
+            b.shi[mt][4 * j + e] = vh[e];
           }
         }
       }
