@@ -102,7 +102,7 @@ __device__ __forceinline__ void hn_unpack8_centered(uint32_t w, half2_t out[4]) 
 
 // Same unpack, producing the MFMA operand directly.  gfx9 VOP3/VOP3P
 // encodings take no literal constants and at most one SGPR, so the masks live
-// in SGPRs and the magic number and the fp16 constants in VGPRs (made opaque
+// in SGPRs and the magic number and the fp16 constants in VGPRs (put there
 // once per kernel with hn_vgpr).  (w & m) | magic is written as the bit-field
 // insert (w & m) | (magic & ~m) -- equal, since the magic has no bit under
 // either mask -- which the compiler emits as one v_bfi_b32 (written as
@@ -114,10 +114,11 @@ struct HnUnpackRegs {
   uint32_t bias_lo, sixteenth, bias_hi;      // VGPR: half2 (-1032), (1/16), (-72)
 };
 
+// A wave-uniform value in a VGPR (an identity DPP move: a real instruction,
+// so the compiler neither folds it back into an SGPR operand nor loses track
+// of it in its hazard checks).
 __device__ __forceinline__ uint32_t hn_vgpr(uint32_t v) {
-  uint32_t r;
-  asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
-  return r;
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xE4, 0xF, 0xF, false);
 }
 
 __device__ __forceinline__ uint32_t hn_and_or(uint32_t w, uint32_t m, uint32_t o) {
