@@ -146,14 +146,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---------------------------------------------------------------------------
-// Work decomposition.  A tile is 128 tokens x 256 weight rows; a workgroup of
-// four waves computes it, each wave 64 rows: one 32-row block of gate and the
-// same 32 rows of up (MATS 2, so the SwiGLU epilogue finds both values of an
-// output in one lane) or two 32-row blocks of one matrix (MATS 1).  Two
-// workgroups per CU (two waves per SIMD: one wave's unpack runs under the
-// other's MFMAs, and one workgroup's tile start and epilogue under the
-// other's K loop).  K advances in stages of 64: three LDS stages, the loads
-// of stages t + 1 and t + 2 in flight while stage t computes.
+// Work decomposition.  A tile is up to 256 tokens (NRB row blocks of 32) x 256
+// weight rows; a workgroup of four waves computes it, each wave 64 rows: one
+// 32-row block of gate and the same 32 rows of up (MATS 2, so the SwiGLU
+// epilogue finds both values of an output in one lane) or two 32-row blocks
+// of one matrix (MATS 1).  One workgroup per CU: its accumulators take all
+// 256 AGPRs of each wave.  K advances in stages of 64: three LDS stages, the
+// loads of stages t + 1 and t + 2 in flight while stage t computes.
 // ---------------------------------------------------------------------------
 #ifndef HN_GEMM_KSM
 #define HN_GEMM_KSM 1         // k per stage = 64 * KSM
@@ -218,20 +217,24 @@ __device__ __forceinline__ uint32_t a_offset(int j, int wave, int lane, int rows
 // Issue stage t's loads into the LDS stage at byte address st.  Weights: per
 // block kKSM loads; load d brings lane l's 16 bytes at 16 kKSM (l / 32) + 16 d
 // of row (l % 32)'s 32 kKSM bytes of the stage.  Scales: the dword holding the
-// lane's scale.
+// lane's scale.  With real false the same loads go out against empty buffer
+// ranges: they read nothing from memory (out of range), write zeros into a
+// stage no one reads, and keep the count of loads per stage fixed, so the
+// K loop's waits are the same at every stage (no branch in the loop).
 template <int NRB>
-__device__ __forceinline__ void issue_stage(const TileLoads& tl, int t, uint32_t st, int wave) {
+__device__ __forceinline__ void issue_stage(const TileLoads& tl, int t, uint32_t st, int wave,
+                                            bool real) {
   using L = Stage;
   constexpr int NA = a_loads<NRB>();
   {
-    const __amdgpu_buffer_rsrc_t r = rsrc(tl.px, tl.nx);
+    const __amdgpu_buffer_rsrc_t r = rsrc(tl.px, real ? tl.nx : 0);
 #pragma unroll
     for (int j = 0; j < NA; ++j)
       dma_b128(r, tl.va[j], 2 * kKS * t, st + L::kA + (wave * NA + j) * 1024);
   }
 #pragma unroll
   for (int b = 0; b < kBlk; ++b) {
-    const __amdgpu_buffer_rsrc_t r = rsrc(tl.pq[b], tl.nq);
+    const __amdgpu_buffer_rsrc_t r = rsrc(tl.pq[b], real ? tl.nq : 0);
 #pragma unroll
     for (int d = 0; d < kKSM; ++d)
       dma_b128(r, tl.vq[b] + 16 * d, kKS / 2 * t,
@@ -240,7 +243,8 @@ __device__ __forceinline__ void issue_stage(const TileLoads& tl, int t, uint32_t
   const uint32_t soff = 2 * ((kKS * t) / tl.group);
 #pragma unroll
   for (int b = 0; b < kBlk; ++b)
-    dma_b32(rsrc(tl.ps[b], tl.ns), (tl.vs[b] + soff) & ~3u, st + L::kS + (wave * kBlk + b) * 256);
+    dma_b32(rsrc(tl.ps[b], real ? tl.ns : 0), (tl.vs[b] + soff) & ~3u,
+            st + L::kS + (wave * kBlk + b) * 256);
 }
 
 // Unpack constants (gfx9 VOP3 takes no literals): mask in an SGPR, the rest
@@ -282,6 +286,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // ahead of step s's MFMAs into the other buffer.
 struct Ops {
   uint32_t pk[kBlk][kSteps];  // packed weights of the current stage, one dword per step
+  uint32_t sv[kBlk];      // scales as read (fp16 bits in the low half)
   half2_t s2[kBlk];       // scales, both halves
   half8_t af[2][kRBMax];  // A fragments of the row blocks
   half8_t bw[2][kBlk];    // unpacked weights
@@ -300,7 +305,8 @@ __device__ __forceinline__ void read_a(Ops& o, int buf, uint32_t st, int s, int 
 }
 
 // Weights + scales of the stage at st (stage number t); half-word of each
-// scale dword from the byte offset the dword was loaded for.
+// scale dword from the byte offset the dword was loaded for.  LDS reads only:
+// the scales are put in both halves by the first unpack of the stage.
 __device__ __forceinline__ void read_b(Ops& o, const TileLoads& tl, uint32_t st, int t, int wave,
                                        int lane) {
   using L = Stage;
@@ -315,58 +321,69 @@ __device__ __forceinline__ void read_b(Ops& o, const TileLoads& tl, uint32_t st,
       for (int i = 0; i < 4; ++i) o.pk[b][4 * d + i] = v[i];
     }
     const uint32_t hsel = (tl.vs[b] + soff) & 2u;
-    const uint32_t sv =
-        lds_read<unsigned short>(st + L::kS + (wave * kBlk + b) * 256 + lane * 4 + hsel);
-    o.s2[b] = hn_bits_h2(sv | (sv << 16));
+    o.sv[b] = lds_read<unsigned short>(st + L::kS + (wave * kBlk + b) * 256 + lane * 4 + hsel);
   }
 }
 
 __device__ __forceinline__ void deq_step(Ops& o, int buf, int s, const DeqRegs& dr) {
 #pragma unroll
-  for (int b = 0; b < kBlk; ++b) o.bw[buf][b] = deq8(o.pk[b][s], dr, o.s2[b]);
-}
-
-template <int NRB>
-__device__ __forceinline__ void mfma_step(const Ops& o, int buf, f32x16 (&acc)[kRBMax][kBlk]) {
-#pragma unroll
-  for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-    for (int b = 0; b < kBlk; ++b)
-      acc[rb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.af[buf][rb], o.bw[buf][b], acc[rb][b],
-                                                          0, 0, 0);
-}
-
-// Interleave hint for one step: LDS reads first, then NRB kBlk x (1 MFMA,
-// 16 / NRB VALU) -- the next step's unpack under this step's MFMAs.
-template <int NRB, int NDS>
-__device__ __forceinline__ void sched_step() {
-  if (NDS) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // DS read
-#pragma unroll
-  for (int i = 0; i < NRB * kBlk; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 16 / NRB, 0);   // VALU
+  for (int b = 0; b < kBlk; ++b) {
+    if (s == 0) o.s2[b] = hn_bits_h2(o.sv[b] | (o.sv[b] << 16));
+    o.bw[buf][b] = deq8(o.pk[b][s], dr, o.s2[b]);
   }
 }
 
-// K loop of one tile over stages [tb, T) of kKS k each.  In a stage, step s's MFMAs
-// overlap the unpack and A-fragment reads of step s + 1; during the last
-// step the wave waits for its own loads of stage t + 1 (those of t + 2 stay in
-// flight), reads that stage's weights and unpacks its first step; the barrier
-// then makes every wave's activation loads of t + 1 visible.
+// MFMAs I0 .. I1 - 1 of a step, in the order (row block, weight block).
+template <int I0, int I1>
+__device__ __forceinline__ void mfma_range(const Ops& o, int buf, f32x16 (&acc)[kRBMax][kBlk]) {
+#pragma unroll
+  for (int i = I0; i < I1; ++i)
+    acc[i / kBlk][i % kBlk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        o.af[buf][i / kBlk], o.bw[buf][i % kBlk], acc[i / kBlk][i % kBlk], 0, 0, 0);
+}
+
+// Interleave hint for one step: NRB kBlk x (1 MFMA, 16 / NRB VALU), with one
+// of the next step's NRB A-fragment reads after every kBlk-th MFMA -- the
+// next step's LDS reads and unpack under this step's MFMAs.  (Issued as a
+// burst, the reads stall the wave's issue and the MFMA pipe with it:
+// measured on MI355X, a stage of 64 MFMAs with its 32 reads in bursts took
+// about 20 % longer than with them spread.)
+template <int NRB>
+__device__ __forceinline__ void sched_step() {
+#pragma unroll
+  for (int i = 0; i < NRB * kBlk; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+    if (i % kBlk == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x002, 16 / NRB, 0);       // VALU
+  }
+}
+
+// K loop of one tile over stages [tb, te) of kKS k each.  In a stage, step s's
+// MFMAs overlap the unpack and A-fragment reads of step s + 1.  The last step
+// is ordered by hand (scheduling fences; the compiler would otherwise hoist
+// the barrier above the MFMAs and sink the unpack below it): the wave waits
+// for its own loads of stage t + 1 (those of t + 2 stay in flight) and reads
+// that stage's weights, issues a few MFMAs under the read, unpacks the next
+// stage's first step under most of the rest, meets the other waves at the
+// barrier (every wave's activation loads of t + 1 now visible, every read of
+// stage t done) and reads the next stage's first A fragments under the last
+// POST MFMAs.  Every stage issues the same loads (dummies past the end), so
+// the waits take no branch.
 template <int NRB>
 __device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int te, uint32_t lds0,
                                        int row32, int h, int wave, int lane, const DeqRegs& dr,
                                        f32x16 (&acc)[kRBMax][kBlk]) {
   using L = Stage;
   constexpr int LPS = loads_per_stage<NRB>();
+  constexpr int NM = NRB * kBlk;                   // MFMAs per step
+  constexpr int POST = NM / 2 < 6 ? NM / 2 : 6;    // MFMAs after the barrier
+  constexpr int PRE = NM - POST;
+  constexpr int COVER = PRE >= 8 ? 3 : (PRE >= 4 ? 2 : 1);  // MFMAs under the weight reads
+  constexpr int VPM = PRE > COVER ? (40 + PRE - COVER - 1) / (PRE - COVER) : 40;
   Ops o;
-  issue_stage<NRB>(tl, tb, lds0, wave);
-  if (tb + 1 < te) {
-    issue_stage<NRB>(tl, tb + 1, lds0 + L::kSize, wave);
-    wait_vmcnt<LPS>();
-  } else {
-    wait_vmcnt<0>();
-  }
+  issue_stage<NRB>(tl, tb, lds0, wave, true);
+  issue_stage<NRB>(tl, tb + 1 < te ? tb + 1 : tb, lds0 + L::kSize, wave, tb + 1 < te);
+  wait_vmcnt<LPS>();
   __syncthreads();
   read_b(o, tl, lds0, tb, wave, lane);
   deq_step(o, 0, 0, dr);
@@ -378,26 +395,35 @@ __device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int te, uint
     const uint32_t cur = lds0 + sc * L::kSize;
     const uint32_t nxt = lds0 + s1 * L::kSize;
     const bool ahead = t + 2 < te;  // uniform
-    if (ahead) issue_stage<NRB>(tl, t + 2, lds0 + s2 * L::kSize, wave);
+    issue_stage<NRB>(tl, ahead ? t + 2 : t, lds0 + s2 * L::kSize, wave, ahead);
 #pragma unroll
     for (int s = 0; s < kSteps - 1; ++s) {
-      // step s + 1's A fragments are requested before step s's MFMAs (the
-      // scheduling fences keep them there); its unpack runs under them
+      // step s + 1's A fragments and unpack under step s's MFMAs
       read_a<NRB>(o, (s + 1) & 1, cur, s + 1, row32, h);
-      __builtin_amdgcn_sched_barrier(0);
       deq_step(o, (s + 1) & 1, s + 1, dr);
-      mfma_step<NRB>(o, s & 1, acc);
-      sched_step<NRB, 0>();
+      mfma_range<0, NM>(o, s & 1, acc);
+      sched_step<NRB>();
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (ahead) wait_vmcnt<LPS>();
-    else wait_vmcnt<0>();
+    wait_vmcnt<LPS>();
     read_b(o, tl, nxt, t + 1, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_range<0, COVER>(o, 1, acc);
+    __builtin_amdgcn_sched_barrier(0);
     deq_step(o, 0, 0, dr);
-    mfma_step<NRB>(o, 1, acc);
-    sched_step<NRB, kBlk * kKSM + kBlk>();
+    mfma_range<COVER, PRE>(o, 1, acc);
+#pragma unroll
+    for (int i = COVER; i < PRE; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    if (t + 1 < te) read_a<NRB>(o, 0, nxt, 0, row32, h);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a<NRB>(o, 0, nxt, 0, row32, h);  // past the last stage: unused
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_range<PRE, NM>(o, 1, acc);
+    __builtin_amdgcn_sched_barrier(0);
     sc = s1;
   }
 }
@@ -406,39 +432,88 @@ __device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int te, uint
 // blocks), lane-interleaved so every store / load instruction is coalesced.
 constexpr long kWaveSlot = (long)kRBMax * kBlk * 16 * 64;  // floats
 
-// Stream-K: the iterations (tile, stage) are split evenly over the ranks
-// 0..nr-1 (rank r: [it_total r / nr, it_total (r + 1) / nr)); nr <= it_total,
-// so no range is empty and a tile's segments belong to consecutive ranks.
-// A tile whose stages belong to several ranks ("segments") is finished by the
+// Work.  A problem's M-tiles are RBM row blocks each ("full"), except its
+// last when that needs fewer: it runs the even number of blocks (2, 4, 6)
+// that covers its rows ("tail"), so rows past a problem's end cost at most
+// one block of MFMAs.  Tiles are numbered full ones first (problem by
+// problem, super-blocks of kSuperM M-tiles x all n-tiles), then tails
+// (problem by problem, n-tile by n-tile).
+//
+// Without a workspace every workgroup takes whole tiles round-robin.  With
+// one, whole rounds of full tiles go round-robin (one tile per workgroup per
+// round, all of equal cost: nothing to split), and the rest -- the full tiles
+// short of a round, then the tails -- are dealt out stream-K: their (tile,
+// chunk) iterations are numbered item by item and dealt by weight, a chunk of
+// a tile running w row blocks counting w + kTailC units (the stage's cost:
+// MFMAs per row block plus a part that does not shrink with the rows --
+// weight loads and unpack, barrier); rank r takes the chunks that start in
+// units [U r / nr, U (r + 1) / nr).  Every range holds at least as many units
+// as the largest chunk (nr <= U / (RBM + kTailC)), so it holds a chunk start:
+// no rank is idle, and the ranks holding a tile's chunks are consecutive.  A
+// tile whose chunks belong to several ranks ("segments") is finished by the
 // wave that arrives last: every segment stores its fp32 partial (relaxed
-// agent-scope atomics), publishes them and counts itself in
-// (hn_arrive); the last one acquires, sums all the partials from the slots in
-// segment order (deterministic) and resets the counter.
+// agent-scope atomics), publishes them and counts itself in (hn_arrive); the
+// last one acquires, sums the partials from the slots in segment order
+// (deterministic) and resets the counter.
+#ifndef HN_GEMM_TAILC
+#define HN_GEMM_TAILC 4
+#endif
+constexpr int kTailC = HN_GEMM_TAILC;  // fixed stage cost, in row blocks' MFMA time
+
+struct SkPlan {
+  long U;            // units
+  int nr;            // ranks
+  int RF;            // full tiles dealt stream-K (items 0 .. RF - 1), before the tails
+  int wF;            // their weight per chunk
+  int NT, NCH, nprob;
+  const int* thalf;  // tail M-tiles per problem, prefix (LDS)
+  const int* wt;     // row blocks of each problem's tail M-tile (LDS)
+  const long* upre;  // tail units per problem, prefix (LDS)
+
+  __device__ long UF() const { return (long)RF * NCH * wF; }
+  // first unit of chunk c of item i (a tail of problem p when i >= RF)
+  __device__ long unit(int i, int c, int p) const {
+    if (i < RF) return ((long)i * NCH + c) * wF;
+    return UF() + upre[p] + ((long)(i - RF - thalf[p] * NT) * NCH + c) * (wt[p] + kTailC);
+  }
+  // number (item NCH + chunk) of the first chunk that starts at unit u or
+  // later (the chunk count when none does)
+  __device__ long chunk_at(long u) const {
+    if (u < UF()) return (u + wF - 1) / wF;
+    if (u >= U) return ((long)RF + (long)thalf[nprob] * NT) * NCH;
+    const long ut = u - UF();
+    int lo = 0, hi = nprob - 1;  // the largest p with upre[p] <= ut: it has a tail
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (upre[mid] <= ut) lo = mid; else hi = mid - 1;
+    }
+    const int w = wt[lo] + kTailC;
+    return ((long)RF + (long)thalf[lo] * NT) * NCH + (ut - upre[lo] + w - 1) / w;
+  }
+  __device__ long bound(int r) const { return U * r / nr; }
+  // rank whose range holds unit u: the largest r with U r / nr <= u
+  __device__ int owner(long u) const { return (int)(((u + 1) * nr + U - 1) / U - 1); }
+  // a rank's partial slot for an item: 2 r, + 1 unless the item is the rank's
+  // first (a rank splits at most its first and its last item)
+  __device__ long slot(int r, int item) const {
+    return 2L * r + (chunk_at(bound(r)) / NCH == item ? 0 : 1);
+  }
+};
+
 struct SkSeg {
   int wf, nseg;  // first rank of the tile's segments, their number
 };
 
-__device__ __forceinline__ long sk_slot(int r, int tile, int pass, int T, long it_total, int nr) {
-  // a rank's slot for a tile of a pass: 4 r + 2 pass, + 1 unless the tile is
-  // the rank's first of the pass
-  const long br = it_total * r / nr;
-  return 4L * r + 2 * pass + (br / T == tile ? 0 : 1);
-}
-
 // Stores this wave's partial and counts it in.  True when it was the last
 // segment of the tile (the caller then finishes the tile from the slots).
 template <int RBM>
-__device__ __forceinline__ bool streamk_arrive(const GemmArgs& A, const f32x16 (&acc)[kRBMax][kBlk],
-                                               int nrb, int tile, int ctile, int pass, int T,
-                                               long it_total, int nr, int rank, int wave,
-                                               int lane, SkSeg& sgi) {
-  const long i0 = (long)tile * T, i1 = i0 + T - 1;
-  // rank owning iteration i: the largest r with it_total r / nr <= i
-  auto owner = [&](long i) { return (int)(((i + 1) * nr + it_total - 1) / it_total - 1); };
-  sgi.wf = owner(i0);
-  sgi.nseg = owner(i1) - sgi.wf + 1;
-  float* mine =
-      A.part + (sk_slot(rank, tile, pass, T, it_total, nr) * kWaves + wave) * kWaveSlot;
+__device__ __forceinline__ bool streamk_arrive(const GemmArgs& A, const SkPlan& sp,
+                                               const f32x16 (&acc)[kRBMax][kBlk], int nrb,
+                                               int item, int p, int rank, int wave, int lane,
+                                               SkSeg& sgi) {
+  sgi.wf = sp.owner(sp.unit(item, 0, p));
+  sgi.nseg = sp.owner(sp.unit(item, sp.NCH - 1, p)) - sgi.wf + 1;
+  float* mine = A.part + (sp.slot(rank, item) * kWaves + wave) * kWaveSlot;
 #pragma unroll
   for (int rb = 0; rb < RBM; ++rb)
     if (rb < nrb)  // uniform
@@ -449,7 +524,7 @@ __device__ __forceinline__ bool streamk_arrive(const GemmArgs& A, const f32x16 (
           __hip_atomic_store(mine + ((rb * kBlk + b) * 16 + r) * 64 + lane, acc[rb][b][r],
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   hn_publish_partials();
-  unsigned long long* c = A.ctr + (long)ctile * kWaves + wave;
+  unsigned long long* c = A.ctr + (long)item * kWaves + wave;
   int n = 0;
   if (lane == 0) n = hn_arrive(c, A.tag);
   n = __builtin_amdgcn_readfirstlane(n);
@@ -459,27 +534,76 @@ __device__ __forceinline__ bool streamk_arrive(const GemmArgs& A, const f32x16 (
   return true;
 }
 
-// The sum over the tile's segments of one accumulator register r of block
-// (rb, b), in segment order.
-__device__ __forceinline__ void sk_sum16(const GemmArgs& A, const SkSeg& sgi, int tile, int pass,
-                                         int T, long it_total, int nr, int wave, int lane,
-                                         int rb, int b, float (&v)[16]) {
-  for (int sg = 0; sg < sgi.nseg; ++sg) {
-    const float* src =
-        A.part + (sk_slot(sgi.wf + sg, tile, pass, T, it_total, nr) * kWaves + wave) * kWaveSlot +
-                       (long)(rb * kBlk + b) * 16 * 64 + lane;
-    float pv[16];
+// Row block rb of the tile summed over its segments' partial slots, in
+// segment order: v[b][r] for the wave's weight block b, accumulator register
+// r.  Plain loads: the caller's agent-scope acquire (L2 invalidate) has made
+// the other segments' stores, written through past their L2s, visible to
+// them; two segments' loads are in flight together.
+__device__ __forceinline__ void sk_sum_rb(const GemmArgs& A, const SkPlan& sp, const SkSeg& sgi,
+                                          int item, int wave, int lane, int rb,
+                                          float (&v)[kBlk][16]) {
+  for (int s0 = 0; s0 < sgi.nseg; s0 += 2) {
+    float t[2][kBlk][16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      pv[r] = __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int q = 0; q < 2; ++q)
+      if (s0 + q < sgi.nseg) {  // uniform
+        const float* src = A.part + (sp.slot(sgi.wf + s0 + q, item) * kWaves + wave) * kWaveSlot +
+                           (long)rb * kBlk * 16 * 64 + lane;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = sg == 0 ? pv[r] : v[r] + pv[r];
+        for (int b = 0; b < kBlk; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) t[q][b][r] = src[(b * 16 + r) * 64];
+      }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (s0 + q < sgi.nseg)
+#pragma unroll
+        for (int b = 0; b < kBlk; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) v[b][r] = s0 + q == 0 ? t[q][b][r] : v[b][r] + t[q][b][r];
   }
 }
 
-// RBM: row blocks of 32 tokens per M-tile (4 or 8).  With 8, a tile whose
-// rows fit in 128 runs the 4-block K loop (no MFMAs or loads for absent
-// rows beyond that granularity).
+// The K loop of a tile of NRB row blocks, with the activation offsets for it.
+template <int NRB>
+__device__ __forceinline__ void tile_k(TileLoads& tl, int rows, long ld_x, int nst, uint32_t lds0,
+                                       int row32, int h, int wave, int lane, const DeqRegs& dr,
+                                       f32x16 (&acc)[kRBMax][kBlk]) {
+#pragma unroll
+  for (int j = 0; j < a_loads<NRB>(); ++j) tl.va[j] = a_offset<NRB>(j, wave, lane, rows, ld_x);
+  k_loop<NRB>(tl, 0, nst, lds0, row32, h, wave, lane, dr, acc);
+}
+
+// Stores row block rb of the tile's output: lane holds column n (+ 32 ob),
+// tokens 32 rb + 8 (r / 4) + 4 h + r % 4.  MATS 2: silu(g) * u.
+template <int MATS>
+__device__ __forceinline__ void store_rb(const Prob& pr, const GemmArgs& A, int m0, int rows,
+                                         int n0, int N, int h, int rb, const float (&v)[kBlk][16]) {
+#pragma unroll
+  for (int ob = 0; ob < kBlk / MATS; ++ob) {
+    const int n = n0 + 32 * ob;
+    if (n < N) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m < rows) {
+          h16 o;
+          if (MATS == 2) {
+            // silu(g) * u in fp32 from the fp16-rounded projections; the
+            // fast exp / reciprocal are well inside the fp16 rounding
+            const float gv = (float)(h16)v[0][r];
+            const float uv = (float)(h16)v[1][r];
+            o = (h16)(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
+          } else {
+            o = (h16)v[ob][r];
+          }
+          pr.out[(long)(m0 + m) * A.ld_o + n] = o;
+        }
+      }
+    }
+  }
+}
+
 template <bool GROUPED, int MATS, int RBM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOccW))) void gemm_kernel(
     GemmArgs A, const GExpert* __restrict__ table, const int* __restrict__ active,
@@ -489,8 +613,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
   constexpr int WN = kWaves * 32 * kBlk / MATS;  // output columns per tile
   using L = Stage;
   __shared__ __align__(16) unsigned char lds[kNST * L::kSize];
-  __shared__ int toff[kMaxProb + 1];
-  __shared__ int thalf[kMaxProb + 1];
+  __shared__ int toff[kMaxProb + 1];   // full M-tiles, prefix
+  __shared__ int thalf[kMaxProb + 1];  // tail M-tiles (0 / 1 per problem), prefix
+  __shared__ int twt[kMaxProb];        // row blocks of each problem's tail M-tile
+  __shared__ long tunit[kMaxProb + 1]; // stream-K units of the tails, prefix
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -499,6 +625,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
   const int N = A.N;
   const int T = A.K / kKS;
   const int NT = (N + WN - 1) / WN;
+  const bool sk = A.part != nullptr;
+  const int CH = sk ? A.sk_ch : T;
+  const int NCH = T / CH;  // chunks per tile
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds;
   DeqRegs dr;
   dr.m_pair = A.m_pair;
@@ -506,105 +635,104 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
   dr.mul = hn_vgpr(0x2C003C00u);  // half2(1, 0.0625)
   dr.add = hn_vgpr(0xD480E408u);  // half2(-1032, -72)
 
-  // ---- M-tiles per problem: toff[] = prefix of the full ones, thalf[] of
-  //      the short remainders (RBM 8: a last M-tile of <= 128 rows, run by the
-  //      4-block K loop at about half the cost).  The work is two passes, the
-  //      full tiles, then the short ones, each spread evenly over the
-  //      workgroups.
+  // ---- M-tiles per problem
   int nprob = 1;
-  auto count = [&](int rows_p, int& nf, int& nh) {
+  auto count = [&](int rows_p, int& nf, int& nh, int& w) {
     const int mt = (rows_p + BM - 1) / BM;
     const int rem = rows_p - (mt - 1) * BM;
-    nh = (RBM == 8 && mt > 0 && rem <= 128) ? 1 : 0;
+    const int nrb = ((rem + 63) / 64) * 2;  // even row blocks covering the last M-tile
+    const bool tail = mt > 0 && nrb < RBM;
+    nh = tail ? 1 : 0;
     nf = mt - nh;
+    w = tail ? nrb : 0;
   };
   if (GROUPED) {
     nprob = min(*n_active, kMaxProb);
     for (int i = tid; i < nprob; i += blockDim.x) {
       const int e = active[i];
-      int nf, nh;
-      count(offsets[e + 1] - offsets[e], nf, nh);
+      int nf, nh, w;
+      count(offsets[e + 1] - offsets[e], nf, nh, w);
       toff[i + 1] = nf;
       thalf[i + 1] = nh;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      toff[0] = 0;
-      thalf[0] = 0;
-      for (int i = 1; i <= nprob; ++i) {
-        toff[i] += toff[i - 1];
-        thalf[i] += thalf[i - 1];
-      }
+      twt[i] = w;
     }
   } else if (tid == 0) {
-    int nf, nh;
-    count(A.M, nf, nh);
-    toff[0] = 0;
+    int nf, nh, w;
+    count(A.M, nf, nh, w);
     toff[1] = nf;
-    thalf[0] = 0;
     thalf[1] = nh;
+    twt[0] = w;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    toff[0] = 0;
+    thalf[0] = 0;
+    tunit[0] = 0;
+    for (int i = 0; i < nprob; ++i) {
+      toff[i + 1] += toff[i];
+      thalf[i + 1] += thalf[i];
+      tunit[i + 1] = tunit[i] + (twt[i] ? (long)NT * NCH * (twt[i] + kTailC) : 0);
+    }
   }
   __syncthreads();
   if (nprob <= 0) return;
   const int tot_f = __builtin_amdgcn_readfirstlane(toff[nprob]) * NT;   // full tiles
-  const int tot_h = __builtin_amdgcn_readfirstlane(thalf[nprob]) * NT;  // short tiles
+  const int tot_h = __builtin_amdgcn_readfirstlane(thalf[nprob]) * NT;  // tail tiles
   const int nwg = gridDim.x;
   const int bid = blockIdx.x;
   // workgroups are dealt round-robin to the 8 XCDs: give each XCD a
   // contiguous run of tile numbers
   const int vid = (nwg % 8 == 0) ? (bid % 8) * (nwg / 8) + bid / 8 : bid;
 
-  // Work items: whole tiles round-robin, or (stream-K) this rank's range of
-  // (tile, chunk of A.sk_ch stages) iterations of each pass, ranks = min(grid,
-  // iterations) so that no range is empty and a tile's segments belong to
-  // consecutive ranks.  A segment starts the K loop at stage 0 of tile
-  // pointers moved to its first chunk (whole scale dwords), so the loop never
-  // starts at a run-time stage.
-  const bool sk = A.part != nullptr;
-  const int CH = sk ? A.sk_ch : T;
-  const int NCH = T / CH;  // chunks per tile
-  int pass = 0;
-  long it = 0, it_end = 0, it_total = 0;
-  int nr = 1;
-  int tile_rr = vid;
-  auto start_pass = [&](int ps) {
-    pass = ps;
-    const int tot = ps == 0 ? tot_f : tot_h;
-    it_total = (long)tot * NCH;
-    nr = (int)max(1L, min((long)nwg, it_total));
-    it = sk && vid < nr ? it_total * vid / nr : 0;
-    it_end = sk && vid < nr ? it_total * (vid + 1) / nr : 0;
-    tile_rr = vid;
-  };
-  start_pass(0);
+  // full tiles taken whole, round-robin; the stream-K plan for the rest
+  const int R = sk ? tot_f - tot_f % nwg : tot_f;
+  SkPlan sp;
+  sp.RF = tot_f - R;
+  sp.wF = RBM + kTailC;
+  sp.NT = NT;
+  sp.NCH = NCH;
+  sp.nprob = nprob;
+  sp.thalf = thalf;
+  sp.wt = twt;
+  sp.upre = tunit;
+  sp.U = sp.UF() + tunit[nprob];
+  sp.nr = (int)max(1L, min((long)nwg, sp.U / (RBM + kTailC)));
+  // A segment starts the K loop at stage 0 of tile pointers moved to its
+  // first chunk (whole scale dwords), so the loop never starts at a
+  // run-time stage.
+  long it = 0, it_end = 0;  // stream-K: this rank's chunk range
+  if (sk && vid < sp.nr) {
+    it = sp.chunk_at(sp.bound(vid));
+    it_end = sp.chunk_at(sp.bound(vid + 1));
+  }
+  int g_rr = vid;  // next whole tile (round-robin): full tiles < R, then (no workspace) tails
+  const int tot_rr = sk ? R : tot_f + tot_h;
   while (true) {
-    int tile, c0, c1;
-    if (sk) {
-      if (it >= it_end) {
-        if (pass == 0) { start_pass(1); continue; }
-        break;
-      }
-      tile = (int)(it / NCH);
-      c0 = (int)(it - (long)tile * NCH);
-      c1 = (int)min((long)NCH, (long)c0 + (it_end - it));
-      it += c1 - c0;
-    } else {
-      if (tile_rr >= (pass == 0 ? tot_f : tot_h)) {
-        if (pass == 0) { start_pass(1); continue; }
-        break;
-      }
-      tile = tile_rr;
+    int g, c0, c1;   // tile number (full ones first, then tails), its chunks
+    int item = -1;   // stream-K item (>= 0: counters and slots)
+    if (g_rr < tot_rr) {
+      g = g_rr;
+      g_rr += nwg;
       c0 = 0;
       c1 = NCH;
-      tile_rr += nwg;
+    } else if (it < it_end) {
+      item = (int)(it / NCH);
+      c0 = (int)(it - (long)item * NCH);
+      c1 = (int)min((long)NCH, (long)c0 + (it_end - it));
+      it += c1 - c0;
+      g = item < sp.RF ? R + item : tot_f + (item - sp.RF);
+    } else {
+      break;
     }
-    tile = __builtin_amdgcn_readfirstlane(tile);
+    g = __builtin_amdgcn_readfirstlane(g);
     c0 = __builtin_amdgcn_readfirstlane(c0);
     c1 = __builtin_amdgcn_readfirstlane(c1);
     const int k0 = c0 * CH * kKS;               // first k of this segment
     const int nst = (c1 - c0) * CH;              // its stages
-    // ---- tile -> (problem, m-tile, n-tile)
-    const int* pref = pass == 0 ? toff : thalf;
+    // ---- tile -> (problem, m-tile, n-tile, row blocks)
+    const bool tail = g >= tot_f;
+    const int tile = tail ? g - tot_f : g;
+    const int* pref = tail ? thalf : toff;
     int p = 0;
     {
       const int mg = tile / NT;  // pref[p] <= mg < pref[p + 1]
@@ -615,8 +743,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
       }
       p = __builtin_amdgcn_readfirstlane(lo);  // uniform: keep the tile state in SGPRs
     }
-    int mtile, ntile;
-    if (pass == 0) {
+    int mtile, ntile, nrb;
+    if (!tail) {
       const int pt0 = __builtin_amdgcn_readfirstlane(toff[p]);
       const int mtp = __builtin_amdgcn_readfirstlane(toff[p + 1]) - pt0;
       const int local = tile - pt0 * NT;
@@ -626,29 +754,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
       const int inb = local - sb * kSuperM * NT;
       mtile = sm0 + inb % sbm;
       ntile = inb / sbm;
+      nrb = RBM;
     } else {
-      // the problem's short M-tile comes after its full ones
+      // the problem's tail M-tile comes after its full ones
       mtile = __builtin_amdgcn_readfirstlane(toff[p + 1] - toff[p]);
       ntile = tile - __builtin_amdgcn_readfirstlane(thalf[p]) * NT;
+      nrb = __builtin_amdgcn_readfirstlane(twt[p]);
     }
-    const int ctile = pass == 0 ? tile : tot_f + tile;  // counter index
     const Prob pr = resolve<GROUPED>(A, table, active, offsets, p);
     const int m0 = mtile * BM;
     const int rows = min(BM, pr.rows - m0);
-    const bool full = RBM == 8 && rows > 128;  // uniform: the 8-block K loop
     // output column of this lane in block 0
     const int n0 = ntile * WN + wave * 32 * kBlk / MATS + row32;
 
     TileLoads tl;
     tl.px = pr.x + (long)m0 * A.ld_x + k0;
     tl.nx = (int)(rows * A.ld_x * 2 - 2 * k0);
-    if (full) {
-#pragma unroll
-      for (int j = 0; j < a_loads<8>(); ++j) tl.va[j] = a_offset<8>(j, wave, lane, rows, A.ld_x);
-    } else {
-#pragma unroll
-      for (int j = 0; j < a_loads<4>(); ++j) tl.va[j] = a_offset<4>(j, wave, lane, rows, A.ld_x);
-    }
     tl.nq = N * A.ld_q - k0 / 2;
     tl.ns = (N * A.ld_s - k0 / A.group) * 2;
     tl.group = A.group;
@@ -672,74 +793,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kOccW, kOcc
 
     // the previous tile's last reads of the stages end before anyone restages
     __syncthreads();
-    if constexpr (RBM == 8) {
-      if (full) k_loop<8>(tl, 0, nst, lds0, row32, h, wave, lane, dr, acc);
-      else k_loop<4>(tl, 0, nst, lds0, row32, h, wave, lane, dr, acc);
-    } else {
-      k_loop<4>(tl, 0, nst, lds0, row32, h, wave, lane, dr, acc);
-    }
+    if (RBM == 8 && nrb == 8)
+      tile_k<RBM>(tl, rows, A.ld_x, nst, lds0, row32, h, wave, lane, dr, acc);
+    else if (RBM == 8 && nrb == 6)
+      tile_k<(RBM == 8 ? 6 : 2)>(tl, rows, A.ld_x, nst, lds0, row32, h, wave, lane, dr, acc);
+    else if (nrb == 4)
+      tile_k<4>(tl, rows, A.ld_x, nst, lds0, row32, h, wave, lane, dr, acc);
+    else
+      tile_k<2>(tl, rows, A.ld_x, nst, lds0, row32, h, wave, lane, dr, acc);
     if (c0 != 0 || c1 != NCH) {  // a segment of the tile (uniform)
       SkSeg sgi;
-      if (!streamk_arrive<RBM>(A, acc, full ? 8 : 4, tile, ctile, pass, NCH, it_total, nr, vid,
-                               wave, lane, sgi))
+      if (!streamk_arrive<RBM>(A, sp, acc, nrb, item, p, vid, wave, lane, sgi))
         continue;  // another segment finishes this wave's part of the tile
       // last segment: the epilogue from the partial slots (acc no longer used)
 #pragma unroll 1
-      for (int rb = 0; rb < (full ? 8 : 4); ++rb) {
-#pragma unroll
-        for (int ob = 0; ob < kBlk / MATS; ++ob) {
-          const int n = n0 + 32 * ob;
-          float g[16], u[16];
-          sk_sum16(A, sgi, tile, pass, NCH, it_total, nr, wave, lane, rb, MATS == 2 ? 0 : ob, g);
-          if (MATS == 2) sk_sum16(A, sgi, tile, pass, NCH, it_total, nr, wave, lane, rb, 1, u);
-          if (n < N) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int m = 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3);
-              if (m < rows) {
-                h16 o;
-                if (MATS == 2) {
-                  const float gv = (float)(h16)g[r];
-                  const float uv = (float)(h16)u[r];
-                  o = (h16)(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
-                } else {
-                  o = (h16)g[r];
-                }
-                pr.out[(long)(m0 + m) * A.ld_o + n] = o;
-              }
-            }
-          }
-        }
+      for (int rb = 0; rb < nrb; ++rb) {
+        float v[kBlk][16];
+        sk_sum_rb(A, sp, sgi, item, wave, lane, rb, v);
+        store_rb<MATS>(pr, A, m0, rows, n0, N, h, rb, v);
       }
       continue;
     }
 
-    // ---- epilogue: lane holds column n, tokens 32 rb + 8 (r / 4) + 4 h + r % 4
+    // ---- epilogue from the accumulators
 #pragma unroll
-    for (int ob = 0; ob < kBlk / MATS; ++ob) {
-      const int n = n0 + 32 * ob;
-      if (n < N) {
+    for (int rb = 0; rb < RBM; ++rb) {
+      float v[kBlk][16];
 #pragma unroll
-        for (int rb = 0; rb < RBM; ++rb) {
+      for (int b = 0; b < kBlk; ++b)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int m = 32 * rb + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (m < rows) {
-              h16 o;
-              if (MATS == 2) {
-                // silu(g) * u in fp32 from the fp16-rounded projections; the
-                // fast exp / reciprocal are well inside the fp16 rounding
-                const float gv = (float)(h16)acc[rb][0][r];
-                const float uv = (float)(h16)acc[rb][1][r];
-                o = (h16)(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
-              } else {
-                o = (h16)acc[rb][ob][r];
-              }
-              pr.out[(long)(m0 + m) * A.ld_o + n] = o;
-            }
-          }
-        }
-      }
+        for (int r = 0; r < 16; ++r) v[b][r] = acc[rb][b][r];
+      store_rb<MATS>(pr, A, m0, rows, n0, N, h, rb, v);
     }
   }
 }
@@ -769,14 +853,14 @@ int grid_for(long tiles_upper) {
   return (int)(tiles_upper < cap ? (tiles_upper < 1 ? 1 : tiles_upper) : cap);
 }
 
-// Stream-K workspace: per-(tile, wave) counters, then four partial slots per
-// workgroup of the full grid (the first and last tile of each pass).
+// Stream-K workspace: per-(item, wave) counters, then two partial slots per
+// workgroup of the full grid (its first and its last item).
 constexpr long kSkCounters = 1L << 16;          // tiles * kWaves
 constexpr long kSkCtrBytes = kSkCounters * 8;
 constexpr int kSkMaxGrid = 256;   // workgroups (one per CU on MI355X)
 static_assert(kSkMaxGrid <= kHnMaxArrivals, "segments per tile fit a counter");
 
-long sk_bytes() { return kSkCtrBytes + 4L * kSkMaxGrid * kWaves * kWaveSlot * 4; }
+long sk_bytes() { return kSkCtrBytes + 2L * kSkMaxGrid * kWaves * kWaveSlot * 4; }
 
 // Stream-K over the full grid when the workspace holds its counters and slots
 // (then every CU takes an equal share of the k-stages, tiles split at the

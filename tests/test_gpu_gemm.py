@@ -80,6 +80,30 @@ def test_int4_linear_gemm(M, N, K, g):
     _close(got, ref)
 
 
+@pytest.mark.parametrize("M", [129, 200, 296, 356, 406, 486, 769])
+@pytest.mark.parametrize("streamk", [True, False])
+def test_int4_linear_gemm_tail_tiles(M, streamk):
+    """Last M-tiles of every size class -- 2, 4 and 6 row blocks of 32 (129:
+    a single 6-block tile, no full one), a full 8-block tile (200, 486) --
+    with the stream-K workspace (tails dealt out by weight) and without it
+    (whole tiles round-robin), against the fp32 product over the oracle's
+    dequantised weights."""
+    from hydranet_amd import _lib
+    N, K, g = 1408, 2048, 128
+    w = _rand_f16(M + 3, (N, K), 0.02)
+    x = _rand_f16(M + 4, (M, K), 1.0).to(DEV)
+    p, s = oracle.quantize(w.numpy(), g, mode=0)
+    pd, sd = torch.from_numpy(p).to(DEV), torch.from_numpy(s.copy()).to(DEV)
+    out = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
+    work = _lib.gemm_workspace(x.device) if streamk else None
+    _lib.call("hn_int4_linear", _lib.ptr(x), x.stride(0), _lib.ptr(pd), pd.stride(0),
+              _lib.ptr(sd), sd.stride(0), _lib.ptr(out), out.stride(0), M, N, K, g,
+              _lib.ptr(work) if streamk else None, work.numel() if streamk else 0,
+              _lib.stream(x.device))
+    torch.cuda.synchronize()
+    _close(out, (x.float() @ _deq32(pd, sd, g).t()).half())
+
+
 def test_int4_linear_gemm_strided_rows():
     """x with a row stride larger than K (a column slice) goes through the GEMM."""
     from hydranet_amd.kernels.int4_gemm import int4_linear
