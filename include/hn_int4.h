@@ -52,10 +52,12 @@ long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long E);
 /* Workspace bytes of the prefill (MFMA GEMM) kernels' stream-K split: fp32
  * partial slots for two tile segments per workgroup plus per-(tile, wave)
  * counters.  Passed (zero-filled once; the kernels leave the counters at zero)
- * as the work argument of the entry points below at prefill sizes, it makes
- * every CU take an equal share of the (tile, k-stage) iterations, tiles split
- * at the shares' ends being summed in a fixed order by the last segment to
- * finish.  No counterpart in the reference (Triton's GEMM takes no workspace). */
+ * as the work argument of the entry points below at prefill sizes, it lets
+ * the tiles short of a whole round over the CUs (and the experts' last,
+ * shorter M-tiles) be split over every CU by cost-weighted (tile, k-chunk)
+ * iterations, tiles split at the shares' ends being summed in a fixed order
+ * by the last segment to finish.  No counterpart in the reference (Triton's
+ * GEMM takes no workspace). */
 long hn_gemm_workspace_bytes(void);
 
 /* out[M, N] = fp16(x[M, K] @ deq(W)^T), fp32 accumulation.  Replaces the
@@ -146,8 +148,8 @@ int hn_moe_unpermute(const void* y_perm, long ld_y, const int* inv, const int* i
  * y_perm [rows, H] fp16 out; work: hn_skinny_workspace_bytes(3, rows, H, I, E),
  * zero-filled once.  Above 64 rows per expert (the MFMA GEMM kernels) work
  * may instead hold hn_gemm_workspace_bytes() bytes, which enables their
- * stream-K split of the k-stages over the CUs, or be NULL (whole tiles go
- * round-robin).
+ * stream-K split of the remainder tiles over the CUs, or be NULL (whole
+ * tiles go round-robin).
  * Replaces the per-expert loop calling expert_mlp_int4_fused
  * (model/mixtral.py:327-354, model/glm4.py:421-455). */
 int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int* active,
