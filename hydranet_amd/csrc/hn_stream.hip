@@ -567,6 +567,11 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   const long G = K / 128;
   int lpw = 2;
   while (lpw < 16 && (G + lpw - 1) / lpw > kMaxWaves) lpw *= 2;
+  // grouped single-matrix (down) launches: at least four groups per wave --
+  // fewer waves per workgroup, more workgroups per CU (below); measured on
+  // GLM's down projection (K = 1408): 2 groups x 6 waves, 2 workgroups per CU
+  // 92 us, 4 groups x 3 waves, 4 workgroups per CU 79 us
+  if (mats == 1 && grouped && !route && lpw < 4) lpw = 4;
   const long kw = (G + lpw - 1) / lpw;
   if (kw > kMaxWaves || rows < 1 || K % 128 != 0) return p;
   p.lpw = lpw;
@@ -592,12 +597,16 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
     if (p.tc < 1) return p;
     p.lds = p.tc * per_tok + cs + red + meta;
     if (route && p.tc * per_tok + cs + red < kRouteScratch) return p;
-    // single-matrix (down) launches of 4 or more rows per matrix: two
-    // workgroups per CU when their LDS and waves fit, for more loads in flight
-    // where a column has little work (measured: gate/up launches and 1-row
-    // launches are faster with one)
-    p.occ = (mats == 1 && !route && rows >= 4 && 2 * (p.lds + kStaticLds) <= kLdsPerCu &&
-             2 * kw <= 16) ? 2 : 1;
+    // single-matrix (down) launches of 4 or more rows per matrix: as many
+    // workgroups per CU (up to four) as their LDS and 16 waves allow, for more
+    // loads in flight where a column has little work (measured: gate/up
+    // launches and 1-row launches are faster with one); launch_one caps this
+    // by what the registers allow
+    p.occ = 1;
+    if (mats == 1 && !route && rows >= 4)
+      while (p.occ < 4 && (p.occ + 1) * (p.lds + kStaticLds) <= kLdsPerCu &&
+             (p.occ + 1) * kw <= 16)
+        ++p.occ;
     p.ok = true;
     return p;
   }
