@@ -11,9 +11,10 @@
 // This is the one place the path is a real dense contraction, so it is built
 // around the MFMA pipe (v_mfma_f32_32x32x16_f16, which one wave per SIMD can
 // keep busy back to back):
-//  * Tile = up to 256 tokens (eight 32-token row blocks; a tile whose rows
-//    fit in 128 runs the four-block loop) x 256 weight rows, one workgroup of
-//    four waves per CU; a wave owns 64 weight rows -- one 32-row block of gate
+//  * Tile = up to 256 tokens (eight 32-token row blocks; an expert's last
+//    M-tile runs the 2, 4 or 6 blocks that cover its rows) x 256 weight rows,
+//    one workgroup of four waves per CU; a wave owns 64 weight rows -- one
+//    32-row block of gate
 //    and the same rows of up (so the SwiGLU epilogue has both values of an
 //    output in one lane), or two 32-row blocks of one matrix -- for all the
 //    tile's tokens.  Waves split N, never M, so each weight is dequantised by
@@ -25,7 +26,7 @@
 //  * Each k-step's A fragments and unpacked weights are double-buffered: step
 //    s + 1's LDS reads and unpack are issued ahead of / under step s's MFMAs.
 //    A packed dword becomes eight fp16 weights in k order: a byte broadcast
-//    (v_perm_b32) and one v_and_or_b32 put two nibbles in the mantissas of
+//    (v_perm_b32) and one bit-field insert put two nibbles in the mantissas of
 //    1024 (0x6400), one v_pk_fma_f16 gives the exact (n - 8) pair, and
 //    v_pk_mul_f16 by the fp16 scale rounds the exact product once: the
 //    reference's dequantised weight bit for bit.
@@ -34,10 +35,11 @@
 //    super-blocks of up to 8 M-tiles x n-tiles, and workgroups on one XCD
 //    take consecutive numbers, so tiles running together on an XCD share
 //    activation and weight slices in its L2.
-//  * Single problems with a caller workspace run stream-K: the (tile, stage)
-//    iterations are split evenly over the grid, and a tile whose stages span
-//    several workgroups is summed by its last-arriving wave from fp32
-//    partials (tagged counters, agent-scope acquire, hn_arrive).
+//  * With a caller workspace, whole rounds of full tiles go round-robin and
+//    the rest is split stream-K by cost-weighted (tile, chunk) iterations; a
+//    tile whose chunks span several workgroups is summed by its last-arriving
+//    wave from fp32 partials (tagged counters, agent-scope acquire,
+//    hn_arrive).
 #include "hn_common.h"
 
 namespace {
@@ -66,11 +68,12 @@ struct GemmArgs {
   int ld_q;         // packed row stride (bytes)
   int ld_s;         // scale row stride (elements)
   uint32_t m_pair, magic;
-  // stream-K (part != nullptr): the workgroups split the (tile, k-stage)
-  // iterations evenly; a tile whose stages span several workgroups is summed
-  // from fp32 partial slots by the last of them to arrive (per wave).
-  float* part;      // [4 * grid][kWaves][kWaveSlot]
-  unsigned long long* ctr;  // [tiles * kWaves] tagged counters (hn_arrive), left zero
+  // stream-K (part != nullptr): the tiles short of a whole round are split by
+  // cost-weighted (tile, chunk) iterations; a tile whose chunks span several
+  // workgroups is summed from fp32 partial slots by the last of them to
+  // arrive (per wave).
+  float* part;      // [2 * grid][kWaves][kWaveSlot]
+  unsigned long long* ctr;  // [items * kWaves] tagged counters (hn_arrive), left zero
   unsigned long long tag;   // this launch's counter tag (hn_next_tag)
   int sk_ch;        // stages per stream-K chunk (chunks start on whole scale groups)
 };
@@ -368,7 +371,7 @@ __device__ __forceinline__ void sched_step() {
 // barrier (every wave's activation loads of t + 1 now visible, every read of
 // stage t done) and reads the next stage's first A fragments under the last
 // POST MFMAs.  Every stage issues the same loads (dummies past the end), so
-// the waits take no branch.
+// the waits take no branch; the loop ends waiting for all of them.
 template <int NRB>
 __device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int te, uint32_t lds0,
                                        int row32, int h, int wave, int lane, const DeqRegs& dr,
@@ -426,6 +429,11 @@ __device__ __forceinline__ void k_loop(const TileLoads& tl, int tb, int te, uint
     __builtin_amdgcn_sched_barrier(0);
     sc = s1;
   }
+  // the last stages' dummy loads have landed before the K loop returns: the
+  // next tile's loads (after a barrier) may write the same LDS bytes from
+  // another wave when its row blocks differ, and loads of different waves
+  // land in no fixed order
+  wait_vmcnt<0>();
 }
 
 // Stream-K partial slots: one wave's accumulators (kRBMax x kBlk 32x32 fp32
