@@ -104,6 +104,26 @@ def test_int4_linear_gemm_tail_tiles(M, streamk):
     _close(out, (x.float() @ _deq32(pd, sd, g).t()).half())
 
 
+def test_int4_linear_gemm_rounds_and_streamk():
+    """One problem whose work has all three parts: a whole round of full
+    tiles taken round-robin (4 M-tiles x 80 n-tiles = 320 full tiles, 256 of
+    them in the round), the 64 full tiles short of a second round and the
+    4-row-block tail (1100 = 4 x 256 + 76 rows) split stream-K by weight."""
+    from hydranet_amd import _lib
+    M, N, K, g = 1100, 20480, 4096, 128
+    w = _rand_f16(91, (N, K), 0.02)
+    x = _rand_f16(92, (M, K), 1.0).to(DEV)
+    p, s = oracle.quantize(w.numpy(), g, mode=0)
+    pd, sd = torch.from_numpy(p).to(DEV), torch.from_numpy(s.copy()).to(DEV)
+    out = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
+    work = _lib.gemm_workspace(x.device)
+    _lib.call("hn_int4_linear", _lib.ptr(x), x.stride(0), _lib.ptr(pd), pd.stride(0),
+              _lib.ptr(sd), sd.stride(0), _lib.ptr(out), out.stride(0), M, N, K, g,
+              _lib.ptr(work), work.numel(), _lib.stream(x.device))
+    torch.cuda.synchronize()
+    _close(out, (x.float() @ _deq32(pd, sd, g).t()).half())
+
+
 def test_int4_linear_gemm_strided_rows():
     """x with a row stride larger than K (a column slice) goes through the GEMM."""
     from hydranet_amd.kernels.int4_gemm import int4_linear
