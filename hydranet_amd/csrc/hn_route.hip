@@ -318,10 +318,18 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
   } else if constexpr (LG > 0) {
     const int ksl = H >> 4, kb0 = wave * ksl, steps = ksl >> 5;
     const int tl = lane & 15, kq = (lane >> 4) * 8;
+    // lanes past the T tokens / E experts load nothing (their products are
+    // never read): their MFMA operand is zero
     const h16* ap[LG];
+    bool a_on[LG];
 #pragma unroll
-    for (int u = 0; u < LG; ++u) ap[u] = h + (long)min(16 * u + tl, T - 1) * ld_h + kb0 + kq;
+    for (int u = 0; u < LG; ++u) {
+      ap[u] = h + (long)min(16 * u + tl, T - 1) * ld_h + kb0 + kq;
+      a_on[u] = 16 * u + tl < T;
+    }
     const h16* bp = reinterpret_cast<const h16*>(w) + (long)min(tl, E - 1) * ld_w + kb0 + kq;
+    const bool b_on = tl < E;
+    const half8_t z8 = {};
     float4_t acc[LG];
 #pragma unroll
     for (int u = 0; u < LG; ++u) acc[u] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -333,9 +341,10 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
 #pragma unroll
       for (int i = 0; i < KST; ++i) {
         const int st = min(s0 + i, steps - 1);
-        bv[i] = *reinterpret_cast<const half8_t*>(bp + 32 * st);
+        bv[i] = b_on ? *reinterpret_cast<const half8_t*>(bp + 32 * st) : z8;
 #pragma unroll
-        for (int u = 0; u < LG; ++u) av[i][u] = *reinterpret_cast<const half8_t*>(ap[u] + 32 * st);
+        for (int u = 0; u < LG; ++u)
+          av[i][u] = a_on[u] ? *reinterpret_cast<const half8_t*>(ap[u] + 32 * st) : z8;
       }
 #pragma unroll
       for (int i = 0; i < KST; ++i) {
