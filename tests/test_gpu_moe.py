@@ -472,6 +472,42 @@ def test_decode_layer_fused_routing_matches_route_then_experts(T, mixtral_expert
     assert torch.equal(out2, moe_dispatch(moe_route(x2, 2, 0, gate_w=gw), table))
 
 
+@pytest.mark.parametrize("case", ["all_active", "one_idle", "one_over_a_chunk"])
+def test_decode_layer_skewed_routings(case, mixtral_experts):
+    """hn_moe_decode_layer at T = 16, top-2 over 8 experts under routings that
+    change the kernel's column layout: every expert active with at most 8 rows
+    (one 8-token chunk each), expert 7's gate row steered against every token
+    (its logit about -10: never chosen, 7 active experts), or expert 0's
+    towards every token (16 rows: two chunks).  The layer equals hn_moe_route
+    + hn_moe_experts_decode bit for bit in each case."""
+    from hydranet_amd.model.moe import ExpertTable, moe_decode_layer, moe_dispatch, moe_route
+    slots, _ = mixtral_experts
+    table = ExpertTable.from_slots(slots)
+    T = 16
+    g = torch.Generator().manual_seed(91)
+    x = torch.randn(T, 4096, generator=g)
+    gw = torch.randn(8, 4096, generator=g) * 0.02
+    steer = x.sum(0) * (10.0 / 4096)  # h_t . steer ~ 10 for every token t
+    if case == "one_idle":
+        gw[7] = -steer
+    elif case == "one_over_a_chunk":
+        gw[0] = steer
+    x, gw = x.half().to(DEV), gw.half().to(DEV)
+    r0 = moe_route(x, 2, 0, gate_w=gw)
+    counts = torch.bincount(r0.idx.view(-1).long().cpu(), minlength=8)
+    if case == "all_active":
+        assert bool((counts > 0).all()) and int(counts.max()) <= 8
+    elif case == "one_idle":
+        assert counts[7] == 0 and int(r0.n_active.item()) == 7
+    elif case == "one_over_a_chunk":
+        assert counts[0] == T
+    ref = moe_dispatch(r0, table)
+    out, r1 = moe_decode_layer(x, gw, 2, table)
+    torch.cuda.synchronize()
+    assert torch.equal(r1.idx, r0.idx) and torch.equal(r1.offsets, r0.offsets)
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("T,k", [(1, 1), (4, 1), (16, 2), (20, 1), (32, 2), (64, 1)])
 def test_decode_layer_with_given_logits_matches_route_then_experts(T, k, mixtral_experts):
     """hn_moe_decode_layer fed the router logits (as the decoder's norm kernel
