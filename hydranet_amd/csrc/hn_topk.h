@@ -60,10 +60,14 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 // Top-k of one token's logits row by one wave: lanes hold experts lane +
 // 64 j (E <= 256).  The k-th largest candidate key is found by bisection over
 // its 32 bits (one ballot per bit and candidate register: no lane exchanges),
-// ties at that key go to the lower experts, and each selected candidate's
-// place in the (value desc, expert asc) order is the number of selected
-// candidates ahead of it.  Same selection and weight arithmetic as topk_small /
-// topk_weights: the sums over the selected experts run in selection order.
+// ties at that key go to the lower experts.  The selected candidates (at most
+// k <= 16) are then moved to lanes 0..k-1 in expert order (ds_permute to
+// their rank among the selected), each finds its place in the (value desc,
+// expert asc) order against the others (readlane over the k lanes), and a
+// second ds_permute puts them in selection order, so the weight sums read
+// lane p for the p-th selected.  Same selection and weight arithmetic as
+// topk_small / topk_weights: the sums over the selected experts run in
+// selection order.
 __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int E, int k,
                                           int mode, float eps, float scaling, int lane,
                                           int* idx_o, h16* w_o) {
@@ -112,57 +116,67 @@ __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int
     sel[j] = key[j] > t || (eq && above + tie + __popcll(m & lt) < k);
     tie += __popcll(m);
   }
-  // place of each selected candidate: selected candidates ahead of it
-  int pos[NJ] = {0, 0, 0, 0};
+  // 1. the selected to lanes 0..ns-1 in expert order: the candidate of rank
+  //    r among the selected sends (key, expert, raw) to lane r; the others
+  //    send to lane 63 (>= 16 > ns), whose values are never read
+  int ns = 0;
+  uint32_t ck = 0u;
+  int ce = 0;
+  float cr = 0.f;
 #pragma unroll
-  for (int jr = 0; jr < NJ; ++jr) {
-    uint64_t m = __ballot(sel[jr]);
-    while (m) {
-      const int L = __builtin_ctzll(m);
-      m &= m - 1;
-      const uint32_t kr = __builtin_amdgcn_readlane(key[jr], L);
-      const int er = L + 64 * jr;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int e = lane + 64 * j;
-        if (sel[j] && (kr > key[j] || (kr == key[j] && er < e))) ++pos[j];
+  for (int j = 0; j < NJ; ++j) {
+    const uint64_t m = __ballot(sel[j]);
+    const int cnt = __popcll(m);
+    if (cnt) {  // uniform
+      const int dst = 4 * (sel[j] ? ns + __popcll(m & lt) : 63);
+      const uint32_t pk = (uint32_t)__builtin_amdgcn_ds_permute(dst, (int)key[j]);
+      const int pe = __builtin_amdgcn_ds_permute(dst, lane + 64 * j);
+      const float pr =
+          __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(dst, __builtin_bit_cast(int, raw[j])));
+      if (lane >= ns && lane < ns + cnt) {
+        ck = pk;
+        ce = pe;
+        cr = pr;
       }
+      ns += cnt;
     }
   }
-  // the selected raw values in selection order, on every lane
-  auto at = [&](int r) -> float {
-    float x = 0.f;
+  // 2. place of lane r's candidate: selected candidates ahead of it (a larger
+  //    key, or an equal key and a lower expert = a lower lane)
+  int pos = 0;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const uint64_t m = __ballot(sel[j] && pos[j] == r);
-      if (m) x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                     __builtin_bit_cast(int, raw[j]), __builtin_ctzll(m)));
+  for (int s = 0; s < kMaxTopK; ++s) {
+    if (s < ns) {  // uniform
+      const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)ck, s);
+      pos += (ks > ck || (ks == ck && s < lane)) ? 1 : 0;
     }
-    return x;
+  }
+  // 3. lane p holds the p-th selected (expert, raw)
+  const int dst = 4 * (lane < ns ? pos : 63);
+  const int oe = __builtin_amdgcn_ds_permute(dst, ce);
+  const float orr = __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(dst, __builtin_bit_cast(int, cr)));
+  auto at = [&](int r) -> float {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, orr), r));
   };
   if (mode == 0) {
     // fp32 softmax over the selected logits, renormalised (topk_weights)
     const float mx = at(0);
     float z = 0.f;
-    for (int r = 0; r < k; ++r) z += expf(at(r) - mx);
+    for (int r = 0; r < ns; ++r) z += expf(at(r) - mx);
     float sum = 0.f;
-    for (int r = 0; r < k; ++r) sum += expf(at(r) - mx) / z;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (sel[j]) {
-        idx_o[pos[j]] = lane + 64 * j;
-        w_o[pos[j]] = (h16)((expf(raw[j] - mx) / z) / sum);
-      }
+    for (int r = 0; r < ns; ++r) sum += expf(at(r) - mx) / z;
+    if (lane < ns) {
+      idx_o[lane] = oe;
+      w_o[lane] = (h16)((expf(orr - mx) / z) / sum);
+    }
   } else {
     float sum = 0.f;
-    for (int r = 0; r < k; ++r) sum += at(r);
+    for (int r = 0; r < ns; ++r) sum += at(r);
     const float d = sum + eps;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (sel[j]) {
-        idx_o[pos[j]] = lane + 64 * j;
-        w_o[pos[j]] = (h16)((raw[j] / d) * scaling);
-      }
+    if (lane < ns) {
+      idx_o[lane] = oe;
+      w_o[lane] = (h16)((orr / d) * scaling);
+    }
   }
 }
 
