@@ -413,16 +413,51 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 
 
 class GLM4DenseMLP(nn.Module):
-    """fp16 dense SwiGLU (model/glm4.py:220-235); shared expert of GLM4MoELayer."""
+    """fp16 dense SwiGLU (model/glm4.py:220-235); shared expert of GLM4MoELayer.
+
+    At inference the gate and up projections run as one GEMM over their
+    stacked weights: the two parameters are re-pointed into one [2I, H]
+    buffer on first use (no second copy), so every later call reads it with
+    a single launch.  Same fp16 Linear / SiLU / product sequence as the
+    reference; the stacked GEMM may pick another kernel than two separate
+    ones (fp32 summation order inside a dot product)."""
 
     def __init__(self, hidden_dim: int, intermediate_dim: int):
         super().__init__()
         self.gate_proj = nn.Linear(hidden_dim, intermediate_dim, bias=False)
         self.up_proj = nn.Linear(hidden_dim, intermediate_dim, bias=False)
         self.down_proj = nn.Linear(intermediate_dim, hidden_dim, bias=False)
+        self._stacked: Optional[torch.Tensor] = None
+
+    def _gate_up_weight(self) -> Optional[torch.Tensor]:
+        g, u = self.gate_proj, self.up_proj
+        if type(g) is not nn.Linear or type(u) is not nn.Linear or g.bias is not None \
+                or u.bias is not None:
+            return None  # e.g. converted to Int4Linear
+        wg, wu = g.weight, u.weight
+        if torch.is_grad_enabled() and (wg.requires_grad or wu.requires_grad):
+            return None
+        st = self._stacked
+        n = wg.shape[0]
+        if st is not None and wg.data_ptr() == st.data_ptr() and \
+                wu.data_ptr() == st[n:].data_ptr() and wg.shape == st[:n].shape and \
+                wu.shape == st[n:].shape:
+            return st
+        if wg.dtype != wu.dtype or wg.device != wu.device or wg.shape[1] != wu.shape[1]:
+            return None
+        st = torch.cat([wg.detach(), wu.detach()], 0).contiguous()
+        g.weight.data = st[:n]
+        u.weight.data = st[n:]
+        self._stacked = st
+        return st
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        w = self._gate_up_weight()
+        if w is None:
+            return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        n = self.gate_proj.out_features
+        gu = F.linear(x, w)
+        return self.down_proj(F.silu(gu[..., :n]) * gu[..., n:])
 
 
 class GLM4MoELayer(nn.Module):
