@@ -30,6 +30,7 @@ SIGNATURES: dict[str, list] = {
     "hn_int4_gate_up_silu": [P, L, P, P, P, P, L, L, P, L, L, L, L, L, P, L, P],
     "hn_expert_mlp_int4": [P, P, P, P, P, P, P, P, L, L, L, L, P, P, L, P],
     "hn_silu_mul": [P, L, P, L, P, L, L, L, P],
+    "hn_silu_then_mul": [P, L, P, L, P, L, L, L, P],
     "hn_router_logits": [P, L, P, L, I, P, L, L, L, P],
     "hn_router_topk": [P, P, L, L, L, I, F, F, P, P, P],
     "hn_moe_permute": [P, L, L, L, P, P, P, P, P, P],

@@ -422,6 +422,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void grouped_kernel(SkinnyArgs A) {
   }
 }
 
+// ROUND_SILU: the SiLU is rounded to fp16 before the product (two fp16
+// operations, as F.silu(g) * u on fp16 tensors), else one rounding.
+template <bool ROUND_SILU>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const h16* __restrict__ g, long ld_g,
                                                        const h16* __restrict__ u, long ld_u,
                                                        h16* __restrict__ o, long ld_o, int M,
@@ -432,7 +435,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const h16* __restrict__ g
   const int n = (int)(i - (long)m * N);
   const float gv = (float)g[(long)m * ld_g + n];
   const float uv = (float)u[(long)m * ld_u + n];
-  o[(long)m * ld_o + n] = (h16)(hn_silu(gv) * uv);
+  const float sv = ROUND_SILU ? (float)(h16)hn_silu(gv) : hn_silu(gv);
+  o[(long)m * ld_o + n] = (h16)(sv * uv);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -754,10 +758,21 @@ extern "C" int hn_silu_mul(const void* g, long ld_g, const void* u, long ld_u, v
                            long ld_o, long M, long N, void* stream) {
   HN_ARG_CHECK(M >= 0 && N >= 0, "hn_silu_mul: negative dims");
   if (M == 0 || N == 0) return 0;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3(hn_cdiv(M * N, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(silu_mul_kernel<false>, dim3(hn_cdiv(M * N, 256)), dim3(256), 0,
                      (hipStream_t)stream, (const h16*)g, ld_g, (const h16*)u, ld_u, (h16*)out,
                      ld_o, (int)M, (int)N);
   HN_LAUNCH_CHECK("hn_silu_mul");
+  return 0;
+}
+
+extern "C" int hn_silu_then_mul(const void* g, long ld_g, const void* u, long ld_u, void* out,
+                                long ld_o, long M, long N, void* stream) {
+  HN_ARG_CHECK(M >= 0 && N >= 0, "hn_silu_then_mul: negative dims");
+  if (M == 0 || N == 0) return 0;
+  hipLaunchKernelGGL(silu_mul_kernel<true>, dim3(hn_cdiv(M * N, 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const h16*)g, ld_g, (const h16*)u, ld_u, (h16*)out,
+                     ld_o, (int)M, (int)N);
+  HN_LAUNCH_CHECK("hn_silu_then_mul");
   return 0;
 }
 

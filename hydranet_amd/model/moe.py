@@ -418,9 +418,10 @@ class GLM4DenseMLP(nn.Module):
     At inference the gate and up projections run as one GEMM over their
     stacked weights: the two parameters are re-pointed into one [2I, H]
     buffer on first use (no second copy), so every later call reads it with
-    a single launch.  Same fp16 Linear / SiLU / product sequence as the
-    reference; the stacked GEMM may pick another kernel than two separate
-    ones (fp32 summation order inside a dot product)."""
+    a single launch; the SiLU and the product (two fp16 roundings, as
+    F.silu(g) * u) are one launch too.  Same fp16 Linear / SiLU / product
+    sequence as the reference; the stacked GEMM may pick another kernel than
+    two separate ones (fp32 summation order inside a dot product)."""
 
     def __init__(self, hidden_dim: int, intermediate_dim: int):
         super().__init__()
@@ -453,11 +454,15 @@ class GLM4DenseMLP(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         w = self._gate_up_weight()
-        if w is None:
+        if w is None or w.dtype != torch.float16 or not w.is_cuda:
             return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
         n = self.gate_proj.out_features
-        gu = F.linear(x, w)
-        return self.down_proj(F.silu(gu[..., :n]) * gu[..., n:])
+        gu = F.linear(x, w).reshape(-1, 2 * n)
+        h = torch.empty((gu.shape[0], n), dtype=torch.float16, device=gu.device)
+        # fp16(fp16(silu(g)) * u): F.silu then the product, in one launch
+        _lib.call("hn_silu_then_mul", _lib.ptr(gu), 2 * n, _lib.ptr(gu[:, n:]), 2 * n,
+                  _lib.ptr(h), n, gu.shape[0], n, _lib.stream(gu.device))
+        return self.down_proj(h.view(*x.shape[:-1], n))
 
 
 class GLM4MoELayer(nn.Module):

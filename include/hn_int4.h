@@ -88,6 +88,12 @@ int hn_expert_mlp_int4(const void* x, const void* gq, const void* gs, const void
 int hn_silu_mul(const void* g, long ld_g, const void* u, long ld_u, void* out, long ld_o, long M,
                 long N, void* stream);
 
+/* out = fp16(float(fp16(silu(float(g)))) * float(u)): the two fp16 operations
+ * of act_fn(gate_proj(x)) * up_proj(x) in one launch.  Replaces the SiLU and
+ * the product of GLM4DenseMLP.forward (model/glm4.py:232-233). */
+int hn_silu_then_mul(const void* g, long ld_g, const void* u, long ld_u, void* out, long ld_o,
+                     long M, long N, void* stream);
+
 /* logits[T, E] fp32 = h[T, H] @ W^T.  w_dtype 0: fp16 gate, logits rounded to fp16
  * (TopKRouter.gate(...).float(), model/router.py:102); w_dtype 1: fp32 weight
  * (GLM4SigmoidRouter, model/glm4.py:279). */

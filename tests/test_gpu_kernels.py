@@ -140,6 +140,61 @@ def test_silu_mul_vs_oracle():
     assert torch.equal(got3.view(3, 1000), got)
 
 
+def test_silu_then_mul_matches_torch_fp16_ops():
+    """hn_silu_then_mul = F.silu(g) * u on fp16 GPU tensors (two fp16
+    roundings), bit for bit, over a wide range of gate values (large
+    negative: tiny or zero products; around 0; large positive) and strided
+    operand rows (the gate and up halves of one [M, 2N] GEMM output)."""
+    from hydranet_amd import _lib
+    M, N = 37, 1408
+    g = torch.Generator().manual_seed(77)
+    gu = (torch.randn(M, 2 * N, generator=g) * 6.0).half()
+    gu[0, :N] = torch.linspace(-20.0, 20.0, N).half()
+    gu[1, :N] = (torch.randn(N, generator=g) * 1e-3).half()
+    gu = gu.to(DEV)
+    out = torch.empty(M, N, dtype=torch.float16, device=DEV)
+    _lib.call("hn_silu_then_mul", _lib.ptr(gu), 2 * N, _lib.ptr(gu[:, N:]), 2 * N, _lib.ptr(out),
+              N, M, N, _lib.stream())
+    ref = torch.nn.functional.silu(gu[:, :N]) * gu[:, N:]
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    # and the single-rounding variant differs from it only by the SiLU's rounding
+    one = torch.empty_like(out)
+    _lib.call("hn_silu_mul", _lib.ptr(gu), 2 * N, _lib.ptr(gu[:, N:]), 2 * N, _lib.ptr(one), N, M,
+              N, _lib.stream())
+    assert (one.float() - out.float()).abs().max().item() <= 1e-2 * out.float().abs().max().item()
+
+
+def test_glm_shared_expert_stacked_gate_up():
+    """GLM4DenseMLP's stacked gate/up GEMM + fused SiLU-product against the
+    three separate fp16 Linears of the reference's forward on the same
+    weights (within the fp16 output bar; a different GEMM kernel may sum in
+    another order), and the re-pointed parameters keep their values."""
+    from hydranet_amd.model.moe import GLM4DenseMLP
+    torch.manual_seed(3)
+    m = GLM4DenseMLP(4096, 1408).half().to(DEV)
+    with torch.no_grad():
+        for lin in (m.gate_proj, m.up_proj, m.down_proj):
+            lin.weight.normal_(0.0, 0.02)
+    wg, wu = m.gate_proj.weight.detach().clone(), m.up_proj.weight.detach().clone()
+    x = torch.randn(1, 32, 4096, device=DEV).half()
+    F = torch.nn.functional
+    with torch.no_grad():
+        ref = F.linear(F.silu(F.linear(x, wg)) * F.linear(x, wu), m.down_proj.weight)
+        got = m(x)
+        got2 = m(x)  # the stacked buffer is reused
+    assert torch.equal(m.gate_proj.weight, wg) and torch.equal(m.up_proj.weight, wu)
+    assert m.gate_proj.weight.data_ptr() + wg.numel() * 2 == m.up_proj.weight.data_ptr()
+    assert torch.equal(got, got2)
+    _close(got, ref)
+    # replacing a weight afterwards is picked up
+    with torch.no_grad():
+        m.up_proj.weight.data = (wu * 0.5).contiguous()
+        ref3 = F.linear(F.silu(F.linear(x, wg)) * F.linear(x, wu * 0.5), m.down_proj.weight)
+        got3 = m(x)
+    _close(got3, ref3)
+
+
 # --------------------------------------------------------------------------- expert MLP
 def test_expert_mlp_vs_reference_golden():
     from hydranet_amd.kernels import expert_mlp_int4_fused
