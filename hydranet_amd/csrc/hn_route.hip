@@ -530,6 +530,8 @@ extern "C" int hn_router_topk(const void* logits, const void* bias, long T, long
                               void* stream) {
   HN_ARG_CHECK(T >= 0 && E > 0 && k > 0 && k <= kMaxTopK && k <= E,
                "hn_router_topk: need 0 < k <= min(E, %d)", kMaxTopK);
+  // one wave per token holds at most 4 x 64 candidates
+  HN_ARG_CHECK(E <= kMaxExperts, "hn_router_topk: need E <= %d (got %ld)", kMaxExperts, E);
   HN_ARG_CHECK(mode == 0 || mode == 1, "hn_router_topk: mode must be 0 or 1");
   if (T == 0) return 0;
   hipLaunchKernelGGL(router_topk_kernel, dim3(E <= 16 ? hn_cdiv(T, 256) : hn_cdiv(T, 4)), dim3(256),

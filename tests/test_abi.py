@@ -61,6 +61,9 @@ def test_argument_errors_raise_without_gpu():
     with pytest.raises(RuntimeError, match="mode must be"):
         _lib.call("hn_router_topk", None, None, 1, 8, 2, 5, ctypes.c_float(0), ctypes.c_float(1),
                   None, None, None)
+    with pytest.raises(RuntimeError, match="E <= 256"):
+        _lib.call("hn_router_topk", None, None, 1, 257, 2, 1, ctypes.c_float(0),
+                  ctypes.c_float(1), None, None, None)
     with pytest.raises(RuntimeError, match="decode sizes"):
         _lib.call("hn_moe_route", None, 4096, None, 4096, 0, None, None, 2048, 8, 4096, 2, 0,
                   ctypes.c_float(0), ctypes.c_float(1), None, None, None, None, None, None, None,
