@@ -139,13 +139,17 @@ __global__ __launch_bounds__(kPermThreads) void moe_permute_kernel(
     const int j = base + tid;
     int e = (j < n) ? idx[j] : -1;
     if (e < 0 || e >= E) e = -1;
-    // rank among earlier lanes of this wave with the same expert
-    int rank = 0;
-    for (int l2 = 0; l2 < 64; ++l2) {
-      const int e2 = __shfl(e, l2, 64);
-      rank += (l2 < lane && e2 == e) ? 1 : 0;
+    // rank among earlier lanes of this wave with the same expert, from nine
+    // ballots over the bits of e (E <= 256; -1 sets bit 8); the rank-0 lane
+    // of each expert writes the wave's count
+    uint64_t same = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 9; ++b) {
+      const uint64_t bal = __ballot((e >> b) & 1);
+      same &= ((e >> b) & 1) ? bal : ~bal;
     }
-    if (e >= 0) atomicAdd(&wtab[wave][e], 1);
+    const int rank = __popcll(same & ((1ull << lane) - 1));
+    if (e >= 0 && rank == 0) wtab[wave][e] = __popcll(same);
     __syncthreads();
     if (e >= 0) {
       int before = 0;
