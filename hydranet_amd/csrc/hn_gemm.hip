@@ -129,16 +129,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
 // an offset past the descriptor's range and read as 0 without touching
 // memory); the per-group part is in soffset.
 // ---------------------------------------------------------------------------
+// gfx9 reads M0 for an LDS-DMA load without an interlock: an SALU write of M0
+// needs one wait state before the load (the compiler inserts it for its own
+// code, never inside inline asm), else the load may take the previous M0 and
+// write its data over another load's LDS bytes.
 __device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                          uint32_t lds) {
   // soffset and m0 are uniform by construction; readfirstlane keeps them in SGPRs
-  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)),
                   "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
 __device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
                :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
