@@ -64,6 +64,11 @@ def test_argument_errors_raise_without_gpu():
     with pytest.raises(RuntimeError, match="E <= 256"):
         _lib.call("hn_router_topk", None, None, 1, 257, 2, 1, ctypes.c_float(0),
                   ctypes.c_float(1), None, None, None)
+    with pytest.raises(RuntimeError, match="negative dims"):
+        _lib.call("hn_silu_then_mul", None, 8, None, 8, None, 8, -1, 8, None)
+    # empty products return before any HIP call
+    _lib.call("hn_silu_then_mul", None, 8, None, 8, None, 8, 0, 8, None)
+    _lib.call("hn_silu_mul", None, 8, None, 8, None, 8, 4, 0, None)
     with pytest.raises(RuntimeError, match="decode sizes"):
         _lib.call("hn_moe_route", None, 4096, None, 4096, 0, None, None, 2048, 8, 4096, 2, 0,
                   ctypes.c_float(0), ctypes.c_float(1), None, None, None, None, None, None, None,
