@@ -148,10 +148,12 @@ def test_glm_router_vs_oracle(bias):
     np.testing.assert_allclose(wt.cpu().float().sum(-1).numpy(), 1.0, atol=1e-2)
 
 
-@pytest.mark.parametrize("E,k", [(17, 2), (64, 8), (128, 8), (128, 16), (160, 4), (256, 8)])
+@pytest.mark.parametrize("E,k", [(8, 2), (16, 4), (17, 2), (64, 8), (128, 8), (128, 16),
+                                 (160, 4), (256, 8)])
 @pytest.mark.parametrize("ties", [False, True])
 def test_wave_topk_vs_oracle(E, k, ties):
-    """The one-wave-per-token top-k (E > 16) against the C oracle: indices bit
+    """hn_router_topk (one thread per token up to 16 experts, one wave per
+    token above) against the C oracle: indices bit
     for bit in both modes (ties: the lower expert first), sigmoid weights bit
     for bit (fp32 sum in selection order, +eps, scaling), softmax weights
     within one fp16 ulp (the oracle sums its exponentials in double).  With
