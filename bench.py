@@ -635,6 +635,79 @@ def c1phase(args):
                       + T * I * 2 + T * H * 2, "copy_bytes": src.numel() * 2}), flush=True)
 
 
+def bench_h2d(args):
+    """Expert-miss path of the residency layer, one Mixtral expert = one 90.8 MB
+    blob (a18): (1) pinned staging -> HBM, GpuExpertSlot.load_from_pinned on a
+    copy stream (the host link alone, HIP events on that stream); (2) the whole
+    PackedExpertStore.load_to_gpu_slot from an experts.bin on local disk (one
+    read into the pinned staging ring -> one H2D copy per expert; the next
+    expert's read overlaps the previous copy), page cache warm, host
+    clock.  Eight experts, five passes each; every slab is compared with its
+    blob byte for byte afterwards."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from hydranet_amd.cache.blob_layout import BlobLayout
+    from hydranet_amd.cache.packed_expert_store import GpuExpertSlot, PackedExpertStore
+    from hydranet_amd.preprocess import pack_store as ps
+    H, I, g, E, reps = 4096, 14336, 128, 8, 5
+    lay = BlobLayout.from_dims(H, I, g)
+    n = lay.total_size
+    gen = np.random.default_rng(7)
+    blobs = [gen.integers(0, 256, n, dtype=np.uint8) for _ in range(E)]
+    pinned = [torch.from_numpy(b).pin_memory() for b in blobs]
+    slots = [GpuExpertSlot(e, H, I, g, "cuda") for e in range(E)]
+    cs = torch.cuda.Stream()
+
+    def exact():
+        return all(bool(torch.equal(slots[e].slab.cpu(), torch.from_numpy(blobs[e])))
+                   for e in range(E))
+
+    def load_pinned():
+        for e in range(E):
+            slots[e].load_from_pinned(pinned[e], lay, 0, e, stream=cs)
+
+    load_pinned()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cs)
+    for _ in range(reps):
+        load_pinned()
+    e1.record(cs)
+    e1.synchronize()
+    us_pinned = e0.elapsed_time(e1) * 1e3 / (reps * E)
+    ok = exact()
+    for sl in slots:
+        sl.slab.zero_()
+    tmp = tempfile.mkdtemp(prefix="hn_h2d_")
+    try:
+        ps.write_packed_store(tmp, ((0, e, blobs[e]) for e in range(E)), 1, E, H, I, g,
+                              model_type="mixtral")
+        st = PackedExpertStore(os.path.join(tmp, "experts.idx"), device="cuda")
+        for e in range(E):  # warms the page cache
+            st.load_to_gpu_slot(0, e, slots[e])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            for e in range(E):
+                st.load_to_gpu_slot(0, e, slots[e])
+        torch.cuda.synchronize()
+        us_store = (time.perf_counter() - t0) * 1e6 / (reps * E)
+        ok = ok and exact()
+        st.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return {"workload": "h2d: one Mixtral expert blob (4096 -> 14336 -> 4096 INT4 g128) per "
+                        "load, 8 experts x 5 passes",
+            "bytes_per_expert": n, "us_per_expert": round(us_pinned, 1),
+            "GB_s": round(n / us_pinned / 1e3, 2),
+            "store_path": {"us_per_expert": round(us_store, 1),
+                           "GB_s": round(n / us_store / 1e3, 2),
+                           "path": "experts.bin -> pinned staging (one read per expert) -> "
+                                   "H2D, page cache warm"},
+            "bit_exact": ok}
+
+
 def c2phase(args):
     """Counter run: 20 launches of the C2 T=16 routing + gate/up stream kernel (the
     roofline kernel), then 20 copies of 512 MiB (the copy calibrates FETCH_SIZE /
@@ -810,10 +883,13 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c5", "c1phase", "c2phase", "c4phase"],
+                    choices=["c1", "c2", "c3", "c4", "c5", "c1phase", "c2phase", "c4phase",
+                             "h2d"],
                     help="c2phase: only the C2 T=16 routing + gate/up kernel and a 512 MiB copy "
                          "(the two kernels whose rocprofv3 counters give roofline.traffic); "
-                         "c4phase: only the C4 grouped GEMM launches (MFMA counters)")
+                         "c4phase: only the C4 grouped GEMM launches (MFMA counters); "
+                         "h2d: the expert-miss load path (pinned -> HBM, and from a store "
+                         "on disk)")
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--decode-tokens", type=int, default=256, help="c5: tokens generated")
     ap.add_argument("--warmup-decode", type=int, default=3, help="c5: untimed decode forwards")
@@ -848,6 +924,14 @@ def main():
         return
     if args.workload == "c4phase":
         c4phase(args)
+        return
+    if args.workload == "h2d":
+        r = bench_h2d(args)
+        _log("h2d", r)
+        print(json.dumps({"metric": "expert H2D load GB/s (residency miss path, 1 GPU)",
+                          "value": r["GB_s"], "unit": "GB/s", "n_gpus": 1,
+                          "higher_is_better": True, "dtype": "u8", "data": "synthetic",
+                          "config": r}), flush=True)
         return
     if args.workload == "c3":
         c3 = bench_c3(args)

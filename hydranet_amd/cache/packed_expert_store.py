@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import json
 import mmap
+import os
 import threading
 import warnings
 from collections import deque
@@ -265,13 +266,33 @@ class PackedExpertStore:
         return src[ent.offset:ent.offset + ent.size], self.layout
 
     def load_to_staging(self, layer_idx: int, expert_idx: int):
-        blob, layout = self.get_expert_blob(layer_idx, expert_idx)
+        if self._file is None:
+            blob, layout = self.get_expert_blob(layer_idx, expert_idx)
+            slot_idx, staging = self.staging.acquire()
+            with warnings.catch_warnings():  # a read-only window, only copied from
+                warnings.simplefilter("ignore", UserWarning)
+                t = torch.frombuffer(blob, dtype=torch.uint8)
+            staging[: t.numel()].copy_(t)
+            return slot_idx, staging, layout
+        # read the blob from the file straight into the pinned slot: one
+        # kernel copy out of the page cache (slicing the mmap would first copy
+        # it into a bytes object, then into the slot)
+        key = (layer_idx, expert_idx)
+        if key not in self.index:
+            raise ValueError(f"Expert ({layer_idx}, {expert_idx}) not in index")
+        ent = self.index[key]
         slot_idx, staging = self.staging.acquire()
-        with warnings.catch_warnings():  # a read-only mmap window, only copied from
-            warnings.simplefilter("ignore", UserWarning)
-            t = torch.frombuffer(blob, dtype=torch.uint8)
-        staging[: t.numel()].copy_(t)
-        return slot_idx, staging, layout
+        dst = memoryview(staging.numpy())[: ent.size]
+        got = 0
+        while got < ent.size:
+            k = os.preadv(self._file.fileno(), [dst[got:]], ent.offset + got)
+            if k <= 0:
+                self.staging.release(slot_idx, None)
+                raise IOError(f"experts.bin ended inside expert ({layer_idx}, {expert_idx})")
+            got += k
+        self.load_count += 1
+        self.total_bytes_loaded += ent.size
+        return slot_idx, staging, self.layout
 
     def load_to_gpu_slot(self, layer_idx: int, expert_idx: int, gpu_slot: GpuExpertSlot,
                          stream: Optional[torch.cuda.Stream] = None):
