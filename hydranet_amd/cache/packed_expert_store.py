@@ -26,6 +26,7 @@ import os
 import threading
 import warnings
 from collections import deque
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Dict, Optional, Tuple
@@ -184,6 +185,12 @@ class PinnedStagingRing:
             self._inflight.append((ev, idx))
 
 
+# Blob reads: pieces of 8 MiB on up to eight threads (one Mixtral expert is
+# twelve pieces).
+_READ_CHUNK = 8 << 20
+_READ_THREADS = 8
+
+
 class PackedExpertStore:
     """experts.idx + experts.bin reader feeding GPU slots through pinned staging."""
 
@@ -230,6 +237,7 @@ class PackedExpertStore:
                               if self.device.type == "cuda" and torch.cuda.is_available() else None)
         self.load_count = 0
         self.total_bytes_loaded = 0
+        self._readers: Optional[ThreadPoolExecutor] = None
 
     @property
     def hidden_dim(self) -> int:
@@ -274,22 +282,33 @@ class PackedExpertStore:
                 t = torch.frombuffer(blob, dtype=torch.uint8)
             staging[: t.numel()].copy_(t)
             return slot_idx, staging, layout
-        # read the blob from the file straight into the pinned slot: one
-        # kernel copy out of the page cache (slicing the mmap would first copy
-        # it into a bytes object, then into the slot)
+        # read the blob from the file straight into the pinned slot, in
+        # _READ_CHUNK pieces on a few threads (the read releases the GIL):
+        # kernel copies out of the page cache (slicing the mmap would first
+        # copy it into a bytes object, then into the slot)
         key = (layer_idx, expert_idx)
         if key not in self.index:
             raise ValueError(f"Expert ({layer_idx}, {expert_idx}) not in index")
         ent = self.index[key]
         slot_idx, staging = self.staging.acquire()
         dst = memoryview(staging.numpy())[: ent.size]
-        got = 0
-        while got < ent.size:
-            k = os.preadv(self._file.fileno(), [dst[got:]], ent.offset + got)
-            if k <= 0:
-                self.staging.release(slot_idx, None)
-                raise IOError(f"experts.bin ended inside expert ({layer_idx}, {expert_idx})")
-            got += k
+        fd = self._file.fileno()
+
+        def read_piece(lo: int) -> bool:
+            hi = min(lo + _READ_CHUNK, ent.size)
+            while lo < hi:
+                k = os.preadv(fd, [dst[lo:hi]], ent.offset + lo)
+                if k <= 0:
+                    return False
+                lo += k
+            return True
+
+        starts = range(0, ent.size, _READ_CHUNK)
+        if self._readers is None:
+            self._readers = ThreadPoolExecutor(max_workers=_READ_THREADS)
+        if not all(self._readers.map(read_piece, starts)):
+            self.staging.release(slot_idx, None)
+            raise IOError(f"experts.bin ended inside expert ({layer_idx}, {expert_idx})")
         self.load_count += 1
         self.total_bytes_loaded += ent.size
         return slot_idx, staging, self.layout
@@ -317,6 +336,9 @@ class PackedExpertStore:
                 "total_mb_loaded": self.total_bytes_loaded / (1024 * 1024)}
 
     def close(self):
+        if getattr(self, "_readers", None) is not None:
+            self._readers.shutdown(wait=True)
+            self._readers = None
         if self._mmap is not None:
             try:
                 self._mmap.close()
