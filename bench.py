@@ -703,7 +703,7 @@ def bench_h2d(args):
             "GB_s": round(n / us_pinned / 1e3, 2),
             "store_path": {"us_per_expert": round(us_store, 1),
                            "GB_s": round(n / us_store / 1e3, 2),
-                           "path": "experts.bin -> pinned staging (one read per expert) -> "
+                           "path": "experts.bin -> pinned staging (8 MiB preadv pieces on eight threads) -> "
                                    "H2D, page cache warm"},
             "bit_exact": ok}
 

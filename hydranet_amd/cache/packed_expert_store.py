@@ -237,6 +237,10 @@ class PackedExpertStore:
                               if self.device.type == "cuda" and torch.cuda.is_available() else None)
         self.load_count = 0
         self.total_bytes_loaded = 0
+        # the compute thread (misses) and the cache manager's prefetch thread
+        # both load: one reader pool, made under the lock, and the counters
+        # updated under it
+        self._lock = threading.Lock()
         self._readers: Optional[ThreadPoolExecutor] = None
 
     @property
@@ -268,8 +272,7 @@ class PackedExpertStore:
         if key not in self.index:
             raise ValueError(f"Expert ({layer_idx}, {expert_idx}) not in index")
         ent = self.index[key]
-        self.load_count += 1
-        self.total_bytes_loaded += ent.size
+        self._count(ent.size)
         src = self._mmap if self.use_mmap else self._data
         return src[ent.offset:ent.offset + ent.size], self.layout
 
@@ -304,13 +307,14 @@ class PackedExpertStore:
             return True
 
         starts = range(0, ent.size, _READ_CHUNK)
-        if self._readers is None:
-            self._readers = ThreadPoolExecutor(max_workers=_READ_THREADS)
-        if not all(self._readers.map(read_piece, starts)):
+        with self._lock:
+            if self._readers is None:
+                self._readers = ThreadPoolExecutor(max_workers=_READ_THREADS)
+            readers = self._readers
+        if not all(readers.map(read_piece, starts)):
             self.staging.release(slot_idx, None)
             raise IOError(f"experts.bin ended inside expert ({layer_idx}, {expert_idx})")
-        self.load_count += 1
-        self.total_bytes_loaded += ent.size
+        self._count(ent.size)
         return slot_idx, staging, self.layout
 
     def load_to_gpu_slot(self, layer_idx: int, expert_idx: int, gpu_slot: GpuExpertSlot,
@@ -331,14 +335,22 @@ class PackedExpertStore:
         self.staging.release(staging_idx, None)
         return None
 
+    def _count(self, nbytes: int) -> None:
+        with self._lock:
+            self.load_count += 1
+            self.total_bytes_loaded += nbytes
+
     def get_stats(self) -> Dict:
         return {"load_count": self.load_count, "total_bytes_loaded": self.total_bytes_loaded,
                 "total_mb_loaded": self.total_bytes_loaded / (1024 * 1024)}
 
     def close(self):
-        if getattr(self, "_readers", None) is not None:
-            self._readers.shutdown(wait=True)
-            self._readers = None
+        lock = getattr(self, "_lock", None)
+        if lock is not None:
+            with lock:
+                readers, self._readers = self._readers, None
+            if readers is not None:
+                readers.shutdown(wait=True)
         if self._mmap is not None:
             try:
                 self._mmap.close()

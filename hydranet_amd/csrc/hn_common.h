@@ -169,8 +169,12 @@ static inline int hn_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 // becomes tag << 16, a count of zero — then adds 1.  The two atomics of one
 // wave to one address stay in program order, so the claim precedes the
 // count.  The last arrival resets the word to 0, which keeps replays of a
-// captured graph (whose tag is fixed at capture) counting from zero; a
-// replay stopped part-way is the one case not healed by the next launch.
+// captured graph (whose tag is fixed at capture) counting from zero.  Two
+// cases are not healed by the next launch, because the word then holds a tag
+// at or above the next launch's: a graph replay stopped part-way, and an
+// eager launch (a later tag) stopped part-way before a replay of a graph
+// captured earlier.  A caller recovering from a stopped launch re-zeroes the
+// counter region (a fill kernel) before the next replay.
 // Launches that share a workspace concurrently race (on the partials too).
 //
 // Ordering, with the wave's partial stores issued before the call:

@@ -20,7 +20,7 @@
 //    tile's tokens.  Waves split N, never M, so each weight is dequantised by
 //    exactly one wave per tile.
 //  * Every load of the K loop goes HBM -> LDS directly (buffer_load ... lds,
-//    issued from inline asm with explicit waits), three LDS stages of 64 k:
+//    with explicit waits), three LDS stages of 64 k:
 //    activations (XOR-swizzled rows so A-fragment reads are conflict-free),
 //    packed weights and the dwords holding the scales.
 //  * Each k-step's A fragments and unpacked weights are double-buffered: step
@@ -121,29 +121,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
 
 // ---------------------------------------------------------------------------
 // Loads.  Everything the K loop reads from memory goes HBM -> LDS directly
-// (buffer_load ... lds: lane i's bytes land at m0 + size * i), issued from
-// inline asm so that the compiler neither counts these loads nor assumes
-// they alias its LDS reads: every wait on them is explicit (s_waitcnt vmcnt
-// below), and loads return in issue order.  Offsets: the per-lane part is in
-// voffset (the buffer range check covers voffset only, so rows past N carry
-// an offset past the descriptor's range and read as 0 without touching
-// memory); the per-group part is in soffset.
+// (buffer_load ... lds: lane i's bytes land at m0 + size * i) through the
+// compiler's LDS-DMA builtin, which sets M0 and places the wait states gfx9
+// needs between a VALU or SALU write of an SGPR operand (M0, soffset, the
+// descriptor) and the load that reads it.  The compiler does not wait on
+// these loads before the K loop's LDS reads: every wait on them is explicit
+// (s_waitcnt vmcnt below), and loads return in issue order.  Offsets: the
+// per-lane part is in voffset (the buffer range check covers voffset only, so
+// rows past N carry an offset past the descriptor's range and read as 0
+// without touching memory); the per-group part is in soffset.
 // ---------------------------------------------------------------------------
-// gfx9 reads M0 for an LDS-DMA load without an interlock: an SALU write of M0
-// needs one wait state before the load (the compiler inserts it for its own
-// code, never inside inline asm), else the load may take the previous M0 and
-// write its data over another load's LDS bytes.
+__device__ __forceinline__ lds_void_t* lds_ptr(uint32_t addr) {
+  return (lds_void_t*)((__attribute__((address_space(3))) char*)nullptr + addr);
+}
+
 __device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                          uint32_t lds) {
-  // soffset and m0 are uniform by construction; readfirstlane keeps them in SGPRs
-  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)),
-                  "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+  // soffset and the LDS address are uniform by construction
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_ptr(__builtin_amdgcn_readfirstlane(lds)), 16,
+                                           voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 
 __device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
-               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_ptr(__builtin_amdgcn_readfirstlane(lds)), 4,
+                                           voff, 0, 0, 0);
 }
 
 template <int N>

@@ -1041,6 +1041,14 @@ extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w,
   if (rc == 0)
     rc = hn_moe_unpermute_split4_impl(part, rows * H, inv, idx, w, T, k, nullptr, H, out, ld_o,
                                       H, stream);
+  if (rc == HN_NOT_HANDLED) {
+    // the dry run passed but a launch declined (e.g. the device refused the
+    // 160 KiB dynamic-LDS limit a plan needs): an argument-style error the
+    // caller can fall back from
+    hn_set_error("%s: the device cannot run this shape's plan (dynamic LDS limit); "
+                 "T=%ld E=%ld k=%ld", who, T, E, k);
+    return -22;
+  }
   return rc;
 }
 

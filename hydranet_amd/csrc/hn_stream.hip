@@ -626,7 +626,9 @@ int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, h
   if (p.th != TH) return HN_NOT_HANDLED;  // the plan was sized for the other chunking
   auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS, ROUTE, TH>;
   static HnPerDevice attr;  // per instantiation and device
-  static HnPerDevice fit;   // workgroups per CU the registers allow
+  // workgroups per CU the registers allow, per block size (kw waves): one
+  // instantiation serves several K (e.g. K = 1408 and 14336 down projections)
+  static HnPerDevice fit[kMaxWaves + 1];
   const int dev = hn_current_device();
   std::atomic<int>& sa = attr.state[dev];
   int st = sa.load(std::memory_order_relaxed);
@@ -641,7 +643,7 @@ int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, h
   if (occ > 1) {
     // the plan checked LDS and waves; the registers decide too (a kernel
     // over 128 VGPRs holds three waves per SIMD: one 7-wave workgroup per CU)
-    std::atomic<int>& sf = fit.state[dev];
+    std::atomic<int>& sf = fit[p.kw].state[dev];
     int n = sf.load(std::memory_order_relaxed);
     if (n == 0) {
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)kern, p.kw * 64, 0) !=

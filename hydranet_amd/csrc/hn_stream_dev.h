@@ -1,7 +1,6 @@
-// Device-side pieces shared by the streaming decode kernels (hn_stream.hip)
-// and the one-launch expert MLP (hn_fused.hip): launch arguments, the
-// weight-column loads, the biased-nibble unpack + MFMA chain, the activation
-// staging with its bias corrections, and the column cursor.  The scheme
+// Device-side pieces of the streaming decode kernels (hn_stream.hip): launch
+// arguments, the weight-column loads, the biased-nibble unpack + MFMA chain,
+// the activation staging with its bias corrections, and the column cursor.  The scheme
 // (column decomposition, biased nibbles, corrections) is described at the
 // top of hn_stream.hip.
 #pragma once
