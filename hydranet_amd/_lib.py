@@ -33,6 +33,7 @@ SIGNATURES: dict[str, list] = {
     "hn_silu_then_mul": [P, L, P, L, P, L, L, L, P],
     "hn_router_logits": [P, L, P, L, I, P, L, L, L, P],
     "hn_router_topk": [P, P, L, L, L, I, F, F, P, P, P],
+    "hn_router_group_limit": [P, L, L, L, L, P, P],
     "hn_moe_permute": [P, L, L, L, P, P, P, P, P, P],
     "hn_moe_gather": [P, L, P, L, P, L, P, L, L, L, P],
     "hn_moe_unpermute": [P, L, P, P, P, L, L, P, L, P, L, L, P],

@@ -87,6 +87,14 @@ class ExpertCacheConfig:
     affinity_bonus: float = 0.1
     affinity_entropy_threshold: float = 0.5
     enable_prefetch: bool = True
+    # MI355X sizing: when a packed store is attached, every layer whose experts
+    # fit the device's free HBM (less the headroom kept for activations, KV
+    # cache and workspaces) becomes one resident arena; only the layers that
+    # do not fit use the slot cache above (the reference's 16 GB heuristic,
+    # config.py:259-267).  288 GB holds all of Mixtral-8x7B's experts (23.3 GB)
+    # or GLM-4.5-Air's (51.4 GB).
+    resident_when_fits: bool = True
+    resident_headroom_bytes: int = 16 << 30
 
     @property
     def slots_per_layer(self) -> int:
@@ -591,6 +599,7 @@ class ExpertCacheManager:
         self.pin_refresh_interval = 16
         self.packed_store = None
         self.use_packed_mode = False
+        self.auto_resident_layers = 0
         self.sequence_lfu: Dict[int, Dict[int, Dict[int, float]]] = {}
         self.lfu_decay_rate = 0.95
         self.active_sequence_id: Optional[int] = None
@@ -608,7 +617,9 @@ class ExpertCacheManager:
         return [base_slots + 1 if (i < 12 or i >= 14) else base_slots for i in range(num_layers)]
 
     def set_packed_store(self, store):
-        """Attach the packed INT4 store to every layer (:911-936)."""
+        """Attach the packed INT4 store to every layer (:911-936), then make
+        resident as many layers as the device's free HBM holds
+        (``resident_plan``)."""
         self.packed_store = store
         self.use_packed_mode = True
         H = store.model_config["hidden_dim"]
@@ -616,14 +627,41 @@ class ExpertCacheManager:
         g = store.quant_config["group_size"]
         for c in self.layer_caches:
             c.set_packed_mode(store, H, I, g)
+        n = self.resident_plan()
+        if n:
+            self.make_resident(range(n))
+        self.auto_resident_layers = n
+
+    def _free_device_bytes(self) -> Optional[int]:
+        """Free memory of the cache's device (None off the GPU)."""
+        if self.device.type != "cuda" or not torch.cuda.is_available():
+            return None
+        return int(torch.cuda.mem_get_info(self.device)[0])
+
+    def layer_resident_bytes(self) -> int:
+        """HBM one resident layer takes (its arena)."""
+        size = self.packed_store.layout.total_size
+        stride = (size + _ARENA_ALIGN - 1) // _ARENA_ALIGN * _ARENA_ALIGN
+        return stride * self.model_config.num_experts
+
+    def resident_plan(self) -> int:
+        """How many layers (from layer 0) to make resident: those whose arenas
+        fit the free device memory less ``resident_headroom_bytes``; 0 when
+        ``resident_when_fits`` is off or the device reports no figure."""
+        if not self.cache_config.resident_when_fits or self.packed_store is None:
+            return 0
+        free = self._free_device_bytes()
+        if free is None:
+            return 0
+        room = free - int(self.cache_config.resident_headroom_bytes)
+        per = self.layer_resident_bytes()
+        return int(max(0, min(len(self.layer_caches), room // per if per > 0 else 0)))
 
     def resident_bytes(self) -> int:
         """HBM that make_resident() needs for every layer."""
         if self.packed_store is None:
             raise RuntimeError("no packed store attached")
-        size = self.packed_store.layout.total_size
-        stride = (size + _ARENA_ALIGN - 1) // _ARENA_ALIGN * _ARENA_ALIGN
-        return stride * self.model_config.num_experts * len(self.layer_caches)
+        return self.layer_resident_bytes() * len(self.layer_caches)
 
     def make_resident(self, layers: Optional[Iterable[int]] = None):
         """Load every expert of the given layers (all by default) into per-layer
@@ -805,7 +843,8 @@ class ExpertCacheManager:
                 "layer_hit_rate_median": rates[len(rates) // 2] if rates else 0.0,
                 "layer_hit_rate_max": rates[-1] if rates else 0.0,
                 "miss_burst_events": self.total_burst_events,
-                "active_sequences": len(self.sequence_lfu)}
+                "active_sequences": len(self.sequence_lfu),
+                "resident_layers": sum(1 for c in self.layer_caches if c.is_resident())}
 
     def reset_stats(self):
         for c in self.layer_caches:

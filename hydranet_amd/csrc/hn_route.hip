@@ -83,6 +83,45 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const h16* __restric
 }
 
 // One wave per token (more than 16 experts) or one thread per token.
+// Group-limited selection of GLM4SigmoidRouter (model/glm4.py:285-298), one
+// wave per token: the experts' sigmoids (sigmoid_f32, as the top-k) go to
+// LDS, lane g < n_group takes the max over its group of E / n_group
+// consecutive experts, the topk_group largest group scores are kept (equal
+// scores: the lower group), and the row is written back with -inf for every
+// expert of the other groups (their sigmoid is then exactly 0, the
+// reference's masked score).
+__global__ __launch_bounds__(256) void router_group_limit_kernel(
+    const float* __restrict__ logits, int T, int E, int n_group, int topk_group,
+    float* __restrict__ out) {
+  __shared__ float s_sc[4][kMaxExperts];
+  __shared__ float s_gs[4][64];
+  __shared__ int s_keep[4][64];
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wv;
+  if (t >= T) return;  // uniform per wave; no block-wide barrier below
+  const float* l = logits + (long)t * E;
+  for (int e = lane; e < E; e += 64) s_sc[wv][e] = sigmoid_f32(l[e]);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  const int gsz = E / n_group;
+  float gmax = -__builtin_inff();
+  if (lane < n_group)
+    for (int j = 0; j < gsz; ++j) gmax = fmaxf(gmax, s_sc[wv][lane * gsz + j]);
+  s_gs[wv][lane] = gmax;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  int rank = 0;
+  for (int g = 0; g < n_group; ++g) {
+    const float o = s_gs[wv][g];
+    rank += (o > gmax || (o == gmax && g < lane)) ? 1 : 0;
+  }
+  s_keep[wv][lane] = (lane < n_group && rank < topk_group) ? 1 : 0;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  for (int e = lane; e < E; e += 64)
+    out[(long)t * E + e] = s_keep[wv][e / gsz] ? l[e] : -__builtin_inff();
+}
+
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int k,
     int mode, float eps, float scaling, int* __restrict__ idx_out, h16* __restrict__ w_out) {
@@ -528,7 +567,8 @@ extern "C" int hn_router_logits(const void* h, long ld_h, const void* w, long ld
   return 0;
 }
 
-// mode 0: softmax top-k (Mixtral); mode 1: sigmoid top-k (GLM), bias may be null.
+// mode 0: softmax top-k (Mixtral); mode 1: sigmoid top-k (GLM), bias may be
+// null; mode 2: sigmoid top-k without the normalisation (norm_topk_prob=False).
 extern "C" int hn_router_topk(const void* logits, const void* bias, long T, long E, long k,
                               int mode, float eps, float scaling, int* idx_out, void* w_out,
                               void* stream) {
@@ -536,13 +576,31 @@ extern "C" int hn_router_topk(const void* logits, const void* bias, long T, long
                "hn_router_topk: need 0 < k <= min(E, %d)", kMaxTopK);
   // one wave per token holds at most 4 x 64 candidates
   HN_ARG_CHECK(E <= kMaxExperts, "hn_router_topk: need E <= %d (got %ld)", kMaxExperts, E);
-  HN_ARG_CHECK(mode == 0 || mode == 1, "hn_router_topk: mode must be 0 or 1");
+  HN_ARG_CHECK(mode >= 0 && mode <= 2, "hn_router_topk: mode must be 0, 1 or 2");
   if (T == 0) return 0;
   hipLaunchKernelGGL(router_topk_kernel, dim3(E <= 16 ? hn_cdiv(T, 256) : hn_cdiv(T, 4)), dim3(256),
                      0, (hipStream_t)stream,
                      (const float*)logits, (const float*)bias, (int)T, (int)E, (int)k, mode, eps,
                      scaling, idx_out, (h16*)w_out);
   HN_LAUNCH_CHECK("hn_router_topk");
+  return 0;
+}
+
+// Group-limited routing: out [T, E] = logits with the experts outside each
+// token's topk_group best groups set to -inf (then hn_router_topk mode 1/2).
+extern "C" int hn_router_group_limit(const void* logits, long T, long E, long n_group,
+                                     long topk_group, void* out, void* stream) {
+  const char* who = "hn_router_group_limit";
+  HN_ARG_CHECK(T >= 0 && E > 0 && E <= kMaxExperts, "%s: need 0 < E <= %d", who, kMaxExperts);
+  HN_ARG_CHECK(n_group >= 1 && n_group <= 64 && E % n_group == 0,
+               "%s: n_group must divide E and be <= 64 (E=%ld n_group=%ld)", who, E, n_group);
+  HN_ARG_CHECK(topk_group >= 1 && topk_group <= n_group,
+               "%s: need 1 <= topk_group <= n_group (got %ld)", who, topk_group);
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(router_group_limit_kernel, dim3(hn_cdiv(T, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const float*)logits, (int)T, (int)E, (int)n_group,
+                     (int)topk_group, (float*)out);
+  HN_LAUNCH_CHECK(who);
   return 0;
 }
 
@@ -610,7 +668,7 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
   HN_ARG_CHECK(T >= 0 && E > 0 && E <= kMaxExperts && H > 0,
                "%s: need 0 < E <= %d", who, kMaxExperts);
   HN_ARG_CHECK(k > 0 && k <= kMaxTopK && k <= E, "%s: need 0 < k <= min(E, %d)", who, kMaxTopK);
-  HN_ARG_CHECK(mode == 0 || mode == 1, "%s: mode must be 0 or 1", who);
+  HN_ARG_CHECK(mode >= 0 && mode <= 2, "%s: mode must be 0, 1 or 2", who);
   HN_ARG_CHECK(T * E <= kRouteMaxLogits && T * k <= kRouteMaxAssign,
                "%s: T*E <= %d and T*k <= %d (decode sizes; use the separate kernels above)",
                who, kRouteMaxLogits, kRouteMaxAssign);

@@ -4,7 +4,8 @@
 // first.  mode 0 = Mixtral: fp32 softmax over the selected logits and
 // renormalisation (model/router.py:109-120); mode 1 = GLM: sigmoid (exp in
 // double, rounded once), optional per-expert selection bias, normalise with
-// +eps and scale (model/glm4.py:282-309).
+// +eps and scale (model/glm4.py:282-309); mode 2 = GLM with
+// norm_topk_prob=False: the selected sigmoids times the scale (:302-307).
 #pragma once
 #include "hn_common.h"
 
@@ -14,6 +15,14 @@ constexpr int kMaxTopK = 16;
 
 __device__ __forceinline__ float sigmoid_f32(float l) {
   return (float)(1.0 / (1.0 + exp(-(double)l)));
+}
+
+// fp32 product a * b, rounded to fp32 (the reference multiplies the fp32
+// weights by the scale, then casts to fp16).  The identity DPP move keeps
+// the compiler from converting the exact product to fp16 in one step
+// (v_fma_mix), which rounds once instead of twice and can differ by an ulp.
+__device__ __forceinline__ float f32_mul(float a, float b) {
+  return __builtin_bit_cast(float, hn_vgpr(__builtin_bit_cast(uint32_t, a * b)));
 }
 
 // Selection order of top-k: larger value first, equal values lower expert
@@ -26,7 +35,7 @@ __device__ __forceinline__ bool topk_beats(float bv, int be, float av, int ae) {
 // the token's raw logits l: mode 0 fp32 softmax over the selected logits and
 // renormalisation by the fp32 sum (model/router.py:114-117); mode 1 sigmoid
 // (exp in double, rounded once: it also ranks the experts), / (sum + eps) * scaling
-// (model/glm4.py:282-307).  Compact loops: each element's value is recomputed
+// (model/glm4.py:282-307); mode 2 sigmoid * scaling.  Compact loops: each element's value is recomputed
 // where it is needed (same arithmetic each time) instead of kept in arrays.
 __device__ __noinline__ void topk_weights(const float* l, const int* sel, int k, int mode,
                                           float eps, float scaling, h16* w_o) {
@@ -41,13 +50,16 @@ __device__ __noinline__ void topk_weights(const float* l, const int* sel, int k,
     for (int i = 0; i < k; ++i) s += expf(l[sel[i]] - mx) / z;
 #pragma unroll 1
     for (int i = 0; i < k; ++i) w_o[i] = (h16)((expf(l[sel[i]] - mx) / z) / s);
-  } else {
+  } else if (mode == 1) {
     float s = 0.f;
 #pragma unroll 1
     for (int i = 0; i < k; ++i) s += sigmoid_f32(l[sel[i]]);
     const float d = s + eps;
 #pragma unroll 1
-    for (int i = 0; i < k; ++i) w_o[i] = (h16)((sigmoid_f32(l[sel[i]]) / d) * scaling);
+    for (int i = 0; i < k; ++i) w_o[i] = (h16)f32_mul(sigmoid_f32(l[sel[i]]) / d, scaling);
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < k; ++i) w_o[i] = (h16)f32_mul(sigmoid_f32(l[sel[i]]), scaling);
   }
 }
 
@@ -82,7 +94,7 @@ __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int
     ok[j] = e < E;
     const float lv = ok[j] ? l[e] : 0.f;
     float v = lv;
-    if (mode == 1 && ok[j]) {
+    if (mode >= 1 && ok[j]) {
       v = sigmoid_f32(lv);
       raw[j] = v;
       if (bias) v = v + bias[e];
@@ -169,13 +181,18 @@ __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int
       idx_o[lane] = oe;
       w_o[lane] = (h16)((expf(orr - mx) / z) / sum);
     }
-  } else {
+  } else if (mode == 1) {
     float sum = 0.f;
     for (int r = 0; r < ns; ++r) sum += at(r);
     const float d = sum + eps;
     if (lane < ns) {
       idx_o[lane] = oe;
-      w_o[lane] = (h16)((orr / d) * scaling);
+      w_o[lane] = (h16)f32_mul(orr / d, scaling);
+    }
+  } else {
+    if (lane < ns) {
+      idx_o[lane] = oe;
+      w_o[lane] = (h16)f32_mul(orr, scaling);
     }
   }
 }
@@ -194,7 +211,7 @@ __device__ __forceinline__ void topk_small(const float* l, const float* bias, in
   for (int e = 0; e < EB; ++e) {
     ok[e] = e < E;
     float v = ok[e] ? l[e] : 0.f;
-    if (mode == 1 && ok[e]) {
+    if (mode >= 1 && ok[e]) {
       v = sigmoid_f32(v);
       if (bias) v = v + bias[e];
     }

@@ -29,7 +29,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .. import _lib
-from .router import GLM4SigmoidRouter, TopKRouter, router_logits
+from .router import GLM4SigmoidRouter, TopKRouter, group_limit, router_logits
 
 
 class ExpertTable:
@@ -471,14 +471,21 @@ class GLM4MoELayer(nn.Module):
 
     def __init__(self, hidden_dim: int = 4096, moe_intermediate_dim: int = 1408,
                  num_experts: int = 128, experts_per_token: int = 8, layer_idx: int = 0,
-                 slots=None, cache_manager=None, routed_scaling_factor: float = 1.0):
+                 slots=None, cache_manager=None, routed_scaling_factor: float = 1.0,
+                 num_shared_experts: int = 1, n_group: int = 1, topk_group: int = 1,
+                 norm_topk_prob: bool = True):
         super().__init__()
         self.layer_idx = layer_idx
         self.router = GLM4SigmoidRouter(hidden_dim, num_experts, experts_per_token,
-                                        routed_scaling_factor=routed_scaling_factor)
-        self.shared_expert = GLM4DenseMLP(hidden_dim, moe_intermediate_dim)
+                                        norm_topk_prob=norm_topk_prob,
+                                        routed_scaling_factor=routed_scaling_factor,
+                                        n_group=n_group, topk_group=topk_group)
+        # one dense MLP as wide as all the shared experts together
+        # (model/glm4.py:341-344)
+        self.shared_expert = GLM4DenseMLP(hidden_dim, moe_intermediate_dim * num_shared_experts)
         self.experts = _ResidentExperts(num_experts, layer_idx, slots, cache_manager)
         self._last_idx: Optional[torch.Tensor] = None
+        self.last_routing = None  # (idx [T, k] i32, w [T, k] fp16) of the last forward
 
     def get_last_selected_experts(self) -> list:
         """Experts the last forward routed to, ascending (the reference records
@@ -518,16 +525,20 @@ class GLM4MoELayer(nn.Module):
             # fp32 logits by the multi-workgroup kernel, the rest in one launch
             logits = router_logits(flat, rt.weight.float() if rt.weight.dtype != torch.float32
                                    else rt.weight)
-            r = moe_route(flat, rt.top_k, 1, logits=logits, bias=rt.selection_bias,
-                          scaling=rt.routed_scaling_factor)
+            if rt.n_group > 1 and rt.topk_group > 0:
+                logits = group_limit(logits, rt.n_group, rt.topk_group)
+            r = moe_route(flat, rt.top_k, 1 if rt.norm_topk_prob else 2, logits=logits,
+                          bias=rt.selection_bias, scaling=rt.routed_scaling_factor)
             cur.wait_stream(side)
             shared.record_stream(cur)
             out = moe_dispatch(r, self.experts.table_for(r.idx), shared=shared.reshape(T, H))
             self._last_idx = r.idx
+            self.last_routing = (r.idx, r.w)
             return out.view(B, S, H)
         shared = self.shared_expert(hidden_states)
         idx, w = rt(hidden_states)
         table = self.experts.table_for(idx)
         out = moe_experts_forward(flat, idx, w, table, shared=shared.reshape(T, H))
         self._last_idx = idx
+        self.last_routing = (idx, w)
         return out.view(B, S, H)

@@ -9,7 +9,8 @@
   only runs (as three elementwise ops on the logits) if a cache checker
   reports an expert as not resident.
 * ``glm_route`` / ``GLM4SigmoidRouter`` — model/glm4.py:238-309: fp32 logits,
-  sigmoid, top-k, weights / (sum + 1e-9) * routed_scaling_factor, fp16.  An
+  sigmoid, the group-limited selection when n_group > 1 (``group_limit``),
+  top-k, weights / (sum + 1e-9) (norm_topk_prob) * routed_scaling_factor, fp16.  An
   optional per-expert bias is added to the scores for selection only (this
   build's extension; the reference loads e_score_correction_bias but does not
   use it, model/glm4_loader.py:164-167).
@@ -63,10 +64,29 @@ def mixtral_route(h: torch.Tensor, gate_w: torch.Tensor, top_k: int = 2):
     return idx, w, logits
 
 
+def group_limit(logits: torch.Tensor, n_group: int, topk_group: int) -> torch.Tensor:
+    """Group-limited selection (model/glm4.py:285-298): a copy of the [T, E]
+    fp32 logits with -inf for the experts outside each token's topk_group
+    groups of largest max-sigmoid (sigmoid(-inf) = 0, the reference's masked
+    score)."""
+    T, E = logits.shape
+    lg = logits.contiguous().float()
+    out = torch.empty_like(lg)
+    _lib.call("hn_router_group_limit", _lib.ptr(lg), T, E, n_group, topk_group, _lib.ptr(out),
+              _lib.stream(lg.device))
+    return out
+
+
 def glm_route(h: torch.Tensor, w: torch.Tensor, top_k: int = 8, bias=None, eps: float = 1e-9,
-              scaling: float = 1.0):
+              scaling: float = 1.0, n_group: int = 1, topk_group: int = 1,
+              norm_topk_prob: bool = True):
+    """GLM4SigmoidRouter.forward's arithmetic: fp32 logits, sigmoid, the
+    group-limited selection when n_group > 1 and topk_group > 0, top-k,
+    weights / (sum + eps) (norm_topk_prob) * scaling, fp16."""
     logits = router_logits(h, w.float() if w.dtype != torch.float32 else w)
-    idx, wt = topk_from_logits(logits, top_k, 1, bias=bias, eps=eps, scaling=scaling)
+    sel = group_limit(logits, n_group, topk_group) if n_group > 1 and topk_group > 0 else logits
+    idx, wt = topk_from_logits(sel, top_k, 1 if norm_topk_prob else 2, bias=bias, eps=eps,
+                               scaling=scaling)
     return idx, wt, logits
 
 
@@ -129,17 +149,20 @@ class TopKRouter(nn.Module):
 
 
 class GLM4SigmoidRouter(nn.Module):
-    """GLM-4.5 sigmoid top-k router (model/glm4.py:238-309) on the gfx950 kernels."""
+    """GLM-4.5 sigmoid top-k router (model/glm4.py:238-309) on the gfx950 kernels,
+    with group-limited selection (n_group > 1) and norm_topk_prob as the
+    reference's."""
 
     def __init__(self, hidden_dim: int, num_experts: int = 128, top_k: int = 8,
                  norm_topk_prob: bool = True, routed_scaling_factor: float = 1.0,
                  n_group: int = 1, topk_group: int = 1):
         super().__init__()
-        if n_group > 1 and topk_group > 0:
-            raise NotImplementedError("group-limited routing (n_group > 1) is not used by "
-                                      "GLM-4.5-Air (n_group=1) and is not implemented")
+        if n_group > 1 and topk_group > 0 and num_experts % n_group != 0:
+            raise ValueError(f"n_group {n_group} must divide num_experts {num_experts}")
         self.num_experts = num_experts
         self.top_k = top_k
+        self.n_group = n_group
+        self.topk_group = topk_group
         self.norm_topk_prob = norm_topk_prob
         self.routed_scaling_factor = routed_scaling_factor
         self.weight = nn.Parameter(torch.empty(num_experts, hidden_dim))
@@ -149,8 +172,7 @@ class GLM4SigmoidRouter(nn.Module):
     def forward(self, hidden_states: torch.Tensor):
         B, S, H = hidden_states.shape
         h = hidden_states.reshape(B * S, H)
-        if not self.norm_topk_prob:
-            raise NotImplementedError("norm_topk_prob=False is not used by GLM-4.5-Air")
         idx, w, _ = glm_route(h, self.weight, self.top_k, bias=self.selection_bias,
-                              scaling=self.routed_scaling_factor)
+                              scaling=self.routed_scaling_factor, n_group=self.n_group,
+                              topk_group=self.topk_group, norm_topk_prob=self.norm_topk_prob)
         return idx, w.to(hidden_states.dtype)

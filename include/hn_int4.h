@@ -102,10 +102,21 @@ int hn_router_logits(const void* h, long ld_h, const void* w, long ld_w, int w_d
 
 /* Top-k routing from fp32 logits.  mode 0: softmax over the selected logits and
  * renormalise (model/router.py:109-120); mode 1: sigmoid, optional selection-only
- * bias[E] (may be NULL), weights / (sum + eps) * scaling (model/glm4.py:282-309).
+ * bias[E] (may be NULL), weights / (sum + eps) * scaling (model/glm4.py:282-309);
+ * mode 2: as mode 1 without the normalisation, weights = sigmoid * scaling
+ * (norm_topk_prob=False, model/glm4.py:302-307).
  * Ties go to the lower expert index.  idx_out int32 [T, k], w_out fp16 [T, k]. */
 int hn_router_topk(const void* logits, const void* bias, long T, long E, long k, int mode,
                    float eps, float scaling, int* idx_out, void* w_out, void* stream);
+
+/* Group-limited selection of GLM4SigmoidRouter.forward (model/glm4.py:285-298):
+ * out[T, E] fp32 = logits, with -inf for every expert outside the token's
+ * topk_group groups of largest max-sigmoid (groups = n_group runs of E/n_group
+ * consecutive experts; equal group scores: the lower group).  A -inf logit has
+ * sigmoid 0, the reference's masked score; hn_router_topk mode 1/2 then
+ * selects from out.  n_group | E, n_group <= 64, E <= 256; out may equal logits. */
+int hn_router_group_limit(const void* logits, long T, long E, long n_group, long topk_group,
+                          void* out, void* stream);
 
 /* Stable counting sort of the [T*k] assignments by expert (the per-expert
  * torch.where loop of MixtralMoELayer.forward, model/mixtral.py:296-338).

@@ -119,6 +119,15 @@ def router_topk(logits: np.ndarray, k: int, mode: int, bias=None, eps: float = 1
     return idx, w.view(np.float16)
 
 
+def router_group_limit(logits: np.ndarray, n_group: int, topk_group: int) -> np.ndarray:
+    """Logits with -inf outside each token's topk_group best groups (max sigmoid)."""
+    T, E = logits.shape
+    out = np.empty((T, E), np.float32)
+    lib().oracle_router_group_limit(_p(_c(logits, np.float32)), L(T), L(E), L(n_group),
+                                    L(topk_group), _p(out))
+    return out
+
+
 def moe_permute(idx: np.ndarray, E: int):
     flat = _c(idx, np.int32).reshape(-1)
     n = flat.size

@@ -177,11 +177,40 @@ void oracle_router_logits(const uint16_t* h, const void* w, int w_dtype, long T,
 
 static float sigmoid_cr(float l) { return (float)(1.0 / (1.0 + exp(-(double)l))); }
 
+/* ---------------- group-limited selection (model/glm4.py:285-298): group score
+ * = max sigmoid over the group's E / n_group consecutive experts; the
+ * topk_group largest groups are kept (equal scores: the lower group first);
+ * out = logits with -inf (sigmoid 0, the masked score) outside them. */
+void oracle_router_group_limit(const float* logits, long T, long E, long n_group,
+                               long topk_group, float* out) {
+  const long gs = E / n_group;
+  float gsc[256];
+  for (long t = 0; t < T; ++t) {
+    const float* l = logits + t * E;
+    for (long g = 0; g < n_group; ++g) {
+      float m = -INFINITY;
+      for (long j = 0; j < gs; ++j) {
+        const float v = sigmoid_cr(l[g * gs + j]);
+        if (v > m) m = v;
+      }
+      gsc[g] = m;
+    }
+    for (long g = 0; g < n_group; ++g) {
+      long rank = 0;
+      for (long o = 0; o < n_group; ++o)
+        if (gsc[o] > gsc[g] || (gsc[o] == gsc[g] && o < g)) ++rank;
+      for (long j = 0; j < gs; ++j)
+        out[t * E + g * gs + j] = rank < topk_group ? l[g * gs + j] : -INFINITY;
+    }
+  }
+}
+
 /* ---------------- top-k
  * mode 0 (model/router.py:109-120): topk over logits (ties: lower index first),
  *   p = softmax(selected) in fp32, w = p / sum(p), fp16.
  * mode 1 (model/glm4.py:282-309): s = sigmoid(l); select by s + bias (bias may be
- *   NULL; a selection-only bias), w = s_sel / (sum + eps) * scaling, fp16. */
+ *   NULL; a selection-only bias), w = s_sel / (sum + eps) * scaling, fp16.
+ * mode 2 (norm_topk_prob=False, model/glm4.py:302-307): as mode 1, w = s_sel * scaling. */
 void oracle_router_topk(const float* logits, const float* bias, long T, long E, long k, int mode,
                         float eps, float scaling, int32_t* idx_out, uint16_t* w_out) {
   float key[64];
@@ -191,7 +220,7 @@ void oracle_router_topk(const float* logits, const float* bias, long T, long E, 
     int n = 0;
     for (int e = 0; e < E; ++e) {
       float v = l[e];
-      if (mode == 1) {
+      if (mode >= 1) {
         v = sigmoid_cr(v);
         if (bias) v = v + bias[e];
       }
@@ -218,7 +247,7 @@ void oracle_router_topk(const float* logits, const float* bias, long T, long E, 
         s += wt[i];
       }
       for (int i = 0; i < n; ++i) wt[i] = wt[i] / s;
-    } else {
+    } else if (mode == 1) {
       float s = 0.0f;
       for (int i = 0; i < n; ++i) {
         wt[i] = sigmoid_cr(l[sel[i]]);
@@ -226,6 +255,8 @@ void oracle_router_topk(const float* logits, const float* bias, long T, long E, 
       }
       const float d = s + eps;
       for (int i = 0; i < n; ++i) wt[i] = (wt[i] / d) * scaling;
+    } else {
+      for (int i = 0; i < n; ++i) wt[i] = sigmoid_cr(l[sel[i]]) * scaling;
     }
     for (int i = 0; i < k; ++i) {
       idx_out[t * k + i] = i < n ? sel[i] : -1;

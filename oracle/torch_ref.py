@@ -89,15 +89,29 @@ def affinity_bonus(logits: torch.Tensor, cached, bonus: float = 0.1,
 
 
 def glm_router(h: torch.Tensor, w: torch.Tensor, top_k: int, bias=None, eps: float = 1e-9,
-               scaling: float = 1.0):
+               scaling: float = 1.0, n_group: int = 1, topk_group: int = 1,
+               norm_topk_prob: bool = True):
+    """GLM4SigmoidRouter.forward (model/glm4.py:275-309): fp32 logits, sigmoid,
+    group-limited selection when n_group > 1 (group score = max score in the
+    group, the topk_group best groups kept, the other experts' scores zeroed,
+    :285-298), top-k, weights / (sum + eps) when norm_topk_prob, * scaling, fp16.
+    bias (this build's extension): added to the scores for selection only."""
     logits = F.linear(h.float(), w.float())
     scores = torch.sigmoid(logits)
+    if n_group > 1 and topk_group > 0:
+        E = scores.shape[-1]
+        grouped = scores.view(-1, n_group, E // n_group)
+        top_groups = grouped.max(dim=-1).values.topk(topk_group, dim=-1).indices
+        mask = torch.zeros_like(grouped)
+        mask.scatter_(1, top_groups.unsqueeze(-1).expand(-1, -1, E // n_group), 1.0)
+        scores = (grouped * mask).view(-1, E)
     if bias is None:
         tw, ti = scores.topk(top_k, dim=-1)
     else:
         _, ti = (scores + bias.float()).topk(top_k, dim=-1)
         tw = scores.gather(-1, ti)
-    tw = tw / (tw.sum(dim=-1, keepdim=True) + eps)
+    if norm_topk_prob:
+        tw = tw / (tw.sum(dim=-1, keepdim=True) + eps)
     tw = tw * scaling
     return ti, tw.to(h.dtype), logits
 

@@ -3,6 +3,7 @@
 Run in the build container only (the reference tree is not on the GPU box):
 
     python tests/golden/make_golden.py /root/reference
+    python tests/golden/make_golden.py /root/reference grouped_router   # one fixture
 
 The reference package is mapped to the name ``hydranet`` without executing its
 package __init__ files (only the modules listed below are imported).  What it
@@ -14,6 +15,8 @@ pins, per fixture (all small, CPU, seeded):
   expert_mlp.npz        ExpertMLPTriton.forward torch path       (kernels/expert_mlp.py:254-330)
   topk_router.npz       TopKRouter.forward, affinity off          (model/router.py:73-130)
   sigmoid_router.npz    GLM4SigmoidRouter.forward                 (model/glm4.py:261-309)
+  grouped_router.npz    GLM4SigmoidRouter.forward with group-limited selection
+                        (n_group > 1) and norm_topk_prob=False    (model/glm4.py:285-307)
   blob_layout.json      BlobLayout.from_dims at Mixtral/GLM dims  (cache/packed_expert_store.py:77-108)
   mixtral_moe_layer.npz MixtralMoELayer.forward, top-2 and top-1  (model/mixtral.py:259-370)
                         (fp16 dequantise-then-F.linear branch, every expert registered in a
@@ -96,6 +99,54 @@ def quantize_cases():
     t[3, 5] = 1e-3
     cases["edge_4x256_g128"] = (t.to(torch.float16), 128)
     return cases
+
+
+# Group-limited / unnormalised sigmoid routing cases:
+# (E, top_k, n_group, topk_group, norm_topk_prob, routed_scaling_factor, seed)
+GROUPED_ROUTER_CASES = {
+    "g8_t3_k6_norm": (64, 6, 8, 3, True, 1.0, 51),
+    "g1_k8_nonorm_s2.5": (128, 8, 1, 1, False, 2.5, 52),
+    "g4_t2_k8_nonorm": (32, 8, 4, 2, False, 1.0, 53),
+    "g16_t4_k8_norm_s1.5": (128, 8, 16, 4, True, 1.5, 54),
+}
+
+
+def grouped_router_fixture(glm4, cfg) -> None:
+    """GLM4SigmoidRouter.forward with n_group > 1 / norm_topk_prob=False, 32
+    tokens of H = 256 per case; inputs rejected unless the group choice and
+    the top-k are tie-free (so the fixture pins the routing, not a tie-break)."""
+    out = {}
+    H, T = 256, 32
+    for name, (E, k, ng, tg, norm, scale, seed) in GROUPED_ROUTER_CASES.items():
+        gc = cfg.GLM4AirConfig()
+        gc.hidden_dim = H
+        gc.num_experts = E
+        gc.experts_per_token = k
+        gc.n_group = ng
+        gc.topk_group = tg
+        gc.norm_topk_prob = norm
+        gc.routed_scaling_factor = scale
+        sr = glm4.GLM4SigmoidRouter(gc, 0)
+        g2 = torch.Generator().manual_seed(seed)
+        sr.weight.data = torch.randn(E, H, generator=g2) * 0.05
+        h = _f16(seed + 100, (1, T, H), 1.0)
+        with torch.no_grad():
+            ti, tw = sr(h)
+            sc = torch.sigmoid(torch.nn.functional.linear(h.view(-1, H).float(), sr.weight.float()))
+        if ng > 1:
+            gmax = sc.view(T, ng, E // ng).max(dim=-1).values
+            _assert_tie_free(gmax, tg, f"{name} group choice")
+            keep = torch.zeros(T, ng)
+            keep.scatter_(1, gmax.topk(tg, dim=-1).indices, 1.0)
+            sc = (sc.view(T, ng, E // ng) * keep.unsqueeze(-1)).view(T, E)
+        _assert_tie_free(sc, k, f"{name} top-k")
+        out[f"{name}/w"] = sr.weight.data.numpy()
+        out[f"{name}/h"] = _bits(h)
+        out[f"{name}/idx"] = ti.numpy().astype(np.int32)
+        out[f"{name}/wts"] = _bits(tw)
+        out[f"{name}/cfg"] = np.array([E, k, ng, tg, int(norm)], dtype=np.int64)
+        out[f"{name}/scaling"] = np.array(scale, dtype=np.float64)
+    np.savez_compressed(os.path.join(HERE, "grouped_router.npz"), **out)
 
 
 def main(root: str) -> None:
@@ -220,6 +271,7 @@ def main(root: str) -> None:
                            int(gc.norm_topk_prob)], dtype=np.int64)
     out["scaling"] = np.array(gc.routed_scaling_factor, dtype=np.float64)
     np.savez_compressed(os.path.join(HERE, "sigmoid_router.npz"), **out)
+    grouped_router_fixture(glm4, cfg)
 
     # ---- BlobLayout
     lay = {}
@@ -400,5 +452,16 @@ def store_format_fixture(pw, cfg, store) -> None:
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def only_grouped_router(root: str) -> None:
+    _map_reference(root)
+    cfg = importlib.import_module("hydranet.config")
+    glm4 = importlib.import_module("hydranet.model.glm4")
+    grouped_router_fixture(glm4, cfg)
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    _root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    if len(sys.argv) > 2 and sys.argv[2] == "grouped_router":
+        only_grouped_router(_root)
+    else:
+        main(_root)

@@ -43,7 +43,7 @@ def _fp16_ulp(v: torch.Tensor) -> torch.Tensor:
     return torch.pow(2.0, e - 10)
 
 
-def assert_only_near_ties(idx_gpu, logits_ref, k, what=""):
+def assert_only_near_ties(idx_gpu, logits_ref, k, what="", tol_abs=None):
     """The GPU's routing may differ from a top-k over the oracle's own logits
     only where the oracle's logits are within one fp16 ulp of a tie at the
     top-k boundary (two summation orders of the same fp16 Linear round a
@@ -53,7 +53,7 @@ def assert_only_near_ties(idx_gpu, logits_ref, k, what=""):
     idx_gpu = idx_gpu.long().cpu().reshape(lg.shape[0], k)
     srt = torch.sort(lg, dim=-1, descending=True)[0]
     kth = srt[:, k - 1]
-    tol = _fp16_ulp(kth)
+    tol = _fp16_ulp(kth) if tol_abs is None else torch.full_like(kth, tol_abs)
     idx_ref = torch.topk(lg, k, dim=-1)[1]
     differ = [t for t in range(lg.shape[0])
               if set(idx_gpu[t].tolist()) != set(idx_ref[t].tolist())]
@@ -340,7 +340,14 @@ def test_glm_moe_layer_c3(T, decode_path):
         lin.weight.data = (torch.randn(*lin.weight.shape, generator=g) * 0.02).half().to(DEV)
     h = _randn(9, (1, T, 4096))
     out = layer(h.to(DEV))
-    idx, w = layer.router(h.to(DEV))
+    # the routing this forward used; it may differ from a top-8 over the
+    # oracle's fp32 logits only at near-ties of the selection keys (sigmoid +
+    # bias; the GPU logits are fp32 sums in another order, ~1e-6 apart)
+    idx, w = layer.last_routing
+    lg_ref = torch_ref.glm_router(h.view(T, 4096), layer.router.weight.data.cpu(), 8,
+                                  bias=bias)[2]
+    keys = torch.sigmoid(lg_ref) + bias
+    assert_only_near_ties(idx, keys, 8, f"GLM C3 T={T}", tol_abs=1e-5)
     used = sorted(set(idx.view(-1).tolist()))
     cpu = {e: slot_to_cpu(slots[e]) for e in used}
     shared = tuple(l.weight.data.cpu() for l in (layer.shared_expert.gate_proj,
@@ -352,6 +359,90 @@ def test_glm_moe_layer_c3(T, decode_path):
     # the experts the forward routed to, for the next layer's prefetch
     # (model/glm4.py:469, 704-713)
     assert layer.get_last_selected_experts() == used
+
+
+@pytest.mark.parametrize("E,ng,tg", [(64, 8, 3), (128, 16, 4), (256, 64, 7), (32, 4, 4),
+                                      (160, 5, 2), (96, 3, 1)])
+@pytest.mark.parametrize("ties", [False, True])
+def test_group_limit_vs_oracle(E, ng, tg, ties):
+    """hn_router_group_limit against the C oracle bit for bit (the kept logits
+    and the -inf of the other groups), with exact ties between group scores
+    when the logits are rounded to 1/2 (the lower group wins)."""
+    from hydranet_amd.model.router import group_limit
+    g = torch.Generator().manual_seed(E * 7 + ng + (3 if ties else 0))
+    lg = torch.randn(40, E, generator=g) * 2.0
+    if ties:
+        lg = torch.round(lg * 2.0) / 2.0
+    out = group_limit(lg.to(DEV), ng, tg).cpu().numpy()
+    ref = oracle.router_group_limit(lg.numpy(), ng, tg)
+    np.testing.assert_array_equal(out.view(np.uint32), ref.view(np.uint32))
+    kept = np.isfinite(out).reshape(40, ng, E // ng).all(-1).sum(-1)
+    assert (kept == tg).all()
+
+
+def test_grouped_router_golden():
+    """GLM4SigmoidRouter with group-limited selection and norm_topk_prob=False
+    against the fixtures the reference's GLM4SigmoidRouter.forward wrote
+    (model/glm4.py:285-307): indices exact, weights bit for bit against the C
+    oracle over the GPU's own logits, within 1e-3 of the reference's."""
+    from hydranet_amd.model.router import GLM4SigmoidRouter, group_limit, router_logits
+    z = np.load(os.path.join(GOLD, "grouped_router.npz"), allow_pickle=False)
+    names = sorted({key.split("/")[0] for key in z.keys()})
+    for nm in names:
+        E, k, ng, tg, norm = (int(v) for v in z[f"{nm}/cfg"])
+        sc = float(z[f"{nm}/scaling"])
+        r = GLM4SigmoidRouter(256, E, k, norm_topk_prob=bool(norm), routed_scaling_factor=sc,
+                              n_group=ng, topk_group=tg).to(DEV)
+        r.weight.data = torch.from_numpy(z[f"{nm}/w"]).to(DEV)
+        h = torch.from_numpy(_f16(z[f"{nm}/h"]).copy()).view(1, -1, 256).to(DEV)
+        idx, w = r(h)
+        np.testing.assert_array_equal(idx.cpu().numpy(), z[f"{nm}/idx"], err_msg=nm)
+        np.testing.assert_allclose(w.cpu().float().numpy(), _f16(z[f"{nm}/wts"]).astype(np.float32),
+                                   atol=1e-3, err_msg=nm)
+        lg = router_logits(h.view(-1, 256), r.weight.data).cpu().numpy()
+        sel = oracle.router_group_limit(lg, ng, tg) if ng > 1 else lg
+        idx_o, w_o = oracle.router_topk(sel, k, mode=1 if norm else 2, scaling=sc)
+        np.testing.assert_array_equal(idx.cpu().numpy(), idx_o, err_msg=nm)
+        np.testing.assert_array_equal(w.cpu().numpy().view(np.uint16), w_o.view(np.uint16),
+                                      err_msg=nm)
+
+
+def test_glm_moe_layer_grouped_unnormalised():
+    """A GLM MoE layer with group-limited routing (8 groups, 3 kept), unnormalised
+    scaled weights and two shared experts (one dense MLP twice as wide,
+    model/glm4.py:341-344) against the oracle dispatch over the routing the
+    forward used; that routing against the oracle's own group limit + top-k
+    (near-ties only)."""
+    from hydranet_amd.model.moe import GLM4MoELayer
+    from hydranet_amd.preprocess.synthetic import slot_to_cpu
+    H, I, E, k, T = 1024, 512, 64, 6, 24
+    slots = _slots(E, H, I, seed0=2000)
+    layer = GLM4MoELayer(H, I, E, k, slots=slots, routed_scaling_factor=1.5,
+                         num_shared_experts=2, n_group=8, topk_group=3,
+                         norm_topk_prob=False).to(DEV).half()
+    assert layer.shared_expert.gate_proj.out_features == 2 * I
+    g = torch.Generator().manual_seed(21)
+    layer.router.weight.data = (torch.randn(E, H, generator=g) * 0.05).float().to(DEV)
+    for lin in (layer.shared_expert.gate_proj, layer.shared_expert.up_proj,
+                layer.shared_expert.down_proj):
+        lin.weight.data = (torch.randn(*lin.weight.shape, generator=g) * 0.02).half().to(DEV)
+    h = _randn(22, (1, T, H))
+    out = layer(h.to(DEV))
+    idx, w = layer.last_routing
+    wcpu = layer.router.weight.data.cpu()
+    ti, tw, lg_ref = torch_ref.glm_router(h.view(T, H), wcpu, k, scaling=1.5, n_group=8,
+                                          topk_group=3, norm_topk_prob=False)
+    masked = torch.from_numpy(oracle.router_group_limit(lg_ref.numpy(), 8, 3))
+    assert_only_near_ties(idx, torch.sigmoid(masked), k, "GLM grouped", tol_abs=1e-5)
+    used = sorted(set(idx.view(-1).tolist()))
+    cpu = {e: slot_to_cpu(slots[e]) for e in used}
+    shared = tuple(l.weight.data.cpu() for l in (layer.shared_expert.gate_proj,
+                                                  layer.shared_expert.up_proj,
+                                                  layer.shared_expert.down_proj))
+    ref = torch_ref.glm_moe(h.view(T, H), None, cpu, shared, routing=(idx.long().cpu(), w.cpu()))
+    _close(out.view(T, H), ref)
+    # the unnormalised weights: sigmoid * 1.5, not summing to 1.5
+    assert not torch.allclose(w.float().sum(-1).cpu(), torch.full((T,), 1.5), atol=1e-2)
 
 
 # --------------------------------------------------------------------------- fused routing

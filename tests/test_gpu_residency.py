@@ -67,8 +67,10 @@ def _layers(cm, experts, layer):
 
 def _manager(store, base):
     cfg = MoEModelConfig(num_layers=L, num_experts=E, hidden_dim=H, intermediate_dim=I)
+    # a partial slot cache on purpose (evictions): no automatic resident arenas
     cm = ExpertCacheManager(cfg, ExpertCacheConfig(0, base // 2, base - base // 2,
-                                                   enable_dynamic_slots=False), device=DEV)
+                                                   enable_dynamic_slots=False,
+                                                   resident_when_fits=False), device=DEV)
     cm.set_packed_store(store)
     return cm
 
@@ -204,12 +206,115 @@ def test_affinity_bonus_with_partial_cache(store):
                                                          "down_packed", "down_scales"))
                    for e in range(E)}
             ref = torch_ref.moe_dispatch(x.view(T, H).cpu(), idx.long().cpu(), w.cpu(), cpu)
-            # output bar on the unscaled N(0, 1) tokens (a token scaled by 30 has
-            # activations far outside the inputs the fp16 bar is stated for)
-            rows = slice(1, T) if step % 4 == 3 else slice(0, T)
-            err = (out.view(T, H)[rows].float().cpu() - ref[rows].float()).abs()
-            ref = ref[rows]
-            assert bool((err <= 1e-2 + 2e-3 * ref.float().abs()).all()), err.max()
+            # the fp16 bar (max-abs 1e-2, relative 2e-3) is stated for N(0, 1)
+            # activations; a token scaled by 30 is held to the same bar with the
+            # absolute part scaled by 30 (its products, and their roundings, are
+            # 30 times larger)
+            err = (out.view(T, H).float().cpu() - ref.float()).abs()
+            atol = torch.full((T, 1), 1e-2)
+            if step % 4 == 3:
+                atol[0] = 30 * 1e-2
+            assert bool((err <= atol + 2e-3 * ref.float().abs()).all()), err.max()
         assert gated > 0
+    finally:
+        cm.shutdown()
+
+
+def test_auto_resident_when_the_experts_fit(store):
+    """With the default config the manager makes every layer resident when
+    the device's free HBM (less the headroom) holds their arenas: no misses,
+    and the same bits as fixed slots."""
+    st, experts = store
+    cfg = MoEModelConfig(num_layers=L, num_experts=E, hidden_dim=H, intermediate_dim=I)
+    cm = ExpertCacheManager(cfg, ExpertCacheConfig(0, 1, 2), device=DEV)
+    try:
+        cm.set_packed_store(st)
+        assert cm.auto_resident_layers == L and cm.get_stats()["resident_layers"] == L
+        ref, got = _layers(cm, experts, 1)
+        for T in (1, 16):
+            x = torch.randn(1, T, H, generator=torch.Generator().manual_seed(40 + T)).half().to(DEV)
+            assert torch.equal(ref(x), got(x)), T
+        assert cm.get_stats()["total_misses"] == 0
+    finally:
+        cm.shutdown()
+
+
+def test_full_mixtral_layer_store_to_arena(tmp_path):
+    """One full Mixtral layer (8 experts of 4096 -> 14336 -> 4096, INT4 g128,
+    8 x 90.8 MB) written to experts.bin by the GPU quantiser, loaded by the
+    manager into its resident arena (store -> pinned staging -> HBM), and the
+    C2 decode layer (T = 1, 4, 16) run over it: bit-identical to the same
+    layer over fixed slots quantised from the same weights."""
+    from hydranet_amd.model.moe import MixtralMoELayer
+    from hydranet_amd.preprocess.synthetic import expert_seed, normal_f16
+    HF, IF, EF = 4096, 14336, 8
+    print("[full layer] writing 8 Mixtral experts", flush=True)
+
+    def weights(e):
+        s = expert_seed(0, e, 77)
+        return {"gate_proj": normal_f16((IF, HF), 3 * s, 0.02, DEV),
+                "up_proj": normal_f16((IF, HF), 3 * s + 1, 0.02, DEV),
+                "down_proj": normal_f16((HF, IF), 3 * s + 2, 0.02, DEV)}
+
+    ps.pack_experts(((0, e, weights(e)) for e in range(EF)), tmp_path, 1, EF, HF, IF, G,
+                    model_type="mixtral")
+    st = PackedExpertStore(tmp_path / "experts.idx", device=DEV)
+    cfg = MoEModelConfig(num_layers=1, num_experts=EF, hidden_dim=HF, intermediate_dim=IF)
+    cm = ExpertCacheManager(cfg, ExpertCacheConfig(), device=DEV)
+    try:
+        cm.set_packed_store(st)
+        assert cm.is_resident(0)
+        print("[full layer] arena loaded", flush=True)
+        fixed = []
+        for e in range(EF):
+            blob = torch.from_numpy(np.frombuffer(st.get_expert_blob(0, e)[0], dtype=np.uint8)
+                                    .copy()).to(DEV)
+            s = GpuExpertSlot(e, HF, IF, G, DEV)
+            s.slab.copy_(blob)
+            fixed.append(s)
+        ref = MixtralMoELayer(HF, EF, 2, layer_idx=0, slots=fixed).to(DEV)
+        got = MixtralMoELayer(HF, EF, 2, layer_idx=0, cache_manager=cm,
+                              enable_affinity_bonus=False).to(DEV)
+        w = (torch.randn(EF, HF, generator=torch.Generator().manual_seed(3)) * 0.05).half()
+        for m in (ref, got):
+            m.eval()
+            m.router.gate.weight.data.copy_(w.to(DEV))
+        for T in (1, 4, 16):
+            x = torch.randn(1, T, HF, generator=torch.Generator().manual_seed(T)).half().to(DEV)
+            a, b = ref(x), got(x)
+            torch.cuda.synchronize()
+            assert torch.equal(a, b), T
+        assert cm.get_stats()["total_misses"] == 0
+    finally:
+        cm.shutdown()
+        st.close()
+
+
+def test_glm_prefetch_predicted_loads_missing_experts(store):
+    """GLM4MoELayer.prefetch_predicted (model/glm4.py:351-363): the predicted
+    experts that are not cached start loading into slots with no hit or miss
+    counted; a later use is a hit on the loaded bytes; cached experts are not
+    loaded again."""
+    from hydranet_amd.model.moe import GLM4MoELayer
+    st, experts = store
+    cm = _manager(st, 3)
+    try:
+        layer = GLM4MoELayer(H, I, E, 2, layer_idx=0, cache_manager=cm).to(DEV).half()
+        n0 = st.get_stats()["load_count"]
+        assert not cm.is_cached(0, 2) and not cm.is_cached(0, 5)
+        layer.prefetch_predicted([2, 5])
+        assert cm.is_cached(0, 2) and cm.is_cached(0, 5)
+        assert st.get_stats()["load_count"] == n0 + 2
+        stats = cm.get_stats()
+        assert stats["total_hits"] == 0 and stats["total_misses"] == 0
+        for e in (2, 5):
+            s = cm.get_int4_slot(0, e)
+            torch.cuda.current_stream().synchronize()
+            for n, v in experts[(0, e)].items():
+                assert torch.equal(getattr(s, n).cpu(), v), (e, n)
+        stats = cm.get_stats()
+        assert stats["total_hits"] == 2 and stats["total_misses"] == 0
+        layer.prefetch_predicted([5, 2])
+        assert st.get_stats()["load_count"] == n0 + 2
     finally:
         cm.shutdown()

@@ -173,6 +173,82 @@ def test_sigmoid_router_matches_reference_golden():
     np.testing.assert_allclose(lg, logits_t, atol=1e-4, rtol=1e-4)
 
 
+def _grouped_cases():
+    z = _npz("grouped_router.npz")
+    names = sorted({k.split("/")[0] for k in z.keys()})
+    return z, names
+
+
+def test_grouped_router_matches_reference_golden():
+    """torch_ref.glm_router with group-limited selection and norm_topk_prob=False
+    equals GLM4SigmoidRouter.forward run by the reference (model/glm4.py:285-307),
+    indices and fp16 weights bit for bit."""
+    z, names = _grouped_cases()
+    assert len(names) == 4
+    for nm in names:
+        E, k, ng, tg, norm = (int(v) for v in z[f"{nm}/cfg"])
+        h = torch.from_numpy(_f16(z[f"{nm}/h"]).reshape(-1, 256))
+        w = torch.from_numpy(z[f"{nm}/w"])
+        idx, wt, _ = torch_ref.glm_router(h, w, k, scaling=float(z[f"{nm}/scaling"]),
+                                          n_group=ng, topk_group=tg, norm_topk_prob=bool(norm))
+        np.testing.assert_array_equal(idx.numpy(), z[f"{nm}/idx"], err_msg=nm)
+        np.testing.assert_array_equal(wt.numpy().view(np.uint16), z[f"{nm}/wts"], err_msg=nm)
+
+
+def test_c_oracle_grouped_router_matches_reference_golden():
+    """The C oracle's group limit + sigmoid top-k (modes 1 and 2) over fp32
+    logits reproduces the reference's grouped / unnormalised routing."""
+    z, names = _grouped_cases()
+    for nm in names:
+        E, k, ng, tg, norm = (int(v) for v in z[f"{nm}/cfg"])
+        h = _f16(z[f"{nm}/h"]).reshape(-1, 256).astype(np.float32)
+        lg = torch.nn.functional.linear(torch.from_numpy(h),
+                                        torch.from_numpy(z[f"{nm}/w"])).numpy()
+        sel = oracle.router_group_limit(lg, ng, tg) if ng > 1 else lg
+        if ng > 1:
+            assert (np.isinf(sel).reshape(len(lg), ng, -1).all(-1).sum(-1) == ng - tg).all()
+        idx, wt = oracle.router_topk(sel, k, mode=1 if norm else 2,
+                                     scaling=float(z[f"{nm}/scaling"]))
+        np.testing.assert_array_equal(idx, z[f"{nm}/idx"], err_msg=nm)
+        np.testing.assert_allclose(wt.astype(np.float32), _f16(z[f"{nm}/wts"]).astype(np.float32),
+                                   atol=1e-3, rtol=0, err_msg=nm)
+
+
+def test_grouped_router_planted_mistakes_fail():
+    """Plausible mistakes in the group step each change a fixture: the group
+    score as a sum instead of the max, the groups ignored, normalising when
+    the config says not to."""
+    z, names = _grouped_cases()
+
+    def route(nm, group_score, use_groups, norm_override=None):
+        E, k, ng, tg, norm = (int(v) for v in z[f"{nm}/cfg"])
+        h = torch.from_numpy(_f16(z[f"{nm}/h"]).reshape(-1, 256)).float()
+        s = torch.sigmoid(h @ torch.from_numpy(z[f"{nm}/w"]).t())
+        if use_groups and ng > 1:
+            g = s.view(-1, ng, E // ng)
+            top = group_score(g).topk(tg, dim=-1).indices
+            m = torch.zeros_like(g).scatter_(1, top.unsqueeze(-1).expand(-1, -1, E // ng), 1.0)
+            s = (g * m).view(-1, E)
+        tw, ti = s.topk(k, dim=-1)
+        if (bool(norm) if norm_override is None else norm_override):
+            tw = tw / (tw.sum(-1, keepdim=True) + 1e-9)
+        return ti.numpy(), (tw * float(z[f"{nm}/scaling"])).half().numpy().view(np.uint16)
+
+    grouped = [nm for nm in names if int(z[f"{nm}/cfg"][2]) > 1]
+    for nm in grouped:
+        ti, _ = route(nm, lambda g: g.sum(-1), True)
+        assert not np.array_equal(ti, z[f"{nm}/idx"]), nm
+        ti, _ = route(nm, lambda g: g.max(-1).values, False)
+        assert not np.array_equal(ti, z[f"{nm}/idx"]), nm
+        ti, tw = route(nm, lambda g: g.max(-1).values, True)
+        assert np.array_equal(ti, z[f"{nm}/idx"]) and np.array_equal(tw, z[f"{nm}/wts"]), nm
+    unnorm = [nm for nm in names if int(z[f"{nm}/cfg"][4]) == 0]
+    assert unnorm
+    for nm in unnorm:
+        _, tw = route(nm, lambda g: g.max(-1).values, True, norm_override=True)
+        assert not np.array_equal(tw, z[f"{nm}/wts"]), nm
+
+
 def test_sigmoid_bias_selection_brute_force():
     rng = np.random.default_rng(9)
     T, E, k = 16, 32, 4

@@ -337,3 +337,56 @@ def test_missing_store_is_an_error():
     c = PerLayerCache(0, 4, 0, ExpertCacheConfig(0, 1, 1), CPU)
     with pytest.raises(RuntimeError, match="no packed store"):
         c.get_int4_slot(0)
+
+
+class _SizedManager(ExpertCacheManager):
+    """The manager with a stated free-memory figure (the GPU's, stubbed)."""
+
+    free_bytes = None
+
+    def _free_device_bytes(self):
+        return self.free_bytes
+
+
+@pytest.mark.parametrize("free_layers,headroom,want", [(10.0, 0, 2), (1.5, 0, 1), (0.5, 0, 0),
+                                                       (3.0, 1, 2), (2.5, 1, 1)])
+def test_resident_plan_from_free_memory(store4, free_layers, headroom, want):
+    """Layers become resident arenas, from layer 0, as long as their arenas fit
+    the free memory less the headroom; the others keep the slot cache."""
+    st, experts = store4
+    cfg = MoEModelConfig(num_layers=2, num_experts=4, hidden_dim=H, intermediate_dim=I)
+    per = 4 * ((st.layout.total_size + 255) // 256 * 256)
+    cc = ExpertCacheConfig(0, 1, 1, resident_headroom_bytes=int(headroom * per))
+    cm = _SizedManager(cfg, cc, device=CPU)
+    cm.free_bytes = int(free_layers * per)
+    try:
+        cm.set_packed_store(st)
+        assert cm.layer_resident_bytes() == per
+        assert cm.auto_resident_layers == want
+        assert [cm.is_resident(l) for l in range(2)] == [l < want for l in range(2)]
+        assert cm.get_stats()["resident_layers"] == want
+        for l in range(want):
+            for e in range(4):
+                assert _same(cm.get_int4_slot(l, e), experts[(l, e)])
+        assert cm.get_stats()["total_misses"] == 0
+    finally:
+        cm.shutdown()
+
+
+def test_resident_plan_off(store4):
+    st, _ = store4
+    cfg = MoEModelConfig(num_layers=2, num_experts=4, hidden_dim=H, intermediate_dim=I)
+    cm = _SizedManager(cfg, ExpertCacheConfig(0, 1, 1, resident_when_fits=False), device=CPU)
+    cm.free_bytes = 1 << 40
+    try:
+        cm.set_packed_store(st)
+        assert cm.auto_resident_layers == 0 and not cm.is_resident(0)
+    finally:
+        cm.shutdown()
+    # no figure (a CPU device): the slot cache
+    cm = ExpertCacheManager(cfg, ExpertCacheConfig(0, 1, 1), device=CPU)
+    try:
+        cm.set_packed_store(st)
+        assert cm.auto_resident_layers == 0
+    finally:
+        cm.shutdown()
