@@ -339,6 +339,8 @@ def bench_c3(args, T: int = 32, n_layers: int = 2):
     for L in range(n_layers):
         slots = [make_expert_slot(expert_seed(L, e), H, I, g, slot_idx=e) for e in range(E)]
         layer = GLM4MoELayer(H, I, E, k, layer_idx=L, slots=slots).cuda().half()
+        if args.fused_routing is not None:
+            layer.fused_routing = bool(args.fused_routing)
         gen = torch.Generator(device="cuda").manual_seed(9000 + L)
         layer.router.weight.data = (torch.randn(E, H, generator=gen, device="cuda") * 0.02).float()
         layer.router.selection_bias = torch.rand(E, generator=gen, device="cuda") * 0.2 - 0.1
@@ -891,6 +893,9 @@ def main():
                          "h2d: the expert-miss load path (pinned -> HBM, and from a store "
                          "on disk)")
     ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--fused-routing", type=int, default=None, choices=[0, 1],
+                    help="c3: routing inside the gate/up kernel (1) or its own launch (0); "
+                         "default: the layer's")
     ap.add_argument("--decode-tokens", type=int, default=256, help="c5: tokens generated")
     ap.add_argument("--warmup-decode", type=int, default=3, help="c5: untimed decode forwards")
     ap.add_argument("--skip-c5", action="store_true",

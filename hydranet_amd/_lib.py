@@ -56,6 +56,9 @@ SIGNATURES: dict[str, list] = {
     "hn_moe_decode_layer": [P, L, P, L, P, L, L, L, P, L, L, L, F, F, P, P, P, P, P, P, P, P,
                             P, P, P, L, P, L, P],
     "hn_expert_mlp_int4_noalloc": [P, P, P, P, P, P, P, P, L, L, L, L, P],
+    "hn_moe_route_experts_decode_check": [L, L, L, I, L, L, L],
+    "hn_moe_route_experts_decode": [P, P, L, L, L, I, F, F, P, L, P, L, L, L, P, P, P, P, P, P,
+                                    P, P, P, P, P, P, L, P, L, P, L, P],
 }
 
 # Sizes up to which hn_moe_route (one launch: logits, top-k, permutation,

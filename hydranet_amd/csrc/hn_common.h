@@ -157,6 +157,30 @@ __device__ __forceinline__ float hn_silu(float g) {
   return g / (1.0f + expf(-g));
 }
 
+// dst[0, n) = src[0, n) (global fp32 -> LDS) with every load of a round in
+// flight before the first store: rounds of four 16-byte loads per thread
+// (a plain loop waits out one memory round trip per element it copies).
+// src and dst 16-byte aligned.
+__device__ __forceinline__ void copy_to_lds_f32(const float* __restrict__ src, float* dst, int n) {
+  const int nv = n >> 2, nthr = blockDim.x, tid = threadIdx.x;
+  const float4_t* s4 = reinterpret_cast<const float4_t*>(src);
+  float4_t* d4 = reinterpret_cast<float4_t*>(dst);
+  for (int base = 0; base < nv; base += 4 * nthr) {
+    float4_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + tid + u * nthr;
+      v[u] = i < nv ? s4[i] : float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + tid + u * nthr;
+      if (i < nv) d4[i] = v[u];
+    }
+  }
+  for (int i = 4 * nv + tid; i < n; i += nthr) dst[i] = src[i];
+}
+
 static inline int hn_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
 // ---------------------------------------------------------------------------

@@ -600,6 +600,14 @@ extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const vo
                                             int* inv, int* active, int* n_active,
                                             long long* usage, void* h_ws, void* stream,
                                             int dry_run);
+extern "C" int hn_stream_route_sel_gate_up_impl(const void* hx, long ld_hx,
+                                                const float* logits_in, const float* bias, long T,
+                                                long E, long k, int mode, float eps,
+                                                float scaling, const void* table, long H, long I,
+                                                long group, int* idx, void* w, int* offsets,
+                                                int* perm, int* inv, int* active, int* n_active,
+                                                long long* usage, void* h_ws, void* stream,
+                                                int dry_run);
 extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, const int* inv,
                                             const int* idx, const void* w, long T, long k,
                                             const void* shared, long ld_sh, void* out,
@@ -1090,6 +1098,91 @@ extern "C" int hn_grouped_decode_phase_int4(int phase, const void* x, const void
   }
   if (rc == HN_NOT_HANDLED) {
     hn_set_error("%s: shape not handled by the streaming kernels", who);
+    return -22;
+  }
+  return rc;
+}
+
+// 0 when hn_moe_route_experts_decode covers the shape, else HN_NOT_HANDLED
+// (sets no error).
+extern "C" int hn_moe_route_experts_decode_check(long T, long E, long k, int mode, long H,
+                                                 long I, long group) {
+  if (g_decode_path != 0) return HN_NOT_HANDLED;
+  static const float dummy = 0.f;
+  if (hn_stream_route_sel_gate_up_impl(nullptr, H, &dummy, nullptr, T, E, k, mode, 0.f, 1.f,
+                                       nullptr, H, I, group, nullptr, nullptr, nullptr, nullptr,
+                                       nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                       1) != 0)
+    return HN_NOT_HANDLED;
+  const long rows = T * k;
+  const bool split = hn_stream_down_split_impl(nullptr, nullptr, nullptr, nullptr, nullptr, E, T,
+                                               rows, H, I, group, nullptr, nullptr, 1) == 0;
+  if (!split && hn_stream_grouped_impl(1, nullptr, I, nullptr, nullptr, nullptr, nullptr, E, T,
+                                       rows, H, I, group, nullptr, H, nullptr, 1) != 0)
+    return HN_NOT_HANDLED;
+  return 0;
+}
+
+// A decode MoE layer from given router logits, in three launches: the
+// routing (top-k in any mode, optional selection bias, E <= 256) computed in
+// the grouped gate/up streaming kernel's prologue with the rows staged from
+// h directly; the down projection (four K slices when I splits, else whole
+// into y_ws); the ordered weighted unpermute with the optional fp16 shared
+// addend.  shared_ready (a hipEvent_t, may be null): the stream waits for it
+// right before the unpermute, so a shared expert computed on another stream
+// overlaps the expert kernels.
+extern "C" int hn_moe_route_experts_decode(const float* logits, const void* bias, long T, long E,
+                                           long k, int mode, float eps, float scaling,
+                                           const void* h, long ld_h, const void* table, long H,
+                                           long I, long group, int* idx, void* w, int* offsets,
+                                           int* perm, int* inv, int* active, int* n_active,
+                                           long long* usage, void* h_ws, void* y_ws,
+                                           void* shared_ready, const void* shared, long ld_sh,
+                                           void* out, long ld_o, void* work, long work_bytes,
+                                           void* stream) {
+  const char* who = "hn_moe_route_experts_decode";
+  HN_ARG_CHECK(logits && aligned16(logits) && aligned16(h) && aligned16(h_ws) && aligned16(y_ws) &&
+                   aligned16(out) &&
+                   ld_o % 8 == 0 && (!shared || (aligned16(shared) && ld_sh % 8 == 0)),
+               "%s: logits needed; logits, h, h_ws, y_ws, shared and out rows 16-byte aligned",
+               who);
+  HN_ARG_CHECK(hn_moe_route_experts_decode_check(T, E, k, mode, H, I, group) == 0,
+               "%s: shape not covered (decode path 0, E <= 256, k <= 16, T k <= the gate/up "
+               "launch's threads, mode 0-2, H %% 512 == 0, group 128; T=%ld E=%ld k=%ld "
+               "mode=%d H=%ld I=%ld group=%ld)", who, T, E, k, mode, H, I, group);
+  hipStream_t s = (hipStream_t)stream;
+  const long rows = T * k;
+  const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
+                                                            : hn_cdiv(H, kTileN);
+  const long need = hn_skinny_workspace_bytes(3, rows, H, I, E);
+  HN_ARG_CHECK(work && work_bytes >= need, "%s: workspace too small (%ld < %ld)", who,
+               work_bytes, need);
+  float* part = (float*)((char*)work + ctr_bytes(E * tmax));
+  int rc = hn_stream_route_sel_gate_up_impl(h, ld_h, logits, (const float*)bias, T, E, k, mode,
+                                            eps, scaling, table, H, I, group, idx, w, offsets,
+                                            perm, inv, active, n_active, usage, h_ws, s, 0);
+  const bool split = hn_stream_down_split_impl(nullptr, nullptr, nullptr, nullptr, nullptr, E, T,
+                                               rows, H, I, group, nullptr, nullptr, 1) == 0;
+  if (rc == 0)
+    rc = split ? hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H,
+                                           I, group, part, s, 0)
+               : hn_stream_grouped_impl(1, h_ws, I, table, active, n_active, offsets, E, T,
+                                        rows, H, I, group, y_ws, H, s, 0);
+  if (rc == 0 && shared_ready) {
+    const hipError_t e = hipStreamWaitEvent(s, (hipEvent_t)shared_ready, 0);
+    if (e != hipSuccess) {
+      hn_set_error("%s: waiting for shared_ready failed: %s", who, hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  if (rc == 0)
+    rc = split ? hn_moe_unpermute_split4_impl(part, rows * H, inv, idx, w, T, k, shared, ld_sh,
+                                              out, ld_o, H, stream)
+               : hn_moe_unpermute(y_ws, H, inv, idx, w, T, k, shared, ld_sh, out, ld_o, H,
+                                  stream);
+  if (rc == HN_NOT_HANDLED) {
+    hn_set_error("%s: the device cannot run this shape's plan (dynamic LDS limit); T=%ld E=%ld "
+                 "k=%ld", who, T, E, k);
     return -22;
   }
   return rc;

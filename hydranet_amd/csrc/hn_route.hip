@@ -242,12 +242,25 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
   int pos[kMaxTopK];
   int ex[kMaxTopK];
   float wt[kMaxTopK];
+  // the token's k (position, expert, weight) loaded together (one memory
+  // round trip, not one per assignment), then ordered by expert
+  int pv[kMaxTopK], ev[kMaxTopK];
+  h16 wv[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    if (s < k) {
+      pv[s] = inv[t * k + s];
+      ev[s] = idx[t * k + s];
+      wv[s] = w[t * k + s];
+    }
+  }
   int n = 0;
-  for (int s = 0; s < k; ++s) {
-    const int j = t * k + s;
-    const int p = inv[j];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    if (s >= k) break;
+    const int p = pv[s];
     if (p < 0) continue;
-    const int e = idx[j];
+    const int e = ev[s];
     // insertion by expert id (ascending): the reference visits experts in
     // unique() order and accumulates into an fp16 buffer
     int q = n;
@@ -259,7 +272,7 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
     }
     ex[q] = e;
     pos[q] = p;
-    wt[q] = (float)w[j];
+    wt[q] = (float)wv[s];
     ++n;
   }
   // the rows of a batch of B selected experts are loaded before any is used
@@ -340,7 +353,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     int* __restrict__ n_active, long long* __restrict__ usage, h16* __restrict__ x_perm,
     long ld_p) {
   // logits, or the MFMA partial tiles (16 waves x 16 LG tokens x 16 experts)
-  __shared__ float s_buf[LG == 4 ? 16 * 64 * 16 : kRouteMaxLogits];
+  __shared__ __align__(16) float s_buf[LG == 4 ? 16 * 64 * 16 : kRouteMaxLogits];
   __shared__ float s_lg[512];               // MFMA logits (T * E <= 512)
   __shared__ int s_sel[kRouteMaxAssign];
   __shared__ h16 s_w[kRouteMaxAssign];
@@ -357,7 +370,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
   // 1. logits
   const float* lg = s_buf;
   if (logits_in) {
-    for (int i = tid; i < T * E; i += blockDim.x) s_buf[i] = logits_in[i];
+    copy_to_lds_f32(logits_in, s_buf, T * E);
   } else if constexpr (LG > 0) {
     const int ksl = H >> 4, kb0 = wave * ksl, steps = ksl >> 5;
     const int tl = lane & 15, kq = (lane >> 4) * 8;
@@ -676,6 +689,7 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
                "%s: h and x_perm rows must be 16-byte aligned with H %% 8 == 0", who);
   HN_ARG_CHECK(logits_in || (w && al16(w) && (w_dtype == 0 ? ld_w % 8 == 0 : ld_w % 4 == 0)),
                "%s: weight rows must be 16-byte aligned (or pass logits_in)", who);
+  HN_ARG_CHECK(!logits_in || al16(logits_in), "%s: logits_in must be 16-byte aligned", who);
   if (T == 0) return 0;
   // about 64 KiB of rows per workgroup; every workgroup repeats the routing
   const long bytes = T * k * H * 2;

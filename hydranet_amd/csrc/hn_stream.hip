@@ -188,6 +188,115 @@ __device__ int route_prologue(const StreamArgs& A, float* part, int* s_act, int*
   return __builtin_amdgcn_readfirstlane(*s_na);
 }
 
+// Decode routing from given logits in the gate/up kernel's prologue (ROUTE
+// 2): any of the top-k modes (Mixtral softmax, GLM sigmoid with an optional
+// selection bias, with or without the normalisation) over E <= 256 experts,
+// T k <= the workgroup's threads.  The arithmetic is moe_route_kernel's
+// (hn_route.hip) from given logits: the top-k of a token by one wave
+// (topk_wave), the stable order by expert from nine ballots over the expert
+// bits per wave and the per-wave counts, the offsets and the active list by
+// wave scans.  Every workgroup computes it into LDS (scratch: the logits, the
+// selection and the per-wave counts, in the staging area used afterwards);
+// workgroup 0 also writes the routing outputs.  Returns the number of
+// active experts (uniform).
+__device__ int route_prologue_sel(const StreamArgs& A, unsigned char* scratch, int* s_act,
+                                  int* s_off, int* rperm, int wave, int lane) {
+  const int tid = threadIdx.x, KW = blockDim.x >> 6;
+  const int T = A.T, E = A.E, k = A.topk, n = T * k;
+  const bool lead = blockIdx.x == 0;
+  float* s_lg = reinterpret_cast<float*>(scratch);          // [T * E]
+  int* s_sel = reinterpret_cast<int*>(s_lg + T * E);        // [n]
+  h16* s_w = reinterpret_cast<h16*>(s_sel + n);             // [n]
+  int* s_wcnt = reinterpret_cast<int*>(s_w + ((n + 1) & ~1));  // [KW][E]
+  int* s_na = s_wcnt + KW * E;
+  for (int i = tid; i < KW * E; i += blockDim.x) s_wcnt[i] = 0;
+  copy_to_lds_f32(A.logits_in, s_lg, T * E);
+  __syncthreads();
+  // 1. top-k, one wave per token
+  for (int t = wave; t < T; t += KW)
+    topk_wave(s_lg + t * E, A.bias, E, k, A.mode, A.eps, A.scaling, lane, s_sel + t * k,
+              s_w + t * k);
+  __syncthreads();
+  // 2. rank among equal experts within the wave (one thread per assignment)
+  const int j = tid;
+  int e = j < n ? s_sel[j] : -1;
+  if (e < 0 || e >= E) e = -1;
+  uint64_t same = ~0ull;
+#pragma unroll
+  for (int b = 0; b < 9; ++b) {
+    const uint64_t bal = __ballot((e >> b) & 1);
+    same &= ((e >> b) & 1) ? bal : ~bal;
+  }
+  const int rank = __popcll(same & ((1ull << lane) - 1));
+  if (e >= 0 && rank == 0) s_wcnt[wave * E + e] = __popcll(same);
+  __syncthreads();
+  // 3. counts, offsets and the active list: 4 experts per lane, wave scans
+  if (wave == 0) {
+    int c[4], f[4], cs = 0, fs = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ex = 4 * lane + q;
+      c[q] = 0;
+      if (ex < E)
+        for (int w2 = 0; w2 < KW; ++w2) c[q] += s_wcnt[w2 * E + ex];
+      f[q] = c[q] > 0 ? 1 : 0;
+      cs += c[q];
+      fs += f[q];
+    }
+    int ci = cs, fi = fs;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int oc = __shfl_up(ci, off, 64), of = __shfl_up(fi, off, 64);
+      if (lane >= off) { ci += oc; fi += of; }
+    }
+    int co = ci - cs, fo = fi - fs;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ex = 4 * lane + q;
+      if (ex < E) {
+        s_off[ex] = co;
+        if (f[q]) s_act[fo] = ex;
+        if (lead) {
+          A.offsets_out[ex] = co;
+          if (f[q]) A.active_out[fo] = ex;
+          if (A.usage && c[q]) A.usage[ex] += c[q];
+        }
+      }
+      co += c[q];
+      fo += f[q];
+    }
+    if (lane == 63) {
+      s_off[E] = ci;
+      *s_na = fi;
+      if (lead) {
+        A.offsets_out[E] = ci;
+        *A.n_active_out = fi;
+      }
+    }
+  }
+  __syncthreads();
+  // 4. the permutation
+  if (j < n) {
+    if (lead) {
+      A.idx_out[j] = s_sel[j];
+      A.w_out[j] = s_w[j];
+    }
+    if (e >= 0) {
+      int pos = s_off[e] + rank;
+      for (int w2 = 0; w2 < wave; ++w2) pos += s_wcnt[w2 * E + e];
+      rperm[pos] = j;
+      if (lead) {
+        A.perm_out[pos] = j;
+        A.inv_out[j] = pos;
+      }
+    } else if (lead) {
+      A.inv_out[j] = -1;
+    }
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(*s_na);
+}
+
 // At most 8 waves per workgroup and one workgroup per CU: 2 waves per SIMD,
 // 256 VGPRs each.
 // KS > 1: the columns of a chunk are (k slice, tile), the slices one after
@@ -204,7 +313,7 @@ template <int MATS, int TH, int LPW>
 constexpr int stream_waves_per_eu() { return MATS == 1 && TH == 1 && LPW <= 4 ? 4 : 1; }
 
 template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS,
-          bool ROUTE = false, int TH = 1>
+          int ROUTE = 0, int TH = 1>
 __global__ __launch_bounds__(512)
 __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void stream_kernel(
     StreamArgs A,
@@ -259,12 +368,29 @@ __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void 
     uint64_t* s_ptr = reinterpret_cast<uint64_t*>(s_off + ((E + 2) & ~1));
     const uint64_t* tw = reinterpret_cast<const uint64_t*>(table);
     int na;
-    if constexpr (ROUTE) {
+    if constexpr (ROUTE == 1) {
       // pointers requested first, stored once the routing is done (4 E <= 32 threads)
       const uint64_t pv = tid < 4 * E ? tw[6 * (tid >> 2) + (tid & 3)] : 0;
       rperm = reinterpret_cast<int*>(s_ptr + 4 * E);
       na = route_prologue(A, reinterpret_cast<float*>(smem), s_act, s_off, rperm, wave, lane);
       if (tid < 4 * E) s_ptr[tid] = pv;
+    } else if constexpr (ROUTE == 2) {
+      // the weight pointers requested first, stored after the routing
+      uint64_t pv[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * (int)blockDim.x;
+        pv[u] = i < 4 * E ? tw[6 * (i >> 2) + (i & 3)] : 0;
+      }
+      rperm = reinterpret_cast<int*>(s_ptr + 4 * E);
+      na = route_prologue_sel(A, smem, s_act, s_off, rperm, wave, lane);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * (int)blockDim.x;
+        if (i < 4 * E) s_ptr[i] = pv[u];
+      }
+      for (int i = tid + 2 * (int)blockDim.x; i < 4 * E; i += blockDim.x)
+        s_ptr[i] = tw[6 * (i >> 2) + (i & 3)];
     } else {
       na = *n_active;
       for (int i = tid; i < E; i += blockDim.x) s_act[i] = active[i];
@@ -376,15 +502,15 @@ __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void 
     const int round = 4 * (int)blockDim.x;
     const bool two = sg.nblk > round;  // uniform
     half8_t v[4], v2[4];
-    stage_load<ROUTE>(A, xsl, sg, 0, v, rperm, st_pr.t0);
-    if (two) stage_load<ROUTE>(A, xsl, sg, round, v2, rperm, st_pr.t0);
+    stage_load<(ROUTE != 0)>(A, xsl, sg, 0, v, rperm, st_pr.t0);
+    if (two) stage_load<(ROUTE != 0)>(A, xsl, sg, round, v2, rperm, st_pr.t0);
     issue_next(b0);
     if (NBUF == 3) issue_next(b1);
     stage_zero_rows(A, sg.Mc, cs);
     stage_store(A, sg, 0, v, xs, cs);
     if (two) stage_store(A, sg, round, v2, xs, cs);
     for (int base = 2 * round; base < sg.nblk; base += round) {
-      stage_load<ROUTE>(A, xsl, sg, base, v, rperm, st_pr.t0);
+      stage_load<(ROUTE != 0)>(A, xsl, sg, base, v, rperm, st_pr.t0);
       stage_store(A, sg, base, v, xs, cs);
     }
     __syncthreads();
@@ -405,7 +531,7 @@ __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<MATS, TH, LPW>()))) void 
         st_ch = ch;
         st_kj = kj;
         sg = geom(ch);
-        stage<ROUTE>(A, st_pr.x + st_kj * A.K, sg, xs, cs, rperm, st_pr.t0);
+        stage<(ROUTE != 0)>(A, st_pr.x + st_kj * A.K, sg, xs, cs, rperm, st_pr.t0);
       }
     }
     issue_next(nxt);
@@ -567,7 +693,8 @@ constexpr int kRouteScratch = 16 * 16 * 16 * 4 + 512 * 4 + 64 * 4 + 64 * 2 + 16;
 bool th2_instantiated(bool /*grouped*/, int /*mats*/, int lpw) { return lpw == 4; }
 
 StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = false,
-                       bool want16 = false, bool grouped = true) {
+                       bool want16 = false, bool grouped = true, long route_rows = 64,
+                       long route_scratch = kRouteScratch) {
   StreamPlan p{};
   const long G = K / 128;
   int lpw = 2;
@@ -585,8 +712,9 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
   p.npair = (int)(kw * lpw / 2);
   p.ldx = p.npair * 128 + 8;  // row stride = 16 B mod 256 B: conflict-free A reads
   // grouped metadata copy: active [E], offsets [E + 1] (each padded to even), pointers [E][4]
-  // (ROUTE: and the permuted-row map, 64 entries)
-  const int meta = (int)(((E + 1) & ~1L) * 4 + ((E + 2) & ~1L) * 4 + E * 32) + (route ? 256 : 0);
+  // (ROUTE: and the permuted-row map, route_rows entries)
+  const int meta = (int)(((E + 1) & ~1L) * 4 + ((E + 2) & ~1L) * 4 + E * 32) +
+                   (route ? (int)(4 * route_rows) : 0);
   const int cs = p.npair * kCsw * 4;
   const int per_tok = 2 * p.ldx * 2;
   for (int th = (want16 && rows > 8 && th2_instantiated(grouped, mats, lpw)) ? 2 : 1;
@@ -601,7 +729,7 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
     p.tc = tc;
     if (p.tc < 1) return p;
     p.lds = p.tc * per_tok + cs + red + meta;
-    if (route && p.tc * per_tok + cs + red < kRouteScratch) return p;
+    if (route && p.tc * per_tok + cs + red < route_scratch) return p;
     // single-matrix (down) launches of 4 or more rows per matrix: as many
     // workgroups per CU (up to four) as their LDS and 16 waves allow, for more
     // loads in flight where a column has little work (measured: gate/up
@@ -621,7 +749,7 @@ StreamPlan stream_plan(long K, int mats, long rows, long E = 0, bool route = fal
 int num_cus() { return hn_device_cus(); }
 
 template <bool GROUPED, int MATS, int EPI, int LPW, int NBUF, bool WIDE, int KS = 1,
-          bool ROUTE = false, int TH = 1>
+          int ROUTE = 0, int TH = 1>
 int launch_one(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p, hipStream_t s) {
   if (p.th != TH) return HN_NOT_HANDLED;  // the plan was sized for the other chunking
   auto kern = stream_kernel<GROUPED, MATS, EPI, LPW, NBUF, WIDE, KS, ROUTE, TH>;
@@ -886,11 +1014,79 @@ extern "C" int hn_stream_route_gate_up_impl(const void* hx, long ld_hx, const vo
   const GroupedPtrs g = {(const SExpert*)table, nullptr, nullptr, nullptr};
   hipStream_t s = (hipStream_t)stream;
   int rc = HN_NOT_HANDLED;
-  if (p.th == 2) rc = launch_one<true, 2, 1, 4, 2, true, 1, true, 2>(A, g, pw, s);
-  else if (p.lpw == 2) rc = launch_one<true, 2, 1, 2, 3, true, 1, true>(A, g, pw, s);
-  else if (p.lpw == 4) rc = launch_one<true, 2, 1, 4, 3, true, 1, true>(A, g, pw, s);
-  else if (p.lpw == 8) rc = launch_one<true, 2, 1, 8, 2, true, 1, true>(A, g, pw, s);
+  if (p.th == 2) rc = launch_one<true, 2, 1, 4, 2, true, 1, 1, 2>(A, g, pw, s);
+  else if (p.lpw == 2) rc = launch_one<true, 2, 1, 2, 3, true, 1, 1>(A, g, pw, s);
+  else if (p.lpw == 4) rc = launch_one<true, 2, 1, 4, 3, true, 1, 1>(A, g, pw, s);
+  else if (p.lpw == 8) rc = launch_one<true, 2, 1, 8, 2, true, 1, 1>(A, g, pw, s);
   if (rc) return rc;
   HN_LAUNCH_CHECK("hn_stream_route_gate_up");
+  return 0;
+}
+
+// Decode routing from given logits fused into the grouped gate/up launch
+// (ROUTE 2): top-k in mode 0 (softmax), 1 (sigmoid) or 2 (sigmoid,
+// unnormalised) with an optional selection bias over E <= 256 experts, T k
+// routed rows (at most the launch's threads), then h_ws = SwiGLU gate/up of
+// the routed rows staged from hx.  Workgroup 0 writes idx, w, offsets, perm,
+// inv, active and n_active (and adds the usage counts).  Returns
+// HN_NOT_HANDLED when the shape is not covered.
+extern "C" int hn_stream_route_sel_gate_up_impl(const void* hx, long ld_hx,
+                                                const float* logits_in, const float* bias, long T,
+                                                long E, long k, int mode, float eps,
+                                                float scaling, const void* table, long H, long I,
+                                                long group, int* idx, void* w, int* offsets,
+                                                int* perm, int* inv, int* active, int* n_active,
+                                                long long* usage, void* h_ws, void* stream,
+                                                int dry_run) {
+  if (T < 1 || E < 1 || E > kMaxActive || k < 1 || k > 16 || k > E || mode < 0 || mode > 2 ||
+      H % 512 != 0 || group != 128 || I % 128 != 0 || ld_hx % 8 != 0 || ld_hx >= (1L << 31))
+    return HN_NOT_HANDLED;
+  const long n = T * k;
+  const long G = H / 128;
+  int lpw = 2;
+  while (lpw < 16 && (G + lpw - 1) / lpw > kMaxWaves) lpw *= 2;
+  const long kw = (G + lpw - 1) / lpw;
+  if (n > kw * 64) return HN_NOT_HANDLED;  // one thread per routed row in the ranks
+  const long scratch = T * E * 4 + n * 4 + ((n + 1) & ~1L) * 2 + kw * E * 4 + 16;
+  const StreamPlan p = stream_plan(H, 2, T, E, true, false, true, n, scratch);
+  if (!p.ok || p.lpw > 8 || p.th != 1 || !wide_scales_ok(p, H, H / group)) return HN_NOT_HANDLED;
+  if (I * (H / 2) >= (long)kOOB || I * (H / group) * 2 >= (long)kOOB) return HN_NOT_HANDLED;
+  if (dry_run) return 0;
+  StreamPlan pw = p;
+  pw.wide = true;
+  StreamArgs A = {};
+  A.x = (const h16*)hx;  // unused: rows come from hx through the permutation
+  A.phase = 0;
+  A.E = (int)E;
+  A.ld_q = (int)(H / 2);
+  A.ld_s = (int)(H / group);
+  A.out = (h16*)h_ws;
+  A.ld_o = (int)I;
+  fill_common(A, p, I, H);
+  A.hx = (const h16*)hx;
+  A.ld_hx = (int)ld_hx;
+  A.logits_in = logits_in;
+  A.bias = bias;
+  A.mode = mode;
+  A.T = (int)T;
+  A.topk = (int)k;
+  A.eps = eps;
+  A.scaling = scaling;
+  A.idx_out = idx;
+  A.w_out = (h16*)w;
+  A.offsets_out = offsets;
+  A.perm_out = perm;
+  A.inv_out = inv;
+  A.active_out = active;
+  A.n_active_out = n_active;
+  A.usage = usage;
+  const GroupedPtrs g = {(const SExpert*)table, nullptr, nullptr, nullptr};
+  hipStream_t s = (hipStream_t)stream;
+  int rc = HN_NOT_HANDLED;
+  if (p.lpw == 2) rc = launch_one<true, 2, 1, 2, 3, true, 1, 2>(A, g, pw, s);
+  else if (p.lpw == 4) rc = launch_one<true, 2, 1, 4, 3, true, 1, 2>(A, g, pw, s);
+  else if (p.lpw == 8) rc = launch_one<true, 2, 1, 8, 2, true, 1, 2>(A, g, pw, s);
+  if (rc) return rc;
+  HN_LAUNCH_CHECK("hn_stream_route_sel_gate_up");
   return 0;
 }

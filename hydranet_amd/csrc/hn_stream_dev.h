@@ -49,6 +49,8 @@ struct StreamArgs {
   const h16* gate; int ld_gate;
   const float* logits_in;
   int T, topk;
+  int mode;            // ROUTE 2: top-k mode (0 softmax, 1 sigmoid, 2 sigmoid unnormalised)
+  const float* bias;   // ROUTE 2: optional selection bias [E]
   float eps, scaling;
   float* logits_out;
   int* idx_out; h16* w_out;

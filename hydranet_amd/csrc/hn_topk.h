@@ -69,130 +69,106 @@ __device__ __forceinline__ uint32_t order_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Unsigned max over the 64 lanes of a wave (every lane gets it): row_shr
+// steps to lane 15 of each row of 16, row_bcast:15 and row_bcast:31 across
+// the rows, then lane 63 read back (a zero fill is the identity of the max).
+template <int CTL>
+__device__ __forceinline__ uint32_t dpp_shr_zero(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTL, 0xf, 0xf, true);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_shr_zero<0x111>(v));  // row_shr:1
+  v = max(v, dpp_shr_zero<0x112>(v));  // row_shr:2
+  v = max(v, dpp_shr_zero<0x114>(v));  // row_shr:4
+  v = max(v, dpp_shr_zero<0x118>(v));  // row_shr:8
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Top-k of one token's logits row by one wave: lanes hold experts lane +
-// 64 j (E <= 256).  The k-th largest candidate key is found by bisection over
-// its 32 bits (one ballot per bit and candidate register: no lane exchanges),
-// ties at that key go to the lower experts.  The selected candidates (at most
-// k <= 16) are then moved to lanes 0..k-1 in expert order (ds_permute to
-// their rank among the selected), each finds its place in the (value desc,
-// expert asc) order against the others (readlane over the k lanes), and a
-// second ds_permute puts them in selection order, so the weight sums read
-// lane p for the p-th selected.  Same selection and weight arithmetic as
-// topk_small / topk_weights: the sums over the selected experts run in
-// selection order.
+// 64 j (E <= 256).  k rounds of a wave-wide maximum over the candidates'
+// order keys (DPP), the winner being the lowest expert among equal keys
+// (ballots, lowest register then lowest lane); the winner's key is cleared
+// for the next round.  Rounds pick in selection order (value desc, expert
+// asc), so the weights sum the selected in that order: the same selection
+// and weight arithmetic as topk_small / topk_weights.
 __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int E, int k,
                                           int mode, float eps, float scaling, int lane,
                                           int* idx_o, h16* w_o) {
   constexpr int NJ = 4;
-  const uint64_t lt = (1ull << lane) - 1;
   uint32_t key[NJ];
-  float raw[NJ];  // sigmoid (mode 1) or logit (mode 0) of the candidate
-  bool ok[NJ];
+  float raw[NJ];  // sigmoid (mode >= 1) or logit (mode 0) of the candidate
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int e = lane + 64 * j;
-    ok[j] = e < E;
-    const float lv = ok[j] ? l[e] : 0.f;
+    const bool ok = e < E;
+    const float lv = ok ? l[e] : 0.f;
     float v = lv;
-    if (mode >= 1 && ok[j]) {
+    if (mode >= 1 && ok) {
       v = sigmoid_f32(lv);
       raw[j] = v;
       if (bias) v = v + bias[e];
     } else {
       raw[j] = lv;
     }
-    key[j] = ok[j] ? order_key(v) : 0u;
+    // every real key is above 0 (the key of -inf is 0x007fffff): absent
+    // candidates (key 0) are never picked while k <= E
+    key[j] = ok ? order_key(v) : 0u;
   }
-  // Largest t with at least k candidates of key >= t.  Every real key is
-  // above 0 (the key of -inf is 0x007fffff) and the thresholds tried are >= 1,
-  // so the zero keys of absent candidates never count: no per-register
-  // conditions, no branches in the 32 steps.
-  uint32_t t = 0;
+  int my_e = -1;       // lane r < k: the r-th selected expert
+  float my_raw = 0.f;  // and its raw value
+  for (int r = 0; r < k; ++r) {  // uniform
+    uint32_t m = key[0];
 #pragma unroll
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t c = t | (1u << bit);
-    int cnt = 0;
+    for (int j = 1; j < NJ; ++j) m = max(m, key[j]);
+    const uint32_t best = wave_max_u32(m);
+    int we = 0x7fffffff;
+    float wr = 0.f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) cnt += __popcll(__ballot(key[j] >= c));
-    t = cnt >= k ? c : t;
-  }
-  bool sel[NJ];
-  int above = 0;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) above += __popcll(__ballot(key[j] > t));
-  int tie = 0;  // ties at t in expert order until k are selected
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const bool eq = key[j] == t;
-    const uint64_t m = __ballot(eq);
-    sel[j] = key[j] > t || (eq && above + tie + __popcll(m & lt) < k);
-    tie += __popcll(m);
-  }
-  // 1. the selected to lanes 0..ns-1 in expert order: the candidate of rank
-  //    r among the selected sends (key, expert, raw) to lane r; the others
-  //    send to lane 63 (>= 16 > ns), whose values are never read
-  int ns = 0;
-  uint32_t ck = 0u;
-  int ce = 0;
-  float cr = 0.f;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const uint64_t m = __ballot(sel[j]);
-    const int cnt = __popcll(m);
-    if (cnt) {  // uniform
-      const int dst = 4 * (sel[j] ? ns + __popcll(m & lt) : 63);
-      const uint32_t pk = (uint32_t)__builtin_amdgcn_ds_permute(dst, (int)key[j]);
-      const int pe = __builtin_amdgcn_ds_permute(dst, lane + 64 * j);
-      const float pr =
-          __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(dst, __builtin_bit_cast(int, raw[j])));
-      if (lane >= ns && lane < ns + cnt) {
-        ck = pk;
-        ce = pe;
-        cr = pr;
+    for (int j = NJ - 1; j >= 0; --j) {  // the lowest register with a tie wins
+      const uint64_t b = __ballot(key[j] == best);
+      if (b) {  // uniform
+        const int wl = __builtin_ctzll(b);
+        we = wl + 64 * j;
+        wr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, raw[j]), wl));
       }
-      ns += cnt;
     }
-  }
-  // 2. place of lane r's candidate: selected candidates ahead of it (a larger
-  //    key, or an equal key and a lower expert = a lower lane)
-  int pos = 0;
 #pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    if (s < ns) {  // uniform
-      const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)ck, s);
-      pos += (ks > ck || (ks == ck && s < lane)) ? 1 : 0;
+    for (int j = 0; j < NJ; ++j)
+      if (lane + 64 * j == we) key[j] = 0u;
+    if (lane == r) {
+      my_e = we;
+      my_raw = wr;
     }
   }
-  // 3. lane p holds the p-th selected (expert, raw)
-  const int dst = 4 * (lane < ns ? pos : 63);
-  const int oe = __builtin_amdgcn_ds_permute(dst, ce);
-  const float orr = __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(dst, __builtin_bit_cast(int, cr)));
   auto at = [&](int r) -> float {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, orr), r));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_raw), r));
   };
   if (mode == 0) {
     // fp32 softmax over the selected logits, renormalised (topk_weights)
     const float mx = at(0);
     float z = 0.f;
-    for (int r = 0; r < ns; ++r) z += expf(at(r) - mx);
+    for (int r = 0; r < k; ++r) z += expf(at(r) - mx);
     float sum = 0.f;
-    for (int r = 0; r < ns; ++r) sum += expf(at(r) - mx) / z;
-    if (lane < ns) {
-      idx_o[lane] = oe;
-      w_o[lane] = (h16)((expf(orr - mx) / z) / sum);
+    for (int r = 0; r < k; ++r) sum += expf(at(r) - mx) / z;
+    if (lane < k) {
+      idx_o[lane] = my_e;
+      w_o[lane] = (h16)((expf(my_raw - mx) / z) / sum);
     }
   } else if (mode == 1) {
     float sum = 0.f;
-    for (int r = 0; r < ns; ++r) sum += at(r);
+    for (int r = 0; r < k; ++r) sum += at(r);
     const float d = sum + eps;
-    if (lane < ns) {
-      idx_o[lane] = oe;
-      w_o[lane] = (h16)f32_mul(orr / d, scaling);
+    if (lane < k) {
+      idx_o[lane] = my_e;
+      w_o[lane] = (h16)f32_mul(my_raw / d, scaling);
     }
   } else {
-    if (lane < ns) {
-      idx_o[lane] = oe;
-      w_o[lane] = (h16)f32_mul(orr, scaling);
+    if (lane < k) {
+      idx_o[lane] = my_e;
+      w_o[lane] = (h16)f32_mul(my_raw, scaling);
     }
   }
 }

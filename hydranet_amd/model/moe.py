@@ -22,6 +22,7 @@ is refreshed for that call.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Sequence
 
 import torch
@@ -126,6 +127,82 @@ def moe_route(hidden: torch.Tensor, k: int, mode: int, gate_w: Optional[torch.Te
               _lib.ptr(r.perm), _lib.ptr(r.inv), _lib.ptr(r.active), _lib.ptr(r.n_active),
               _lib.ptr(_usage_ptr(usage, E, dev)), _lib.ptr(r.x_perm), H, _lib.stream(dev))
     return r
+
+
+def route_experts_fits(T: int, E: int, k: int, mode: int, table: "ExpertTable") -> bool:
+    """Whether hn_moe_route_experts_decode (routing from given logits fused
+    into the gate/up kernel) covers this layer call."""
+    H, I, g = table.dims
+    if table.num_experts != E:
+        return False
+    return _lib.lib().hn_moe_route_experts_decode_check(T, E, k, mode, H, I, g) == 0
+
+
+def moe_route_experts_decode(hidden: torch.Tensor, logits: torch.Tensor, k: int, mode: int,
+                             table: "ExpertTable", bias: Optional[torch.Tensor] = None,
+                             eps: float = 1e-9, scaling: float = 1.0,
+                             shared: Optional[torch.Tensor] = None, shared_ready=None,
+                             usage: Optional[torch.Tensor] = None):
+    """A decode MoE layer from given logits [T, E] in three launches
+    (hn_moe_route_experts_decode): top-k and permutation inside the gate/up
+    kernel, down projection, ordered unpermute (+ the fp16 shared addend once
+    ``shared_ready``, a torch.cuda.Event recorded after it on another stream,
+    has fired).  Returns (out [T, H] fp16, Routed without x_perm)."""
+    T, H = hidden.shape
+    _lib.require_gpu(hidden, logits)
+    dev = hidden.device
+    E = logits.shape[1]
+    Ht, I, g = table.dims
+    assert Ht == H, f"hidden {H} != expert hidden {Ht}"
+    x = _lib.aligned_rows(hidden.to(torch.float16))
+    r = Routed(T, k, E, 0, dev)
+    r.logits = logits.to(torch.float32).contiguous()
+    b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
+    n = T * k
+    h_ws = torch.empty((n, I), dtype=torch.float16, device=dev)
+    y_ws = torch.empty((n, H), dtype=torch.float16, device=dev)
+    sh = None if shared is None else _lib.aligned_rows(shared.reshape(T, H).to(torch.float16))
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    work = _lib.skinny_workspace(3, n, H, I, E, dev)
+    ev = None if shared_ready is None else ctypes.c_void_p(shared_ready.cuda_event)
+    _lib.call("hn_moe_route_experts_decode", _lib.ptr(r.logits), _lib.ptr(b), T, E, k, mode, eps,
+              scaling, _lib.ptr(x), x.stride(0), _lib.ptr(table.dev), H, I, g, _lib.ptr(r.idx),
+              _lib.ptr(r.w), _lib.ptr(r.offsets), _lib.ptr(r.perm), _lib.ptr(r.inv),
+              _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(_usage_ptr(usage, E, dev)),
+              _lib.ptr(h_ws), _lib.ptr(y_ws), ev, _lib.ptr(sh),
+              H if sh is None else sh.stride(0), _lib.ptr(out), H, _lib.ptr(work), work.numel(),
+              _lib.stream(dev))
+    return out, r
+
+
+def moe_dispatch_joined(r: Routed, table: ExpertTable, shared: torch.Tensor,
+                        shared_ready) -> torch.Tensor:
+    """moe_dispatch with the fp16 shared addend produced on another stream:
+    the expert kernels are queued first and the stream waits for
+    ``shared_ready`` (a torch.cuda.Event recorded after the addend) only
+    before the unpermute.  Down projections that run as K slices keep the
+    one-call path (joined before it)."""
+    T, k, E = r.T, r.k, r.E
+    H = r.x_perm.shape[1]
+    Ht, I, g = table.dims
+    dev = r.x_perm.device
+    n = T * k
+    if T > _lib.DECODE_MAX_ROWS or I % 512 == 0:
+        torch.cuda.current_stream(dev).wait_event(shared_ready)
+        return moe_dispatch(r, table, shared=shared)
+    st = _lib.stream(dev)
+    h_ws = torch.empty((max(n, 1), I), dtype=torch.float16, device=dev)
+    y_perm = torch.empty((max(n, 1), H), dtype=torch.float16, device=dev)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    work = _lib.skinny_workspace(3, n, H, I, E, dev)
+    _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(r.x_perm), _lib.ptr(table.dev),
+              _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I, g,
+              _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(work), work.numel(), st)
+    torch.cuda.current_stream(dev).wait_event(shared_ready)
+    sh = _lib.aligned_rows(shared.reshape(T, H).to(torch.float16))  # after the wait
+    _lib.call("hn_moe_unpermute", _lib.ptr(y_perm), H, _lib.ptr(r.inv), _lib.ptr(r.idx),
+              _lib.ptr(r.w), T, k, _lib.ptr(sh), sh.stride(0), _lib.ptr(out), H, H, st)
+    return out
 
 
 def _usage_ptr(usage: Optional[torch.Tensor], E: int, dev) -> Optional[torch.Tensor]:
@@ -486,6 +563,9 @@ class GLM4MoELayer(nn.Module):
         self.experts = _ResidentExperts(num_experts, layer_idx, slots, cache_manager)
         self._last_idx: Optional[torch.Tensor] = None
         self.last_routing = None  # (idx [T, k] i32, w [T, k] fp16) of the last forward
+        # decode routing inside the gate/up kernel (hn_moe_route_experts_decode)
+        # instead of the separate routing launch
+        self.fused_routing = False
 
     def get_last_selected_experts(self) -> list:
         """Experts the last forward routed to, ascending (the reference records
@@ -514,24 +594,52 @@ class GLM4MoELayer(nn.Module):
         T = B * S
         flat = hidden_states.reshape(T, H)
         rt = self.router
-        if route_fits(T, rt.num_experts, rt.top_k):
-            # the shared expert (fp16 GEMMs) runs on a side stream while the
-            # router and the routing kernels run; joined before the experts
+        mode = 1 if rt.norm_topk_prob else 2
+        table = self.experts.static_table(flat.device)
+        if self.fused_routing and table is not None and \
+                route_experts_fits(T, rt.num_experts, rt.top_k, mode, table):
+            # the shared expert (fp16 GEMMs) on a side stream, joined only
+            # before the unpermute; the routing runs inside the gate/up kernel
             cur = torch.cuda.current_stream(flat.device)
             side = _side_stream(flat.device)
             side.wait_stream(cur)
             with torch.cuda.stream(side):
                 shared = self.shared_expert(hidden_states)
+                ready = torch.cuda.Event()
+                ready.record(side)
+            logits = router_logits(flat, rt.weight.float() if rt.weight.dtype != torch.float32
+                                   else rt.weight)
+            if rt.n_group > 1 and rt.topk_group > 0:
+                logits = group_limit(logits, rt.n_group, rt.topk_group)
+            out, r = moe_route_experts_decode(flat, logits, rt.top_k, mode, table,
+                                              bias=rt.selection_bias,
+                                              scaling=rt.routed_scaling_factor,
+                                              shared=shared.reshape(T, H), shared_ready=ready)
+            shared.record_stream(cur)
+            self._last_idx = r.idx
+            self.last_routing = (r.idx, r.w)
+            return out.view(B, S, H)
+        if route_fits(T, rt.num_experts, rt.top_k):
+            # the shared expert (fp16 GEMMs) runs on a side stream while the
+            # router, the routing and the expert kernels run; joined before
+            # the unpermute
+            cur = torch.cuda.current_stream(flat.device)
+            side = _side_stream(flat.device)
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                shared = self.shared_expert(hidden_states)
+                ready = torch.cuda.Event()
+                ready.record(side)
             # fp32 logits by the multi-workgroup kernel, the rest in one launch
             logits = router_logits(flat, rt.weight.float() if rt.weight.dtype != torch.float32
                                    else rt.weight)
             if rt.n_group > 1 and rt.topk_group > 0:
                 logits = group_limit(logits, rt.n_group, rt.topk_group)
-            r = moe_route(flat, rt.top_k, 1 if rt.norm_topk_prob else 2, logits=logits,
+            r = moe_route(flat, rt.top_k, mode, logits=logits,
                           bias=rt.selection_bias, scaling=rt.routed_scaling_factor)
-            cur.wait_stream(side)
             shared.record_stream(cur)
-            out = moe_dispatch(r, self.experts.table_for(r.idx), shared=shared.reshape(T, H))
+            out = moe_dispatch_joined(r, self.experts.table_for(r.idx), shared.reshape(T, H),
+                                      ready)
             self._last_idx = r.idx
             self.last_routing = (r.idx, r.w)
             return out.view(B, S, H)

@@ -228,6 +228,34 @@ int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
                         int* n_active, long long* usage, void* h_ws, void* out, long ld_o,
                         void* work, long work_bytes, void* stream);
 
+/* 0 when hn_moe_route_experts_decode covers (T, E, k, mode, H, I, group) with
+ * the current decode kernel family, else a nonzero code (no message set). */
+int hn_moe_route_experts_decode_check(long T, long E, long k, int mode, long H, long I,
+                                      long group);
+
+/* A decode MoE layer from given router logits [T, E] fp32 (e.g. hn_router_logits,
+ * after hn_router_group_limit) in three launches: the top-k (mode 0 softmax,
+ * 1 sigmoid / (sum + eps) * scaling, 2 sigmoid * scaling; optional selection
+ * bias [E]) and the stable permutation computed inside the grouped gate/up
+ * streaming kernel, whose rows are staged from h [T, H] directly (no x_perm);
+ * the down projection (into y_ws [T k, H], or four fp32 K slices in work when
+ * I splits); the ordered weighted unpermute into out [T, H], plus the fp16
+ * shared addend [T, H] when given (GLM's shared expert).  shared_ready: a
+ * hipEvent_t (may be NULL) the stream waits for just before the unpermute,
+ * so a shared expert computed on another stream overlaps the expert kernels.
+ * E <= 256, k <= 16, T k <= 64 x the gate/up launch's waves (512 at H = 4096),
+ * H % 512 == 0, group 128.  Routing outputs as hn_moe_route writes them
+ * (usage may be NULL); h_ws [T k, I]; work: hn_skinny_workspace_bytes(3, T k,
+ * H, I, E).  Replaces GLM4MoELayer.forward's router call, per-expert loop and
+ * shared + routed sum (model/glm4.py:275-309, 421-473) at decode sizes. */
+int hn_moe_route_experts_decode(const float* logits, const void* bias, long T, long E, long k,
+                                int mode, float eps, float scaling, const void* h, long ld_h,
+                                const void* table, long H, long I, long group, int* idx, void* w,
+                                int* offsets, int* perm, int* inv, int* active, int* n_active,
+                                long long* usage, void* h_ws, void* y_ws, void* shared_ready,
+                                const void* shared, long ld_sh, void* out, long ld_o, void* work,
+                                long work_bytes, void* stream);
+
 /* One phase of hn_moe_experts_decode's streaming path on its own (<= 16 rows per
  * expert, group 128): phase 0 reads x [rows, H] (sorted by expert) and writes
  * h_ws [rows, I]; phase 1 reads h_ws-shaped x [rows, I] and writes the four

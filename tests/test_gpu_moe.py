@@ -323,14 +323,16 @@ def test_grouped_matches_single_expert_path(mixtral_experts):
     _close(out, ref)
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("T", [32, 4])
-def test_glm_moe_layer_c3(T, decode_path):
+def test_glm_moe_layer_c3(T, decode_path, fused):
     """Config C3: 128 GLM experts (4096->1408), fp16 shared expert, sigmoid top-8
     with a seeded selection bias, T = 32 (and T = 4 decode)."""
     from hydranet_amd.model.moe import GLM4MoELayer
     from hydranet_amd.preprocess.synthetic import slot_to_cpu
     slots = _slots(128, 4096, 1408, seed0=1000)
     layer = GLM4MoELayer(4096, 1408, 128, 8, slots=slots).to(DEV).half()
+    layer.fused_routing = fused
     g = torch.Generator().manual_seed(8)
     layer.router.weight.data = (torch.randn(128, 4096, generator=g) * 0.02).float().to(DEV)
     bias = (torch.rand(128, generator=g) * 0.2 - 0.1).float()
@@ -668,6 +670,59 @@ def test_decode_layer_with_given_logits_matches_route_then_experts(T, k, mixtral
     # idx against a brute-force top-k of the logits (ties -> lower expert)
     keys = lg.double() - torch.arange(8, device=DEV).double() * 1e-9
     assert torch.equal(r1.idx.long(), keys.topk(k, dim=-1).indices)
+
+
+@pytest.fixture(scope="module")
+def glm_experts():
+    return _slots(128, 4096, 1408, seed0=3000)
+
+
+@pytest.mark.parametrize("T,k,mode,bias,shared", [(32, 8, 1, True, True), (4, 8, 1, False, True),
+                                                   (32, 8, 2, True, False), (1, 8, 1, True, True),
+                                                   (64, 8, 0, False, False)])
+def test_route_experts_decode_matches_route_then_experts(T, k, mode, bias, shared, glm_experts):
+    """hn_moe_route_experts_decode (top-k and permutation inside the GLM-shaped
+    gate/up kernel, rows staged from h through the permutation) vs
+    hn_moe_route with the same logits followed by hn_moe_experts_decode:
+    routing outputs and the layer output bit for bit, the shared addend
+    joined through an event recorded on a side stream."""
+    from hydranet_amd.model.moe import (ExpertTable, moe_dispatch, moe_route,
+                                        moe_route_experts_decode, route_experts_fits)
+    table = ExpertTable.from_slots(glm_experts)
+    E = 128
+    assert route_experts_fits(T, E, k, mode, table)
+    g = torch.Generator().manual_seed(300 + T + mode)
+    x = torch.randn(T, 4096, generator=g).half().to(DEV)
+    lg = (torch.randn(T, E, generator=g) * 2).float()
+    lg[::3, 7] = lg[::3, 9]  # exact ties
+    lg = lg.to(DEV)
+    b = (torch.rand(E, generator=g) * 0.2 - 0.1).to(DEV) if bias else None
+    sh = torch.randn(T, 4096, generator=g).half().to(DEV) if shared else None
+    print(f"[case] route+experts decode T={T} k={k} mode={mode} bias={bias}", flush=True)
+    r0 = moe_route(x, k, mode, logits=lg, bias=b, scaling=1.5)
+    ref = moe_dispatch(r0, table, shared=sh)
+    ready = None
+    if shared:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            sh2 = sh * 1.0  # the addend produced on the side stream
+            ready = torch.cuda.Event()
+            ready.record(side)
+    else:
+        sh2 = None
+    out, r1 = moe_route_experts_decode(x, lg, k, mode, table, bias=b, scaling=1.5, shared=sh2,
+                                       shared_ready=ready)
+    torch.cuda.synchronize()
+    assert torch.equal(r1.idx, r0.idx)
+    assert torch.equal(r1.w, r0.w)
+    na = int(r0.n_active.item())
+    assert int(r1.n_active.item()) == na
+    assert torch.equal(r1.offsets, r0.offsets)
+    assert torch.equal(r1.active[:na], r0.active[:na])
+    assert torch.equal(r1.perm, r0.perm)
+    assert torch.equal(r1.inv, r0.inv)
+    assert torch.equal(out, ref)
 
 
 @pytest.mark.parametrize("T,k,given", [(4, 2, False), (16, 2, False), (20, 2, False),
