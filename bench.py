@@ -341,6 +341,8 @@ def bench_c3(args, T: int = 32, n_layers: int = 2):
         layer = GLM4MoELayer(H, I, E, k, layer_idx=L, slots=slots).cuda().half()
         if args.fused_routing is not None:
             layer.fused_routing = bool(args.fused_routing)
+        if args.shared_side_stream is not None:
+            layer.shared_side_stream = bool(args.shared_side_stream)
         gen = torch.Generator(device="cuda").manual_seed(9000 + L)
         layer.router.weight.data = (torch.randn(E, H, generator=gen, device="cuda") * 0.02).float()
         layer.router.selection_bias = torch.rand(E, generator=gen, device="cuda") * 0.2 - 0.1
@@ -893,6 +895,9 @@ def main():
                          "h2d: the expert-miss load path (pinned -> HBM, and from a store "
                          "on disk)")
     ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--shared-side-stream", type=int, default=None, choices=[0, 1],
+                    help="c3: the shared expert on a second stream (1) or first on the "
+                         "layer's stream (0); default: the layer's")
     ap.add_argument("--fused-routing", type=int, default=None, choices=[0, 1],
                     help="c3: routing inside the gate/up kernel (1) or its own launch (0); "
                          "default: the layer's")

@@ -134,7 +134,8 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   }
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;
-  topk_wave(logits + (long)t * E, bias, E, k, mode, eps, scaling, threadIdx.x & 63,
+  const TopkBias tb = topk_wave_bias(bias, E, threadIdx.x & 63);
+  topk_wave(logits + (long)t * E, tb, E, k, mode, eps, scaling, threadIdx.x & 63,
             idx_out + (long)t * k, w_out + (long)t * k);
 }
 
@@ -243,16 +244,17 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
   int ex[kMaxTopK];
   float wt[kMaxTopK];
   // the token's k (position, expert, weight) loaded together (one memory
-  // round trip, not one per assignment), then ordered by expert
+  // round trip, not one per assignment), then ordered by expert.  The loads
+  // are unconditional (index clamped to k - 1): a load under `if (s < k)`
+  // ends its own block, and the compiler then waits for each in turn.
   int pv[kMaxTopK], ev[kMaxTopK];
   h16 wv[kMaxTopK];
 #pragma unroll
   for (int s = 0; s < kMaxTopK; ++s) {
-    if (s < k) {
-      pv[s] = inv[t * k + s];
-      ev[s] = idx[t * k + s];
-      wv[s] = w[t * k + s];
-    }
+    const int j = t * k + (s < k ? s : k - 1);
+    pv[s] = inv[j];
+    ev[s] = idx[j];
+    wv[s] = w[j];
   }
   int n = 0;
 #pragma unroll
@@ -281,6 +283,9 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
   for (int c = (blockIdx.y * blockDim.x + threadIdx.x) * 8; c < H;
        c += gridDim.y * blockDim.x * 8) {
     half8_t acc = {0, 0, 0, 0, 0, 0, 0, 0};
+    // the shared expert's row is loaded with the first batch of rows
+    half8_t sv = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (shared) sv = *reinterpret_cast<const half8_t*>(shared + (long)t * ld_sh + c);
     for (int s0 = 0; s0 < n; s0 += B) {
       half8_t v[B];
 #pragma unroll
@@ -319,7 +324,6 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
       }
     }
     if (shared) {
-      const half8_t sv = *reinterpret_cast<const half8_t*>(shared + (long)t * ld_sh + c);
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = (h16)((float)sv[j] + (float)acc[j]);
     }
@@ -364,6 +368,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
   const int nw = blockDim.x >> 6;
   const bool lead = blockIdx.x == 0;
   const int n = T * k;
+  // the selection bias (E > 16: one wave per token) goes out with the logits
+  const TopkBias tb = topk_wave_bias(E > 16 ? bias : nullptr, E, lane);
 
   for (int i = tid; i < kRouteWaves * kMaxExperts; i += blockDim.x) (&s_wcnt[0][0])[i] = 0;
 
@@ -448,7 +454,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
       topk_small<16>(lg + t * E, bias, E, k, mode, eps, scaling, s_sel + t * k, s_w + t * k);
   } else {
     for (int t = wave; t < T; t += nw)
-      topk_wave(lg + t * E, bias, E, k, mode, eps, scaling, lane, s_sel + t * k, s_w + t * k);
+      topk_wave(lg + t * E, tb, E, k, mode, eps, scaling, lane, s_sel + t * k, s_w + t * k);
   }
   __syncthreads();
   if (lead)

@@ -209,12 +209,14 @@ __device__ int route_prologue_sel(const StreamArgs& A, unsigned char* scratch, i
   h16* s_w = reinterpret_cast<h16*>(s_sel + n);             // [n]
   int* s_wcnt = reinterpret_cast<int*>(s_w + ((n + 1) & ~1));  // [KW][E]
   int* s_na = s_wcnt + KW * E;
+  // the selection bias goes out with the logits (once per wave)
+  const TopkBias tb = topk_wave_bias(A.bias, E, lane);
   for (int i = tid; i < KW * E; i += blockDim.x) s_wcnt[i] = 0;
   copy_to_lds_f32(A.logits_in, s_lg, T * E);
   __syncthreads();
   // 1. top-k, one wave per token
   for (int t = wave; t < T; t += KW)
-    topk_wave(s_lg + t * E, A.bias, E, k, A.mode, A.eps, A.scaling, lane, s_sel + t * k,
+    topk_wave(s_lg + t * E, tb, E, k, A.mode, A.eps, A.scaling, lane, s_sel + t * k,
               s_w + t * k);
   __syncthreads();
   // 2. rank among equal experts within the wave (one thread per assignment)

@@ -94,7 +94,27 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // for the next round.  Rounds pick in selection order (value desc, expert
 // asc), so the weights sum the selected in that order: the same selection
 // and weight arithmetic as topk_small / topk_weights.
-__device__ __forceinline__ void topk_wave(const float* l, const float* bias, int E, int k,
+// The selection bias of the lane's four candidates (experts lane + 64 j),
+// loaded once per wave and reused for every token: unconditional loads
+// (index clamped to E - 1) that go out together.  Zero without a bias.
+struct TopkBias {
+  float v[4];
+  bool on;
+};
+__device__ __forceinline__ TopkBias topk_wave_bias(const float* bias, int E, int lane) {
+  TopkBias b;
+  b.on = bias != nullptr;
+  const float* src = b.on ? bias : nullptr;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b.v[j] = 0.f;
+  if (b.on) {  // uniform
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b.v[j] = src[min(lane + 64 * j, E - 1)];
+  }
+  return b;
+}
+
+__device__ __forceinline__ void topk_wave(const float* l, const TopkBias& bias, int E, int k,
                                           int mode, float eps, float scaling, int lane,
                                           int* idx_o, h16* w_o) {
   constexpr int NJ = 4;
@@ -109,7 +129,7 @@ __device__ __forceinline__ void topk_wave(const float* l, const float* bias, int
     if (mode >= 1 && ok) {
       v = sigmoid_f32(lv);
       raw[j] = v;
-      if (bias) v = v + bias[e];
+      if (bias.on) v = v + bias.v[j];
     } else {
       raw[j] = lv;
     }

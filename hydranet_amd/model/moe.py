@@ -566,6 +566,11 @@ class GLM4MoELayer(nn.Module):
         # decode routing inside the gate/up kernel (hn_moe_route_experts_decode)
         # instead of the separate routing launch
         self.fused_routing = False
+        # the shared expert on a second stream, overlapping the routing and
+        # expert kernels (joined before the unpermute); False runs it first on
+        # the layer's stream (measured at 32 tokens: 222.4 us per layer with
+        # the side stream, 226-228 us without)
+        self.shared_side_stream = True
 
     def get_last_selected_experts(self) -> list:
         """Experts the last forward routed to, ascending (the reference records
@@ -616,6 +621,19 @@ class GLM4MoELayer(nn.Module):
                                               scaling=rt.routed_scaling_factor,
                                               shared=shared.reshape(T, H), shared_ready=ready)
             shared.record_stream(cur)
+            self._last_idx = r.idx
+            self.last_routing = (r.idx, r.w)
+            return out.view(B, S, H)
+        if route_fits(T, rt.num_experts, rt.top_k) and not self.shared_side_stream:
+            # the shared expert first, on the same stream
+            shared = self.shared_expert(hidden_states)
+            logits = router_logits(flat, rt.weight.float() if rt.weight.dtype != torch.float32
+                                   else rt.weight)
+            if rt.n_group > 1 and rt.topk_group > 0:
+                logits = group_limit(logits, rt.n_group, rt.topk_group)
+            r = moe_route(flat, rt.top_k, mode, logits=logits,
+                          bias=rt.selection_bias, scaling=rt.routed_scaling_factor)
+            out = moe_dispatch(r, self.experts.table_for(r.idx), shared=shared.reshape(T, H))
             self._last_idx = r.idx
             self.last_routing = (r.idx, r.w)
             return out.view(B, S, H)
