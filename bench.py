@@ -803,6 +803,9 @@ def bench_c5(args):
     cfg = MixtralDecoderConfig(max_position_embeddings=P + N)
     t0 = time.perf_counter()
     model = build_synthetic_decoder(cfg, "cuda", decode_top_k=1, seed=5)
+    if args.attn_decode is not None:
+        for layer in model.layers:
+            layer.self_attn.decode_kernel = bool(args.attn_decode)
     torch.cuda.synchronize()
     _log("c5 built in", round(time.perf_counter() - t0, 1), "s")
     H, I, L = cfg.hidden_dim, cfg.intermediate_dim, cfg.num_layers
@@ -898,6 +901,9 @@ def main():
     ap.add_argument("--shared-side-stream", type=int, default=None, choices=[0, 1],
                     help="c3: the shared expert on a second stream (1) or first on the "
                          "layer's stream (0); default: the layer's")
+    ap.add_argument("--attn-decode", type=int, default=None, choices=[0, 1],
+                    help="c5: decode attention in one launch (1, hn_attn_decode) or the two "
+                         "products with the softmax between (0); default: the model's")
     ap.add_argument("--fused-routing", type=int, default=None, choices=[0, 1],
                     help="c3: routing inside the gate/up kernel (1) or its own launch (0); "
                          "default: the layer's")

@@ -223,6 +223,280 @@ __global__ void rope_append_kernel(const h16* __restrict__ q, long ld_q, const h
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+
+// ---------------------------------------------------------------------------
+// Decode attention: one query token per sequence, grouped-query heads.
+// One workgroup of 16 waves per (sequence b, KV head g) reads that head's
+// keys and values once and computes, for the REP query heads of the group,
+// the reference's formulation (model/mixtral.py:193-207):
+//   s16 = fp16(sum_d q[r][d] k[d][l])            (fp16 product, fp32 sums)
+//   a = fp16(s16 * inv_scale); a = fp16(a + mask[l]) with a mask row
+//   p = fp16(softmax_fp32(a))                    (F.softmax(dtype=float32))
+//   o[r][d] = fp16(sum_l p[r][l] v[l][d])        (fp16 product, fp32 sums)
+// Keys are stored transposed, kt[b][g][d][max_len]; values v[b][g][l][d].
+//  * scores: thread (position group pg = tid / 8, d slice ds = tid % 8)
+//    loads keys d = 16 ds .. 16 ds + 15 at positions 8 pg .. 8 pg + 7 (16
+//    loads of 16 bytes, all in flight: the head's whole K in one round
+//    trip) and accumulates the REP x 8 partial sums in fp32; a three-step
+//    reduce-scatter over the 8 lanes of a group (DPP) leaves lane ds the
+//    sums of position 8 pg + ds;
+//  * the values' loads go out next (thread: 8 d columns dg, positions
+//    ls + 64 i), before the softmax, whose reductions hide their latency;
+//  * softmax per row over LDS (row max, then exp sums: per lane in index
+//    order, then the wave's butterfly, then the waves in order);
+//  * values: per-thread fp32 sums over its positions, a reduce-scatter over
+//    the wave's 4 position slices, then the 16 waves added in order.
+// The fp32 sums run in another order than a library GEMM's, so outputs
+// agree with the two-product formulation within fp16 rounding.
+constexpr int kAttnHd = 128;
+constexpr int kAttnWaves = 16;
+
+template <int CTL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xf, 0xf, false));
+}
+// v from lane ^ 4 (within a row of 16 lanes)
+__device__ __forceinline__ float xor4_f32(float v, bool hi) {
+  const float up = dpp_f32<0x104>(v);  // row_shl:4: lane + 4
+  const float dn = dpp_f32<0x114>(v);  // row_shr:4: lane - 4
+  return hi ? dn : up;
+}
+
+template <int REP, int LMAX>
+__global__ __launch_bounds__(1024) void attn_decode_kernel(
+    const h16* __restrict__ q, const h16* __restrict__ kt, const h16* __restrict__ vc,
+    long max_len, int nkv, int L, const h16* __restrict__ mask, float inv_scale,
+    h16* __restrict__ out, long ld_o) {
+  constexpr int HD = kAttnHd;
+  constexpr int NV = LMAX / 64;  // value positions per thread
+  __shared__ __align__(16) float s_q[HD][4];       // q[r][d] as [d][r]
+  // scaled scores, then probabilities; 1024 rows whatever LMAX, so every
+  // lane's position (8 pg + ds < 1024) has a row and the store after the
+  // DPP exchanges needs no branch
+  __shared__ __align__(16) float s_x[1024][4];
+  __shared__ float s_red[2][kAttnWaves];
+  __shared__ __align__(16) float s_o[kAttnWaves][REP][HD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bg = blockIdx.x;  // b * nkv + g
+  const int b = bg / nkv, g = bg - b * nkv;
+  const h16* qb = q + (long)bg * REP * HD;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(kt + (long)bg * HD * max_len), (short)0, (int)(HD * max_len * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(vc + (long)bg * max_len * HD), (short)0, (int)(max_len * HD * 2), 0x00020000);
+  constexpr uint32_t kOOB = 0x7ffffff0u;
+
+  // 1. keys: all 16 loads of the thread in flight (positions past the
+  //    groups of L read nothing)
+  const int pg = tid >> 3, ds = tid & 7;
+  const int npg = (L + 7) >> 3;
+  const uint32_t ko = pg < npg ? (uint32_t)(((16 * ds) * max_len + 8 * pg) * 2) : kOOB;
+  u32x4 kr[16];
+#pragma unroll
+  for (int dd = 0; dd < 16; ++dd)
+    kr[dd] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rk, ko == kOOB ? kOOB : ko + (uint32_t)(dd * max_len * 2),
+                                           0, 0));
+  // this lane's score position and its mask entry (loaded with the keys)
+  const int lpos = 8 * pg + ds;
+  const bool lon = lpos < L;
+  const float mv = mask ? (float)mask[lon ? lpos : L - 1] : 0.f;
+  if (tid < REP * HD) {
+    const int r = tid / HD, d = tid - r * HD;
+    s_q[d][r] = (float)qb[r * HD + d];
+  }
+  __syncthreads();
+
+  // 2. scores: fp32 sums over the thread's 16 d, then over the 8 d slices
+  float acc[REP][8];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[r][j] = 0.f;
+#pragma unroll
+  for (int dd = 0; dd < 16; ++dd) {
+    const float4_t qv = *reinterpret_cast<const float4_t*>(&s_q[16 * ds + dd][0]);
+    const half8_t kv = __builtin_bit_cast(half8_t, kr[dd]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float kf = (float)kv[j];
+#pragma unroll
+      for (int r = 0; r < REP; ++r) acc[r][j] = __builtin_fmaf(qv[r], kf, acc[r][j]);
+    }
+  }
+  // reduce-scatter over ds (lane bits 2, 1, 0): keep positions of bit 2 = h
+  // (4 of 8), then bit 1 (2 of 4), then bit 0 (1 of 2); each step adds the
+  // kept half of this lane and the partner's copy of the same positions
+  float r4[REP][4], r2[REP][2], r1[REP];
+  {
+    const bool h = (ds >> 2) & 1;
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float keep = h ? acc[r][4 + jj] : acc[r][jj];
+        const float send = h ? acc[r][jj] : acc[r][4 + jj];
+        r4[r][jj] = keep + xor4_f32(send, h);
+      }
+  }
+  {
+    const bool h = (ds >> 1) & 1;
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const float keep = h ? r4[r][2 + jj] : r4[r][jj];
+        const float send = h ? r4[r][jj] : r4[r][2 + jj];
+        r2[r][jj] = keep + dpp_f32<0x4E>(send);  // quad_perm [2,3,0,1]: lane ^ 2
+      }
+  }
+  {
+    const bool h = ds & 1;
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const float keep = h ? r2[r][1] : r2[r][0];
+      const float send = h ? r2[r][0] : r2[r][1];
+      r1[r] = keep + dpp_f32<0xB1>(send);  // quad_perm [1,0,3,2]: lane ^ 1
+    }
+  }
+  // lane ds holds position l = 8 pg + ds: scale and mask with the
+  // reference's fp16 roundings (straight-line code: the exchanged sums are
+  // not consumed under a lane-dependent branch)
+  {
+    const int l = lpos;
+    const bool on = lon;
+    float4_t xs;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float xv = -__builtin_inff();
+      if (r < REP) {
+        h16 a = (h16)((float)(h16)r1[r] * inv_scale);
+        a = (h16)((float)a + mv);  // + 0 without a mask: the same value
+        xv = on ? (float)a : -__builtin_inff();
+      }
+      xs[r] = xv;
+    }
+    *reinterpret_cast<float4_t*>(&s_x[l][0]) = xs;
+  }
+
+  // 3. values: thread (8 columns dg, positions ls + 64 i); loads out now
+  const int dg = tid & 15, ls = tid >> 4;
+  u32x4 vr[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int l = ls + 64 * i;
+    const uint32_t vo = l < L ? (uint32_t)((l * HD + 8 * dg) * 2) : kOOB;
+    vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, 0));
+  }
+  __syncthreads();
+
+  // 4. softmax of row r: wave w takes row w % REP, part w / REP of the
+  //    positions (lane + 64 i within the part)
+  {
+    constexpr int PARTS = kAttnWaves / REP;
+    constexpr int PER = LMAX / PARTS;  // positions per part
+    constexpr int IT = (PER + 63) / 64;
+    const int r = wave % REP, part = wave / REP;
+    float x[IT];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int l = part * PER + lane + 64 * i;
+      x[i] = (lane + 64 * i < PER && l < L) ? s_x[l][r] : -__builtin_inff();
+      mx = mx > x[i] ? mx : x[i];
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float o = __shfl_xor(mx, off, 64);
+      mx = mx < o ? o : mx;
+    }
+    if (lane == 0) s_red[0][wave] = mx;
+    __syncthreads();
+    mx = s_red[0][r];
+#pragma unroll
+    for (int p2 = 1; p2 < PARTS; ++p2) mx = mx < s_red[0][r + REP * p2] ? s_red[0][r + REP * p2] : mx;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      x[i] = expf(x[i] - mx);
+      sum += x[i];
+    }
+    for (int off = 32; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, 64);
+    if (lane == 0) s_red[1][wave] = sum;
+    __syncthreads();
+    sum = s_red[1][r];
+#pragma unroll
+    for (int p2 = 1; p2 < PARTS; ++p2) sum += s_red[1][r + REP * p2];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int l = part * PER + lane + 64 * i;
+      if (lane + 64 * i < PER) s_x[l][r] = l < L ? (float)(h16)(x[i] / sum) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // 5. values: o[r][8 dg + j] over the thread's positions
+  float oa[REP][8];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) oa[r][j] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int l = ls + 64 * i;
+    if (64 * i < L) {  // uniform enough: past L the loads returned zero
+      const float4_t pv = *reinterpret_cast<const float4_t*>(&s_x[l][0]);
+      const half8_t vv = __builtin_bit_cast(half8_t, vr[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float vf = (float)vv[j];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) oa[r][j] = __builtin_fmaf(pv[r], vf, oa[r][j]);
+      }
+    }
+  }
+  // reduce-scatter over the wave's 4 position slices (lane bits 5, 4):
+  // lane keeps columns 8 dg + 4 h5 + 2 h4 + {0, 1}
+  float o4[REP][4], o2[REP][2];
+  {
+    const bool h = (lane >> 5) & 1;
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float keep = h ? oa[r][4 + jj] : oa[r][jj];
+        const float send = h ? oa[r][jj] : oa[r][4 + jj];
+        o4[r][jj] = keep + __shfl_xor(send, 32, 64);
+      }
+  }
+  {
+    const bool h = (lane >> 4) & 1;
+#pragma unroll
+    for (int r = 0; r < REP; ++r)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const float keep = h ? o4[r][2 + jj] : o4[r][jj];
+        const float send = h ? o4[r][jj] : o4[r][2 + jj];
+        o2[r][jj] = keep + __shfl_xor(send, 16, 64);
+      }
+  }
+  {
+    const int c0 = 8 * dg + 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1);
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      s_o[wave][r][c0] = o2[r][0];
+      s_o[wave][r][c0 + 1] = o2[r][1];
+    }
+  }
+  __syncthreads();
+  if (tid < REP * HD) {
+    const int r = tid / HD, d = tid - r * HD;
+    float o = s_o[0][r][d];
+#pragma unroll
+    for (int w2 = 1; w2 < kAttnWaves; ++w2) o += s_o[w2][r][d];
+    out[(long)b * ld_o + (long)(g * REP + r) * HD + d] = (h16)o;
+  }
+}
 }  // namespace
 
 // out[t] = RMSNorm(x[t] (+ res[t])) * w, rows t < T of H fp16; with res, the
@@ -318,5 +592,40 @@ extern "C" int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k
                      (const h16*)k, ld_k, (const h16*)v, ld_v, cos_t, sin_t, pos, (int)S,
                      (int)nh, (int)nkv, (int)hd, (h16*)q_out, (h16*)kt, (h16*)vc, max_len);
   HN_LAUNCH_CHECK("hn_rope_append");
+  return 0;
+}
+
+// Decode attention over the KV cache (one query token per sequence).  See
+// include/hn_int4.h.
+extern "C" int hn_attn_decode(const void* q, const void* kt, const void* v, long max_len, long B,
+                              long nkv, long rep, long hd, long L, const void* mask,
+                              float inv_scale, void* out, long ld_o, void* stream) {
+  const char* who = "hn_attn_decode";
+  HN_ARG_CHECK(B >= 0 && nkv > 0 && (rep == 1 || rep == 2 || rep == 4) && hd == kAttnHd,
+               "%s: need head_dim %d and 1, 2 or 4 query heads per KV head (rep=%ld hd=%ld)",
+               who, kAttnHd, rep, hd);
+  HN_ARG_CHECK(L >= 1 && L <= 1024 && max_len >= (L + 7) / 8 * 8,
+               "%s: need 1 <= L <= 1024 and max_len >= L rounded up to 8 (L=%ld max_len=%ld)",
+               who, L, max_len);
+  HN_ARG_CHECK(hd * max_len * 2 < 0x7ffffff0L, "%s: one head's cache must stay below 2 GiB",
+               who);
+  HN_ARG_CHECK(al16(q) && al16(kt) && al16(v) && max_len % 8 == 0 && al16(out) && ld_o % 8 == 0 &&
+                   ld_o >= nkv * rep * hd,
+               "%s: q, caches and out must be 16-byte aligned (max_len %% 8 == 0)", who);
+  if (B == 0) return 0;
+  const dim3 grid((unsigned)(B * nkv)), block(64 * kAttnWaves);
+  hipStream_t st = (hipStream_t)stream;
+#define HN_ATTN(R, LM)                                                                        \
+  hipLaunchKernelGGL((attn_decode_kernel<R, LM>), grid, block, 0, st, (const h16*)q,        \
+                     (const h16*)kt, (const h16*)v, max_len, (int)nkv, (int)L,              \
+                     (const h16*)mask, inv_scale, (h16*)out, ld_o)
+#define HN_ATTN_L(R) \
+  if (L <= 256) HN_ATTN(R, 256); else if (L <= 512) HN_ATTN(R, 512); else HN_ATTN(R, 1024)
+  if (rep == 1) { HN_ATTN_L(1); }
+  else if (rep == 2) { HN_ATTN_L(2); }
+  else { HN_ATTN_L(4); }
+#undef HN_ATTN_L
+#undef HN_ATTN
+  HN_LAUNCH_CHECK(who);
   return 0;
 }

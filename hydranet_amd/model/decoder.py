@@ -132,6 +132,17 @@ class Attention(nn.Module):
         self.k_proj = nn.Linear(H, self.nkv * self.hd, bias=False)
         self.v_proj = nn.Linear(H, self.nkv * self.hd, bias=False)
         self.o_proj = nn.Linear(self.nh * self.hd, H, bias=False)
+        # one-token steps on the GPU: attention in one launch (hn_attn_decode)
+        # where its shape limits allow; False keeps the two products
+        self.decode_kernel = True
+
+    def _decode_fits(self, x: torch.Tensor, S: int, cache: "KVCache", kv_len: int,
+                     mask: Optional[torch.Tensor]) -> bool:
+        return (self.decode_kernel and x.is_cuda and S == 1 and self.hd == 128
+                and self.nh // self.nkv in (1, 2, 4) and 1 <= kv_len <= 1024
+                and cache.max_len % 8 == 0 and cache.max_len >= -(-kv_len // 8) * 8
+                and (mask is None or (mask.dtype == torch.float16 and mask.numel() == kv_len
+                                      and mask.is_contiguous())))
 
     def _qkv(self, x2: torch.Tensor) -> torch.Tensor:
         """q, k and v projections of x2 [rows, H] as one product: the fp16
@@ -195,6 +206,14 @@ class Attention(nn.Module):
             q, k = apply_rotary(q, k, cos.to(q.dtype), sin.to(q.dtype))
             cache.update(layer, k, v, pos)
             qg = q.reshape(B, nkv, rep * S, hd)  # rows: (head within the group, token)
+        if self._decode_fits(x, S, cache, kv_len, mask):
+            from .. import _lib
+            o = torch.empty((B, nh * hd), dtype=x.dtype, device=x.device)
+            inv = float(np.float32(1.0) / np.float32(math.sqrt(hd)))
+            _lib.call("hn_attn_decode", _lib.ptr(qg), _lib.ptr(cache.kt[layer]),
+                      _lib.ptr(cache.v[layer]), cache.max_len, B, nkv, rep, hd, kv_len,
+                      _lib.ptr(mask), inv, _lib.ptr(o), o.stride(0), _lib.stream(x.device))
+            return self.o_proj(o.view(B, S, nh * hd))
         kt, vv = cache.get(layer, kv_len)
         scores = torch.matmul(qg, kt)  # [B, nkv, rep * S, kv_len]
         if x.is_cuda and kv_len <= 1024 and (mask is None or mask.dtype == torch.float16):

@@ -341,6 +341,20 @@ int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, long ld_r, 
  *   for rows of up to 1024. */
 int hn_attn_softmax(const void* scores, long ld_s, const void* mask, long ld_m, long mask_rows,
                     long rows, long L, float inv_scale, void* out, long ld_o, void* stream);
+/* hn_attn_decode: grouped-query attention of one query token per sequence
+ *   over the KV cache, one launch per layer (the decode step of the
+ *   reference's Attention, model/mixtral.py:150-207, in place of its two
+ *   products and the softmax between them).  q [B][nkv][rep][hd] fp16 (the
+ *   rotated queries of hn_rope_append), kt [B][nkv][hd][max_len] (keys
+ *   transposed), v [B][nkv][max_len][hd]; attends over positions [0, L):
+ *   s = fp16(q . k) (fp32 sums), a = fp16(s * inv_scale), a = fp16(a +
+ *   mask[l]) with mask [L] fp16 (0 / -inf) when given, p = fp16(
+ *   softmax_fp32(a)), out[b][(g * rep + r) * hd + d] = fp16(sum_l p v) (fp32
+ *   sums).  hd 128, rep 1, 2 or 4, 1 <= L <= 1024, max_len a multiple of 8
+ *   holding L rounded up to 8; 16-byte aligned operands. */
+int hn_attn_decode(const void* q, const void* kt, const void* v, long max_len, long B, long nkv,
+                   long rep, long hd, long L, const void* mask, float inv_scale, void* out,
+                   long ld_o, void* stream);
 int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k, const void* v, long ld_v,
                    const float* cos_t, const float* sin_t, const long* pos, long B, long S,
                    long nh, long nkv, long hd, void* q_out, void* kt, void* vc, long max_len,

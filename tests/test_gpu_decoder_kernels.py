@@ -3,6 +3,7 @@ against the reference's torch formulation of the same steps
 (model/mixtral.py:23-37 RMSNorm, 82-101 RoPE; the KV-cache append):
 the residual add, RoPE and the cache writes bit for bit; RMSNorm within one
 fp16 ulp (fp32 mean in another summation order), nearly all elements equal."""
+import numpy as np
 import pytest
 import torch
 
@@ -121,6 +122,66 @@ def test_attn_softmax_matches_torch_formulation(rows, L, S, masked):
     torch.cuda.synchronize()
     diff = (got != ref)
     assert not bool(diff.any()), (int(diff.sum()), float((got.float() - ref.float()).abs().max()))
+
+
+@pytest.mark.parametrize("B,nkv,rep,L,max_len,masked", [
+    (2, 2, 4, 1, 8, False), (3, 2, 4, 7, 16, True), (2, 8, 4, 512, 768, False),
+    (4, 8, 4, 640, 768, True), (2, 2, 2, 777, 784, False), (2, 2, 1, 1024, 1024, True),
+    (1, 1, 4, 300, 304, False), (64, 8, 4, 576, 768, True)])
+def test_attn_decode_vs_two_products(B, nkv, rep, L, max_len, masked):
+    """hn_attn_decode (one launch) against the reference's steps run by torch
+    on the same GPU: fp16 score product, / sqrt(head_dim), + mask,
+    F.softmax(dtype=float32).to(fp16), fp16 value product; and against a
+    float64 CPU evaluation of the same roundings.  fp16 outputs within
+    max-abs 1e-2 and relative 2e-3 of both (the fp32 sums run in another
+    order than the library GEMM's).  Cache positions past L hold NaN, which
+    must not reach the result."""
+    import math
+    from hydranet_amd.model.decoder import attn_softmax
+    hd = 128
+    print(f"[attn_decode] B={B} nkv={nkv} rep={rep} L={L} max_len={max_len} masked={masked}",
+          flush=True)
+    g = torch.Generator(device=DEV).manual_seed(B * 1000 + L)
+    q = torch.randn(B, nkv, rep, hd, generator=g, device=DEV).half()
+    kt = torch.randn(B, nkv, hd, max_len, generator=g, device=DEV).half()
+    v = torch.randn(B, nkv, max_len, hd, generator=g, device=DEV).half()
+    kt[..., L:] = float("nan")
+    v[:, :, L:] = float("nan")
+    mask = None
+    if masked:
+        mask = torch.zeros((1, L), dtype=torch.float16, device=DEV)
+        mask[:, L - L // 4:] = float("-inf") if L > 1 else 0.0
+    out = torch.full((B, nkv * rep * hd), float("nan"), dtype=torch.float16, device=DEV)
+    inv = float(np.float32(1.0) / np.float32(math.sqrt(hd)))
+    _lib.call("hn_attn_decode", _lib.ptr(q), _lib.ptr(kt), _lib.ptr(v), max_len, B, nkv, rep,
+              hd, L, _lib.ptr(mask), inv, _lib.ptr(out), out.stride(0), _lib.stream())
+    # the reference's two products with the softmax between them
+    sc = torch.matmul(q, kt[..., :L].contiguous())
+    p = attn_softmax(sc, mask, hd)
+    ref = torch.matmul(p, v[:, :, :L].contiguous()).reshape(B, -1)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    err = (out.float() - ref.float()).abs()
+    assert bool((err <= 1e-2 + 2e-3 * ref.float().abs()).all()), float(err.max())
+    # float64 on the CPU with the same fp16 roundings
+    qd, kd, vd = q.double().cpu(), kt[..., :L].double().cpu(), v[:, :, :L].double().cpu()
+    s16 = (qd @ kd).half()
+    a = (s16.float() * inv).half()
+    if mask is not None:
+        a = (a.float() + mask.float().cpu()).half()
+    p64 = torch.softmax(a.double(), dim=-1).half()
+    ref64 = (p64.double() @ vd).reshape(B, -1)
+    err = (out.double().cpu() - ref64).abs()
+    assert bool((err <= 1e-2 + 2e-3 * ref64.abs()).all()), float(err.max())
+
+
+def test_attn_decode_rejects_bad_shapes():
+    for args in ((64, 1, 1, 4, 96, 8), (64, 1, 1, 3, 128, 8), (64, 1, 1, 4, 128, 1025),
+                 (60, 1, 1, 4, 128, 8), (8, 1, 1, 4, 128, 9)):
+        max_len, B, nkv, rep, hd, L = args
+        with pytest.raises(RuntimeError, match="hn_attn_decode"):
+            _lib.call("hn_attn_decode", None, None, None, max_len, B, nkv, rep, hd, L, None,
+                      0.1, None, 4096, None)
 
 
 def _rotate_half(x):
