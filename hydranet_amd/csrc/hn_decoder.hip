@@ -237,15 +237,18 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 //  * scores: thread (position group pg = tid / 8, d slice ds = tid % 8)
 //    loads keys d = 16 ds .. 16 ds + 15 at positions 8 pg .. 8 pg + 7 (16
 //    loads of 16 bytes, all in flight: the head's whole K in one round
-//    trip) and accumulates the REP x 8 partial sums in fp32; a three-step
-//    reduce-scatter over the 8 lanes of a group (DPP) leaves lane ds the
-//    sums of position 8 pg + ds;
+//    trip) and accumulates the REP x 8 partial sums in fp32 with v_dot2
+//    (fp16 pairs of d, the keys of two rows packed per position by
+//    v_perm: 2.5 instructions per key element instead of 4 mixed FMAs);
+//    a three-step reduce-scatter over the 8 lanes of a group (DPP) leaves
+//    lane ds the sums of position 8 pg + ds; waves wholly past L skip it;
 //  * the values' loads go out next (thread: 8 d columns dg, positions
 //    ls + 64 i), before the softmax, whose reductions hide their latency;
 //  * softmax per row over LDS (row max, then exp sums: per lane in index
 //    order, then the wave's butterfly, then the waves in order);
-//  * values: per-thread fp32 sums over its positions, a reduce-scatter over
-//    the wave's 4 position slices, then the 16 waves added in order.
+//  * values: per-thread fp32 sums over its positions (v_dot2 over position
+//    pairs), a reduce-scatter over the wave's 4 position slices, then the 16
+//    waves added in order.
 // The fp32 sums run in another order than a library GEMM's, so outputs
 // agree with the two-product formulation within fp16 rounding.
 constexpr int kAttnHd = 128;
@@ -270,14 +273,18 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     h16* __restrict__ out, long ld_o) {
   constexpr int HD = kAttnHd;
   constexpr int NV = LMAX / 64;  // value positions per thread
-  __shared__ __align__(16) float s_q[HD][4];       // q[r][d] as [d][r]
-  // scaled scores, then probabilities; 1024 rows whatever LMAX, so every
-  // lane's position (8 pg + ds < 1024) has a row and the store after the
-  // DPP exchanges needs no branch
-  __shared__ __align__(16) float s_x[1024][4];
+  // LDS arrays are read with the types they are written with: a vector
+  // load of query pairs written as scalars let the compiler keep only its
+  // first element (all query heads got head 0's scores)
+  __shared__ uint32_t s_q2[HD / 2][4];  // [i][r] = (q[r][2 i], q[r][2 i + 1])
+  // scaled scores, then probabilities, [l][r]; 1024 rows whatever LMAX, so
+  // every lane's position (8 pg + ds < 1024) has a row and the store after
+  // the DPP exchanges needs no branch
+  __shared__ float4_t s_x[1024];
   __shared__ float s_red[2][kAttnWaves];
   __shared__ __align__(16) float s_o[kAttnWaves][REP][HD];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const int bg = blockIdx.x;  // b * nkv + g
   const int b = bg / nkv, g = bg - b * nkv;
   const h16* qb = q + (long)bg * REP * HD;
@@ -288,43 +295,59 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   constexpr uint32_t kOOB = 0x7ffffff0u;
 
   // 1. keys: all 16 loads of the thread in flight (positions past the
-  //    groups of L read nothing)
+  //    groups of L read nothing; waves wholly past them skip the scores)
   const int pg = tid >> 3, ds = tid & 7;
   const int npg = (L + 7) >> 3;
+  const bool kwave = 64 * wave < L;  // uniform
   const uint32_t ko = pg < npg ? (uint32_t)(((16 * ds) * max_len + 8 * pg) * 2) : kOOB;
   u32x4 kr[16];
+  if (kwave) {
 #pragma unroll
-  for (int dd = 0; dd < 16; ++dd)
-    kr[dd] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           rk, ko == kOOB ? kOOB : ko + (uint32_t)(dd * max_len * 2),
-                                           0, 0));
+    for (int dd = 0; dd < 16; ++dd)
+      kr[dd] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rk, ko == kOOB ? kOOB : ko + (uint32_t)(dd * max_len * 2), 0, 0));
+  }
   // this lane's score position and its mask entry (loaded with the keys)
   const int lpos = 8 * pg + ds;
   const bool lon = lpos < L;
   const float mv = mask ? (float)mask[lon ? lpos : L - 1] : 0.f;
-  if (tid < REP * HD) {
-    const int r = tid / HD, d = tid - r * HD;
-    s_q[d][r] = (float)qb[r * HD + d];
+  if (tid < REP * HD / 2) {
+    const int r = tid / (HD / 2), i = tid - r * (HD / 2);
+    s_q2[i][r] = *reinterpret_cast<const uint32_t*>(qb + r * HD + 2 * i);
   }
   __syncthreads();
 
-  // 2. scores: fp32 sums over the thread's 16 d, then over the 8 d slices
+  // 2. scores: fp32 sums over the thread's 16 d (v_dot2: pairs of d, the
+  //    keys of two rows packed per position), then over the 8 d slices
   float acc[REP][8];
 #pragma unroll
   for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[r][j] = 0.f;
+  if (kwave) {
 #pragma unroll
-  for (int dd = 0; dd < 16; ++dd) {
-    const float4_t qv = *reinterpret_cast<const float4_t*>(&s_q[16 * ds + dd][0]);
-    const half8_t kv = __builtin_bit_cast(half8_t, kr[dd]);
+    for (int dd = 0; dd < 16; dd += 2) {
+      uint32_t q2[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float kf = (float)kv[j];
+      for (int r = 0; r < 4; ++r) q2[r] = s_q2[8 * ds + dd / 2][r];
 #pragma unroll
-      for (int r = 0; r < REP; ++r) acc[r][j] = __builtin_fmaf(qv[r], kf, acc[r][j]);
+      for (int w = 0; w < 4; ++w) {
+        // (k[d][2 w], k[d + 1][2 w]) and (k[d][2 w + 1], k[d + 1][2 w + 1])
+        const uint32_t lo = __builtin_amdgcn_perm(kr[dd + 1][w], kr[dd][w], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(kr[dd + 1][w], kr[dd][w], 0x07060302u);
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          const half2_t qa = __builtin_bit_cast(half2_t, q2[r]);
+          acc[r][2 * w] = __builtin_amdgcn_fdot2(qa, __builtin_bit_cast(half2_t, lo),
+                                                 acc[r][2 * w], false);
+          acc[r][2 * w + 1] = __builtin_amdgcn_fdot2(qa, __builtin_bit_cast(half2_t, hi),
+                                                     acc[r][2 * w + 1], false);
+        }
+      }
     }
   }
+  if (kwave) {
   // reduce-scatter over ds (lane bits 2, 1, 0): keep positions of bit 2 = h
   // (4 of 8), then bit 1 (2 of 4), then bit 0 (1 of 2); each step adds the
   // kept half of this lane and the partner's copy of the same positions
@@ -377,7 +400,8 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
       }
       xs[r] = xv;
     }
-    *reinterpret_cast<float4_t*>(&s_x[l][0]) = xs;
+    s_x[l] = xs;
+  }
   }
 
   // 3. values: thread (8 columns dg, positions ls + 64 i); loads out now
@@ -435,23 +459,31 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   }
   __syncthreads();
 
-  // 5. values: o[r][8 dg + j] over the thread's positions
+  // 5. values: o[r][8 dg + j] over the thread's positions, v_dot2 over
+  //    position pairs (i, i + 1): the values of two rows packed per column,
+  //    the probabilities (fp16 values held in fp32, so the packing is exact)
   float oa[REP][8];
 #pragma unroll
   for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int j = 0; j < 8; ++j) oa[r][j] = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int l = ls + 64 * i;
-    if (64 * i < L) {  // uniform enough: past L the loads returned zero
-      const float4_t pv = *reinterpret_cast<const float4_t*>(&s_x[l][0]);
-      const half8_t vv = __builtin_bit_cast(half8_t, vr[i]);
+  for (int i = 0; i < NV; i += 2) {
+    if (64 * i < L) {  // uniform: past L the loads returned zero
+      const float4_t pa = s_x[ls + 64 * i];
+      const float4_t pb = s_x[ls + 64 * (i + 1)];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float vf = (float)vv[j];
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = __builtin_amdgcn_perm(vr[i + 1][w], vr[i][w], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(vr[i + 1][w], vr[i][w], 0x07060302u);
 #pragma unroll
-        for (int r = 0; r < REP; ++r) oa[r][j] = __builtin_fmaf(pv[r], vf, oa[r][j]);
+        for (int r = 0; r < REP; ++r) {
+          const half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(pa[r], pb[r]));
+          oa[r][2 * w] = __builtin_amdgcn_fdot2(p2, __builtin_bit_cast(half2_t, lo),
+                                                oa[r][2 * w], false);
+          oa[r][2 * w + 1] = __builtin_amdgcn_fdot2(p2, __builtin_bit_cast(half2_t, hi),
+                                                    oa[r][2 * w + 1], false);
+        }
       }
     }
   }
@@ -619,8 +651,11 @@ extern "C" int hn_attn_decode(const void* q, const void* kt, const void* v, long
   hipLaunchKernelGGL((attn_decode_kernel<R, LM>), grid, block, 0, st, (const h16*)q,        \
                      (const h16*)kt, (const h16*)v, max_len, (int)nkv, (int)L,              \
                      (const h16*)mask, inv_scale, (h16*)out, ld_o)
-#define HN_ATTN_L(R) \
-  if (L <= 256) HN_ATTN(R, 256); else if (L <= 512) HN_ATTN(R, 512); else HN_ATTN(R, 1024)
+#define HN_ATTN_L(R)             \
+  if (L <= 256) HN_ATTN(R, 256);      \
+  else if (L <= 512) HN_ATTN(R, 512); \
+  else if (L <= 768) HN_ATTN(R, 768); \
+  else HN_ATTN(R, 1024)
   if (rep == 1) { HN_ATTN_L(1); }
   else if (rep == 2) { HN_ATTN_L(2); }
   else { HN_ATTN_L(4); }
