@@ -9,8 +9,9 @@ synthetic input already resident in HBM:
   c2  (default, the headline) one Mixtral MoE layer at decode, T = 1, 4, 16
       (value: T = 16): route + grouped gate/up + down + unpermute.  The default
       line also carries C1 ("c1": one expert at T = 1 against the 0.70 target),
-      C3 ("c3"), C4 ("c4", TFLOP/s with its own MFMA roofline) and the C5
-      decoder (decoder_tokens_per_s); --skip-c34 / --skip-c5 leave those out
+      C3 ("c3"), C4 ("c4", TFLOP/s with its own MFMA roofline), the C5
+      decoder (decoder_tokens_per_s) and the expert-miss load path ("h2d");
+      --skip-c34 / --skip-c5 / --skip-h2d leave those out
   c1  one Mixtral expert SwiGLU (H 4096, I 14336, INT4 g128), T tokens (default 1)
   c3  one GLM-4.5-Air MoE layer at decode (T = 32, 128 experts, shared expert)
   c4  one Mixtral MoE layer at prefill (2048 tokens, Zipf-skewed routing)
@@ -909,6 +910,8 @@ def main():
                          "default: the layer's")
     ap.add_argument("--decode-tokens", type=int, default=256, help="c5: tokens generated")
     ap.add_argument("--warmup-decode", type=int, default=3, help="c5: untimed decode forwards")
+    ap.add_argument("--skip-h2d", action="store_true",
+                    help="c2: leave out the expert-miss load path (workload h2d)")
     ap.add_argument("--skip-c5", action="store_true",
                     help="c2: leave out the whole-decoder tokens/s run (workload c5)")
     ap.add_argument("--skip-c34", action="store_true",
@@ -1045,6 +1048,13 @@ def main():
             res["decoder_tokens_per_s"] = c5["tokens_per_s"]
             res["decoder_tokens_per_s_top2"] = c5["top2"]["tokens_per_s"]
             res["config"]["c5_decoder"] = c5
+        if not args.skip_h2d:
+            # the residency layer's expert-miss load path (pinned -> HBM, and a
+            # store on disk -> HBM), beside the resident-path numbers
+            torch.cuda.empty_cache()
+            h2d = bench_h2d(args)
+            _log("h2d", h2d)
+            res["h2d"] = h2d
     else:
         cpu = cpu_c1
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
