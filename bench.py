@@ -255,13 +255,13 @@ def bench_c2(args, T: int, n_layers: int = 4, phases: bool = False):
 
 
 def time_decode_phases(layers, x, T, H, I, g, E, reps: int = 12):
-    """The two expert phases of the decode layer timed inside the layer's own
-    launch sequence over the rotating layers: routing + gate/up (one launch,
-    hn_moe_route_gate_up) -> down in four K slices (hn_grouped_decode_phase_int4
-    phase 1) -> unpermute, with an event on the launch stream before and after
-    each of the first two.  Bytes per launch: the active experts' packed weights
-    and scales plus activations in and out (and the fp16 gate for the routing;
-    the down phase writes four fp32 K-slice partials)."""
+    """The two expert phases of the decode layer over the rotating layers:
+    routing + gate/up (one launch, hn_moe_route_gate_up) and the down
+    projection in four K slices (hn_grouped_decode_phase_int4 phase 1), each
+    timed as a run of back-to-back launches after a warm-up pass of whole
+    layers.  Bytes per launch: the active experts' packed weights and scales
+    plus activations in and out (and the fp16 gate for the routing; the down
+    phase writes four fp32 K-slice partials)."""
     from hydranet_amd import _lib
     from hydranet_amd.model.moe import Routed
     k = 2
@@ -297,23 +297,26 @@ def time_decode_phases(layers, x, T, H, I, g, E, reps: int = 12):
                   _lib.ptr(r.w), T, k, None, H, _lib.ptr(out), H, H, sp)
 
     n_it = 4 * reps
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4 * n_it)]
-    for it in range(4):  # warm-up
+    for it in range(4):  # warm-up: every layer's routing outputs in place
         route_gate_up(it % 4); down(it % 4); unpermute(it % 4)
     torch.cuda.synchronize()
+    # each phase as n_it back-to-back launches over the rotating layers between
+    # two events on the launch stream (the host enqueues faster than a launch
+    # runs, so the average is the kernel's duration plus the queue's gap, not
+    # the per-launch dispatch an event pair around each eager launch adds)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record()
     for it in range(n_it):
-        li = it % len(layers)
-        ev[4 * it].record()
-        route_gate_up(li)
-        ev[4 * it + 1].record()
-        ev[4 * it + 2].record()
-        down(li)
-        ev[4 * it + 3].record()
-        unpermute(li)
+        route_gate_up(it % len(layers))
+    ev[1].record()
+    ev[2].record()
+    for it in range(n_it):
+        down(it % len(layers))
+    ev[3].record()
     torch.cuda.synchronize()
     nact = [int(r.n_active.item()) for r in rts]
-    t_gu = sum(ev[4 * it].elapsed_time(ev[4 * it + 1]) for it in range(n_it)) / n_it * 1e3
-    t_dn = sum(ev[4 * it + 2].elapsed_time(ev[4 * it + 3]) for it in range(n_it)) / n_it * 1e3
+    t_gu = ev[0].elapsed_time(ev[1]) / n_it * 1e3
+    t_dn = ev[2].elapsed_time(ev[3]) / n_it * 1e3
     res = {}
     avg_act = sum(nact) / len(nact)
     for name, us, nbytes in (("route_gate_up_silu", t_gu,
@@ -882,7 +885,7 @@ def bench_c5(args):
 # --pmc passes over `bench.py --workload c2phase`, each scaled by the same
 # counter on a 512 MiB copy.  Commands, raw counter values and scale factors:
 # profiles/route_gate_up_c2_t16_traffic.md.  Re-measure after a kernel change.
-ROUTE_GATE_UP_C2_T16_TRAFFIC = 487_463_494
+ROUTE_GATE_UP_C2_T16_TRAFFIC = 487_510_777
 
 
 def main():
