@@ -41,6 +41,7 @@ SIGNATURES: dict[str, list] = {
     "hn_add_rmsnorm_router": [P, L, P, L, P, L, P, P, L, L, L, F, P, L, L, P, P],
     "hn_attn_softmax": [P, L, P, L, L, L, L, F, P, L, P],
     "hn_attn_decode": [P, P, P, L, L, L, L, L, L, P, F, P, L, P],
+    "hn_attn_decode_rope": [P, L, P, P, P, P, P, L, L, L, L, L, L, P, F, P, L, P],
     "hn_rope_append": [P, L, P, L, P, L, P, P, P, L, L, L, L, L, P, P, P, L, P],
     "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],
     "hn_set_decode_path": [I],

@@ -185,6 +185,25 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(const h16* __restrict
 // q_out[b][h / rep][h % rep][s][:]; the others are KV heads g: the rotated
 // key goes to kt[b][g][:][pos[s]] (keys transposed), the value to
 // vc[b][g][pos[s]][:].
+// RoPE of element d of one head's row at position p (model/mixtral.py:82-101):
+// c, s = fp16(cos[p][d]), fp16(sin[p][d]); y = fp16(fp16(x[d] c) + fp16(rh(x)[d]
+// s)), rh(x) = (-x[hd/2:], x[:hd/2]).  Each product is rounded to fp16
+// before the sum (no fused multiply-add); one function for every kernel that
+// rotates, so they agree bit for bit.
+__device__ __forceinline__ h16 rope_rot(const h16* src, const float* cos_t, const float* sin_t,
+                                        long p, int d, int hd) {
+#pragma clang fp contract(off)
+  const int half = hd >> 1;
+  const h16 c = (h16)cos_t[p * hd + d];
+  const h16 sn = (h16)sin_t[p * hd + d];
+  const int dp = d < half ? d + half : d - half;
+  const h16 xd = src[d];
+  const h16 xr = d < half ? (h16)(-(float)src[dp]) : src[dp];
+  const h16 a = (h16)((float)xd * (float)c);
+  const h16 bb = (h16)((float)xr * (float)sn);
+  return (h16)((float)a + (float)bb);
+}
+
 __global__ void rope_append_kernel(const h16* __restrict__ q, long ld_q, const h16* __restrict__ k,
                                    long ld_k, const h16* __restrict__ v, long ld_v,
                                    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
@@ -197,17 +216,7 @@ __global__ void rope_append_kernel(const h16* __restrict__ q, long ld_q, const h
   const int b = row / S, s = row - b * S;
   const long p = pos[s];
   if (p < 0 || p >= max_len) return;  // callers check positions on the host too
-  const int half = hd >> 1;
-  const h16 c = (h16)cos_t[p * hd + d];
-  const h16 sn = (h16)sin_t[p * hd + d];
-  const int dp = d < half ? d + half : d - half;
-  auto rot = [&](const h16* src) -> h16 {
-    const h16 xd = src[d];
-    const h16 xr = d < half ? (h16)(-(float)src[dp]) : src[dp];
-    const h16 a = (h16)((float)xd * (float)c);
-    const h16 bb = (h16)((float)xr * (float)sn);
-    return (h16)((float)a + (float)bb);
-  };
+  auto rot = [&](const h16* src) -> h16 { return rope_rot(src, cos_t, sin_t, p, d, hd); };
   const int rep = nh / nkv;
   if (head < nh) {
     const h16* src = q + (long)row * ld_q + (long)head * hd;
@@ -266,11 +275,19 @@ __device__ __forceinline__ float xor4_f32(float v, bool hi) {
   return hi ? dn : up;
 }
 
-template <int REP, int LMAX>
+// ROPE: the step's own query, key and value come unrotated from the fused
+// q/k/v projection (qkv[b][ld_qkv]: nh query heads, nkv keys, nkv values);
+// the workgroup rotates its REP query heads and its key (rope_rot, the same
+// arithmetic as hn_rope_append), writes the key and value to the cache at
+// the step's position p = pos[0], and uses them directly: the cache loads
+// go out first, and the lanes holding position p take the new key and value
+// in registers (the loaded copies are from before the write).
+template <int REP, int LMAX, bool ROPE>
 __global__ __launch_bounds__(1024) void attn_decode_kernel(
-    const h16* __restrict__ q, const h16* __restrict__ kt, const h16* __restrict__ vc,
-    long max_len, int nkv, int L, const h16* __restrict__ mask, float inv_scale,
-    h16* __restrict__ out, long ld_o) {
+    const h16* __restrict__ q, h16* __restrict__ kt, h16* __restrict__ vc, long max_len,
+    int nkv, int L, const h16* __restrict__ mask, float inv_scale, h16* __restrict__ out,
+    long ld_o, const h16* __restrict__ qkv, long ld_qkv, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const long* __restrict__ pos) {
   constexpr int HD = kAttnHd;
   constexpr int NV = LMAX / 64;  // value positions per thread
   // LDS arrays are read with the types they are written with: a vector
@@ -283,6 +300,8 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   __shared__ float4_t s_x[1024];
   __shared__ float s_red[2][kAttnWaves];
   __shared__ __align__(16) float s_o[kAttnWaves][REP][HD];
+  __shared__ uint32_t s_knew[HD / 2];  // ROPE: the step's rotated key, d pairs
+  __shared__ uint32_t s_vnew[HD / 2];  // ROPE: the step's value, d pairs
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const int bg = blockIdx.x;  // b * nkv + g
@@ -312,11 +331,66 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
   const int lpos = 8 * pg + ds;
   const bool lon = lpos < L;
   const float mv = mask ? (float)mask[lon ? lpos : L - 1] : 0.f;
-  if (tid < REP * HD / 2) {
+  long pnew = -1;  // ROPE: the step's position
+  if (ROPE) {
+    // threads (row r <= REP, pair i): rows < REP the query heads, row REP the
+    // key; the next HD / 2 threads the value pairs
+    pnew = pos[0];
+    // a position outside the cache writes nothing and patches nothing (the
+    // callers check it on the host too)
+    const bool pok = pnew >= 0 && pnew < max_len;
+    const long prot = pok ? pnew : 0;  // the tables' row the rotation reads
+    if (!pok) pnew = -1;
+    const int nh = nkv * REP;
+    const h16* rowp = qkv + (long)b * ld_qkv;
+    if (tid < (REP + 1) * (HD / 2)) {
+      const int r = tid / (HD / 2), i = tid - r * (HD / 2);
+      const h16* src = r < REP ? rowp + (long)(g * REP + r) * HD : rowp + (long)(nh + g) * HD;
+      const h16 y0 = rope_rot(src, cos_t, sin_t, prot, 2 * i, HD);
+      const h16 y1 = rope_rot(src, cos_t, sin_t, prot, 2 * i + 1, HD);
+      const uint32_t pr = (uint32_t)__builtin_bit_cast(uint16_t, y0) |
+                          ((uint32_t)__builtin_bit_cast(uint16_t, y1) << 16);
+      if (r < REP) {
+        s_q2[i][r] = pr;
+      } else {
+        s_knew[i] = pr;
+        if (pok) {
+          h16* kcol = kt + ((long)bg * HD + 2 * i) * max_len + pnew;
+          kcol[0] = y0;
+          kcol[max_len] = y1;
+        }
+      }
+    } else if (tid < (REP + 2) * (HD / 2)) {
+      const int i = tid - (REP + 1) * (HD / 2);
+      const uint32_t pr =
+          *reinterpret_cast<const uint32_t*>(rowp + (long)(nh + nkv + g) * HD + 2 * i);
+      s_vnew[i] = pr;
+      if (pok) *reinterpret_cast<uint32_t*>(vc + ((long)bg * max_len + pnew) * HD + 2 * i) = pr;
+    }
+  } else if (tid < REP * HD / 2) {
     const int r = tid / (HD / 2), i = tid - r * (HD / 2);
     s_q2[i][r] = *reinterpret_cast<const uint32_t*>(qb + r * HD + 2 * i);
   }
   __syncthreads();
+  if (ROPE && kwave) {
+    // the lanes of position pnew take the new key (the loaded one is from
+    // before this step's write)
+    const int jp = (int)(pnew - 8 * pg);
+    if (jp >= 0 && jp < 8) {
+#pragma unroll
+      for (int dd = 0; dd < 16; ++dd) {
+        const int d = 16 * ds + dd;
+        const uint32_t kn = (s_knew[d >> 1] >> (16 * (d & 1))) & 0xffffu;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          if ((jp >> 1) == w) {
+            const uint32_t cur = kr[dd][w];
+            kr[dd][w] = (jp & 1) ? ((cur & 0xffffu) | (kn << 16)) : ((cur & 0xffff0000u) | kn);
+          }
+        }
+      }
+    }
+  }
 
   // 2. scores: fp32 sums over the thread's 16 d (v_dot2: pairs of d, the
   //    keys of two rows packed per position), then over the 8 d slices
@@ -472,10 +546,19 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     if (64 * i < L) {  // uniform: past L the loads returned zero
       const float4_t pa = s_x[ls + 64 * i];
       const float4_t pb = s_x[ls + 64 * (i + 1)];
+      u32x4 va = vr[i], vb = vr[i + 1];
+      if (ROPE) {
+        // the lanes of position pnew take the step's value
+        u32x4 vn;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) vn[w] = s_vnew[4 * dg + w];
+        if (ls + 64 * i == pnew) va = vn;
+        if (ls + 64 * (i + 1) == pnew) vb = vn;
+      }
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = __builtin_amdgcn_perm(vr[i + 1][w], vr[i][w], 0x05040100u);
-        const uint32_t hi = __builtin_amdgcn_perm(vr[i + 1][w], vr[i][w], 0x07060302u);
+        const uint32_t lo = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
           const half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(pa[r], pb[r]));
@@ -627,12 +710,12 @@ extern "C" int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k
   return 0;
 }
 
-// Decode attention over the KV cache (one query token per sequence).  See
-// include/hn_int4.h.
-extern "C" int hn_attn_decode(const void* q, const void* kt, const void* v, long max_len, long B,
-                              long nkv, long rep, long hd, long L, const void* mask,
-                              float inv_scale, void* out, long ld_o, void* stream) {
-  const char* who = "hn_attn_decode";
+// Decode attention over the KV cache (one query token per sequence); with
+// qkv, the step's RoPE and cache append too.
+static int attn_decode(const char* who, const void* q, const void* qkv, long ld_qkv,
+                       const float* cos_t, const float* sin_t, const long* pos, void* kt, void* v,
+                       long max_len, long B, long nkv, long rep, long hd, long L,
+                       const void* mask, float inv_scale, void* out, long ld_o, void* stream) {
   HN_ARG_CHECK(B >= 0 && nkv > 0 && (rep == 1 || rep == 2 || rep == 4) && hd == kAttnHd,
                "%s: need head_dim %d and 1, 2 or 4 query heads per KV head (rep=%ld hd=%ld)",
                who, kAttnHd, rep, hd);
@@ -644,13 +727,27 @@ extern "C" int hn_attn_decode(const void* q, const void* kt, const void* v, long
   HN_ARG_CHECK(al16(q) && al16(kt) && al16(v) && max_len % 8 == 0 && al16(out) && ld_o % 8 == 0 &&
                    ld_o >= nkv * rep * hd,
                "%s: q, caches and out must be 16-byte aligned (max_len %% 8 == 0)", who);
+  HN_ARG_CHECK(!qkv || (((uintptr_t)qkv & 3) == 0 && ld_qkv % 2 == 0 &&
+                        ld_qkv >= (nkv * rep + 2 * nkv) * hd && cos_t && sin_t && pos),
+               "%s: qkv rows must be 4-byte aligned and hold q, k and v (with the RoPE "
+               "tables and the position)", who);
   if (B == 0) return 0;
   const dim3 grid((unsigned)(B * nkv)), block(64 * kAttnWaves);
   hipStream_t st = (hipStream_t)stream;
-#define HN_ATTN(R, LM)                                                                        \
-  hipLaunchKernelGGL((attn_decode_kernel<R, LM>), grid, block, 0, st, (const h16*)q,        \
-                     (const h16*)kt, (const h16*)v, max_len, (int)nkv, (int)L,              \
-                     (const h16*)mask, inv_scale, (h16*)out, ld_o)
+#define HN_ATTN(R, LM)                                                                         \
+  do {                                                                                       \
+    if (qkv)                                                                                 \
+      hipLaunchKernelGGL((attn_decode_kernel<R, LM, true>), grid, block, 0, st,              \
+                         (const h16*)nullptr, (h16*)kt, (h16*)v, max_len, (int)nkv, (int)L,  \
+                         (const h16*)mask, inv_scale, (h16*)out, ld_o, (const h16*)qkv,      \
+                         ld_qkv, cos_t, sin_t, pos);                                         \
+    else                                                                                     \
+      hipLaunchKernelGGL((attn_decode_kernel<R, LM, false>), grid, block, 0, st,             \
+                         (const h16*)q, (h16*)kt, (h16*)v, max_len, (int)nkv, (int)L,        \
+                         (const h16*)mask, inv_scale, (h16*)out, ld_o, (const h16*)nullptr,  \
+                         0L, (const float*)nullptr, (const float*)nullptr,                   \
+                         (const long*)nullptr);                                              \
+  } while (0)
 #define HN_ATTN_L(R)             \
   if (L <= 256) HN_ATTN(R, 256);      \
   else if (L <= 512) HN_ATTN(R, 512); \
@@ -663,4 +760,24 @@ extern "C" int hn_attn_decode(const void* q, const void* kt, const void* v, long
 #undef HN_ATTN
   HN_LAUNCH_CHECK(who);
   return 0;
+}
+
+// See include/hn_int4.h.
+extern "C" int hn_attn_decode(const void* q, const void* kt, const void* v, long max_len, long B,
+                              long nkv, long rep, long hd, long L, const void* mask,
+                              float inv_scale, void* out, long ld_o, void* stream) {
+  return attn_decode("hn_attn_decode", q, nullptr, 0, nullptr, nullptr, nullptr, (void*)kt,
+                     (void*)v, max_len, B, nkv, rep, hd, L, mask, inv_scale, out, ld_o, stream);
+}
+
+// See include/hn_int4.h.
+extern "C" int hn_attn_decode_rope(const void* qkv, long ld_qkv, const float* cos_t,
+                                   const float* sin_t, const long* pos, void* kt, void* v,
+                                   long max_len, long B, long nkv, long rep, long hd, long L,
+                                   const void* mask, float inv_scale, void* out, long ld_o,
+                                   void* stream) {
+  const char* who = "hn_attn_decode_rope";
+  HN_ARG_CHECK(qkv != nullptr, "%s: qkv is required", who);
+  return attn_decode(who, nullptr, qkv, ld_qkv, cos_t, sin_t, pos, kt, v, max_len, B, nkv, rep,
+                     hd, L, mask, inv_scale, out, ld_o, stream);
 }

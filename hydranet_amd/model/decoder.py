@@ -190,6 +190,17 @@ class Attention(nn.Module):
             cos_t = rope.cos_cached.float().contiguous()
             sin_t = rope.sin_cached.float().contiguous()
             qkv = self._qkv(x.reshape(B * S, -1))
+            if self._decode_fits(x, S, cache, kv_len, mask) and qkv.stride(-1) == 1 \
+                    and qkv.stride(0) % 2 == 0 and qkv.data_ptr() % 4 == 0:
+                # one-token step: RoPE, the cache append and attention in one
+                # launch (hn_attn_decode_rope)
+                o = torch.empty((B, nh * hd), dtype=x.dtype, device=x.device)
+                inv = float(np.float32(1.0) / np.float32(math.sqrt(hd)))
+                _lib.call("hn_attn_decode_rope", _lib.ptr(qkv), qkv.stride(0), _lib.ptr(cos_t),
+                          _lib.ptr(sin_t), _lib.ptr(pos), _lib.ptr(cache.kt[layer]),
+                          _lib.ptr(cache.v[layer]), cache.max_len, B, nkv, rep, hd, kv_len,
+                          _lib.ptr(mask), inv, _lib.ptr(o), o.stride(0), _lib.stream(x.device))
+                return self.o_proj(o.view(B, S, nh * hd))
             wq, wk = nh * hd, nkv * hd
             qg = torch.empty((B, nkv, rep * S, hd), dtype=x.dtype, device=x.device)
             ld = qkv.stride(0)

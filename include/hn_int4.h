@@ -355,6 +355,20 @@ int hn_attn_softmax(const void* scores, long ld_s, const void* mask, long ld_m, 
 int hn_attn_decode(const void* q, const void* kt, const void* v, long max_len, long B, long nkv,
                    long rep, long hd, long L, const void* mask, float inv_scale, void* out,
                    long ld_o, void* stream);
+
+/* hn_attn_decode_rope: hn_rope_append and hn_attn_decode of a one-token step
+ *   in one launch: qkv [B][ld_qkv] fp16 holds the step's unrotated query heads
+ *   (nkv * rep * hd), keys (nkv * hd) and values (nkv * hd) — the fused q/k/v
+ *   projection — and pos [1] int64 (device) its position p; the keys and
+ *   queries are rotated with cos_t / sin_t [positions][hd] fp32 exactly as
+ *   hn_rope_append rotates them, the key and value written to kt[b][g][:][p]
+ *   and v[b][g][p][:], and attention computed over [0, L) with the new key
+ *   and value for position p.  A p outside [0, max_len) writes nothing.
+ *   Same limits as hn_attn_decode; qkv rows 4-byte aligned. */
+int hn_attn_decode_rope(const void* qkv, long ld_qkv, const float* cos_t, const float* sin_t,
+                        const long* pos, void* kt, void* v, long max_len, long B, long nkv,
+                        long rep, long hd, long L, const void* mask, float inv_scale, void* out,
+                        long ld_o, void* stream);
 int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k, const void* v, long ld_v,
                    const float* cos_t, const float* sin_t, const long* pos, long B, long S,
                    long nh, long nkv, long hd, void* q_out, void* kt, void* vc, long max_len,

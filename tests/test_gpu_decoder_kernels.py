@@ -175,6 +175,59 @@ def test_attn_decode_vs_two_products(B, nkv, rep, L, max_len, masked):
     assert bool((err <= 1e-2 + 2e-3 * ref64.abs()).all()), float(err.max())
 
 
+@pytest.mark.parametrize("B,nkv,rep,max_len,p,L,masked", [
+    (3, 2, 4, 64, 20, 21, False), (2, 8, 4, 768, 600, 640, True), (2, 2, 2, 16, 15, 16, False),
+    (1, 1, 1, 8, 0, 1, False), (64, 8, 4, 768, 513, 576, True)])
+def test_attn_decode_rope_equals_rope_append_then_attention(B, nkv, rep, max_len, p, L, masked):
+    """hn_attn_decode_rope (RoPE, cache append and attention in one launch)
+    against hn_rope_append followed by hn_attn_decode on copies of the same
+    caches: the outputs and both caches bit for bit (the new key and value
+    at position p, everything else untouched)."""
+    import math
+    hd = 128
+    nh = nkv * rep
+    print(f"[attn_decode_rope] B={B} nkv={nkv} rep={rep} max_len={max_len} p={p} L={L}",
+          flush=True)
+    g = torch.Generator(device=DEV).manual_seed(B * 7 + p)
+    qkv = torch.randn(B, (nh + 2 * nkv) * hd, generator=g, device=DEV).half()
+    kt = torch.randn(B, nkv, hd, max_len, generator=g, device=DEV).half()
+    v = torch.randn(B, nkv, max_len, hd, generator=g, device=DEV).half()
+    npos = max(max_len, 1024)
+    inv_f = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=DEV).float() / hd))
+    t = torch.arange(npos, device=DEV, dtype=torch.float32)
+    emb = torch.cat([torch.outer(t, inv_f)] * 2, dim=-1)
+    cos_t, sin_t = emb.cos().contiguous(), emb.sin().contiguous()
+    pos = torch.tensor([p], dtype=torch.int64, device=DEV)
+    mask = None
+    if masked:
+        mask = torch.zeros((1, L), dtype=torch.float16, device=DEV)
+        mask[:, p + 1:] = float("-inf")
+    inv = float(np.float32(1.0) / np.float32(math.sqrt(hd)))
+    st = _lib.stream()
+    # separate launches on copies
+    kt_a, v_a = kt.clone(), v.clone()
+    qg = torch.empty(B, nkv, rep, hd, dtype=torch.float16, device=DEV)
+    ld = qkv.stride(0)
+    base = qkv.data_ptr()
+    _lib.call("hn_rope_append", base, ld, base + 2 * nh * hd, ld, base + 2 * (nh + nkv) * hd, ld,
+              _lib.ptr(cos_t), _lib.ptr(sin_t), _lib.ptr(pos), B, 1, nh, nkv, hd, _lib.ptr(qg),
+              _lib.ptr(kt_a), _lib.ptr(v_a), max_len, st)
+    out_a = torch.empty(B, nh * hd, dtype=torch.float16, device=DEV)
+    _lib.call("hn_attn_decode", _lib.ptr(qg), _lib.ptr(kt_a), _lib.ptr(v_a), max_len, B, nkv, rep,
+              hd, L, _lib.ptr(mask), inv, _lib.ptr(out_a), out_a.stride(0), st)
+    # one launch
+    kt_b, v_b = kt.clone(), v.clone()
+    out_b = torch.full((B, nh * hd), float("nan"), dtype=torch.float16, device=DEV)
+    _lib.call("hn_attn_decode_rope", _lib.ptr(qkv), ld, _lib.ptr(cos_t), _lib.ptr(sin_t),
+              _lib.ptr(pos), _lib.ptr(kt_b), _lib.ptr(v_b), max_len, B, nkv, rep, hd, L,
+              _lib.ptr(mask), inv, _lib.ptr(out_b), out_b.stride(0), st)
+    torch.cuda.synchronize()
+    assert torch.equal(kt_a, kt_b) and torch.equal(v_a, v_b)
+    assert not torch.equal(kt_a[..., p], kt[..., p])  # the step's key was written
+    assert torch.isfinite(out_b).all()
+    assert torch.equal(out_a, out_b)
+
+
 def test_attn_decode_rejects_bad_shapes():
     for args in ((64, 1, 1, 4, 96, 8), (64, 1, 1, 3, 128, 8), (64, 1, 1, 4, 128, 1025),
                  (60, 1, 1, 4, 128, 8), (8, 1, 1, 4, 128, 9)):
