@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
     "hn_add_rmsnorm_router": [P, L, P, L, P, L, P, P, L, L, L, F, P, L, L, P, P],
     "hn_attn_softmax": [P, L, P, L, L, L, L, F, P, L, P],
     "hn_attn_decode": [P, P, P, L, L, L, L, L, L, P, F, P, L, P],
+    "hn_unpermute_add_rmsnorm": [P, L, L, P, P, P, L, L, P, L, P, L, P, P, L, L, F, P],
+    "hn_moe_decode_layer_partials": [L, L, L, L, L],
     "hn_attn_decode_rope": [P, L, P, P, P, P, P, L, L, L, L, L, L, P, F, P, L, P],
     "hn_rope_append": [P, L, P, L, P, L, P, P, P, L, L, L, L, L, P, P, P, L, P],
     "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],
@@ -68,7 +70,8 @@ SIGNATURES: dict[str, list] = {
 ROUTE_MAX_LOGITS = 8192   # T * E
 ROUTE_MAX_ASSIGN = 1024   # T * k
 
-RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long, "hn_gemm_workspace_bytes": ctypes.c_long}
+RESTYPES = {"hn_skinny_workspace_bytes": ctypes.c_long, "hn_gemm_workspace_bytes": ctypes.c_long,
+            "hn_moe_decode_layer_partials": ctypes.c_long}
 
 # Tokens per weight matrix up to which the decode (skinny / streaming) kernels
 # run; above it the MFMA GEMM kernels do (kMaxRows in csrc/hn_gemv.hip).

@@ -15,6 +15,7 @@
 // RMSNorm outputs can differ from the torch formulation by an fp16 ulp;
 // add and RoPE are exact replicas.
 #include "hn_common.h"
+#include "hn_unpermute.h"
 
 namespace {
 
@@ -28,15 +29,33 @@ constexpr int kMaxGate = 16;  // router experts the norm kernel can score
 // the waves in order) stored as fp32 -- the fp16 Linear of TopKRouter
 // (model/router.py:102) on this row.  Every expert's gate loads of a thread
 // go out together and the E wave reductions are interleaved.
-template <int LG>
+// UNP: the residual res is the row's MoE output, computed here from the
+// down projection's four fp32 K-slice partials and the routing (the ordered
+// weighted sum of moe_unpermute_kernel<4>, unp_select / unp_cols), instead of
+// read: the MoE block's last launch and the next RMSNorm in one.
+struct UnpSrc {
+  const float* part;  // [4][rows][ld_y] fp32
+  long ks_stride;     // floats between slices
+  long ld_y;
+  const int* inv;
+  const int* idx;
+  const h16* w;
+  int k;
+};
+
+template <int LG, bool UNP = false>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     const h16* __restrict__ x, long ld_x, const h16* __restrict__ res, long ld_r,
     h16* __restrict__ x_out, long ld_xo, const h16* __restrict__ w, h16* __restrict__ out,
     long ld_o, int H, float eps, const h16* __restrict__ gate, long ld_g, int E,
-    float* __restrict__ logits) {
+    float* __restrict__ logits, UnpSrc U) {
   __shared__ float s_part[kNormThreads / 64];
   __shared__ float s_lg[kNormThreads / 64][kMaxGate];
   const int row = blockIdx.x, tid = threadIdx.x;
+  int upos[kMaxTopK];
+  float uwt[kMaxTopK];
+  int un = 0;
+  if constexpr (UNP) un = unp_select(row, U.inv, U.idx, U.w, U.k, upos, uwt);
   const half8_t* xr = reinterpret_cast<const half8_t*>(x + (long)row * ld_x);
   const half8_t* rr = res ? reinterpret_cast<const half8_t*>(res + (long)row * ld_r) : nullptr;
   half8_t* xo = x_out ? reinterpret_cast<half8_t*>(x_out + (long)row * ld_xo) : nullptr;
@@ -49,8 +68,12 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     const int j = tid + i * kNormThreads;
     if (j < nv) {
       half8_t a = xr[j];
-      if (rr) {
-        const half8_t b = rr[j];
+      if (UNP || rr) {
+        half8_t b;
+        if constexpr (UNP)
+          b = unp_cols<4>(nullptr, U.part, U.ks_stride, U.ld_y, upos, uwt, un, 8 * j);
+        else
+          b = rr[j];
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = (h16)((float)a[e] + (float)b[e]);
         if (xo) xo[j] = a;
@@ -630,7 +653,7 @@ extern "C" int hn_add_rmsnorm(const void* x, long ld_x, const void* res, long ld
   hipLaunchKernelGGL(add_rmsnorm_kernel<0>, dim3((unsigned)T), dim3(kNormThreads), 0,
                      (hipStream_t)stream, (const h16*)x, ld_x, (const h16*)res, ld_r,
                      (h16*)x_out, ld_xo, (const h16*)w, (h16*)out, ld_o, (int)H, eps,
-                     (const h16*)nullptr, 0L, 0, (float*)nullptr);
+                     (const h16*)nullptr, 0L, 0, (float*)nullptr, UnpSrc{});
   HN_LAUNCH_CHECK("hn_add_rmsnorm");
   return 0;
 }
@@ -655,8 +678,34 @@ extern "C" int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, 
   hipLaunchKernelGGL(kern, dim3((unsigned)T), dim3(kNormThreads), 0, (hipStream_t)stream,
                      (const h16*)x, ld_x, (const h16*)res, ld_r, (h16*)x_out, ld_xo,
                      (const h16*)w, (h16*)out, ld_o, (int)H, eps, (const h16*)gate, ld_g, (int)E,
-                     logits);
+                     logits, UnpSrc{});
   HN_LAUNCH_CHECK("hn_add_rmsnorm_router");
+  return 0;
+}
+
+// The MoE block's ordered unpermute (from the four fp32 K-slice partials of
+// the down projection) + residual add + RMSNorm of the next block, one
+// launch.  See include/hn_int4.h.
+extern "C" int hn_unpermute_add_rmsnorm(const float* part, long ks_stride, long ld_y,
+                                        const int* inv, const int* idx, const void* rw, long T,
+                                        long k, const void* x, long ld_x, void* x_out,
+                                        long ld_xo, const void* w, void* out, long ld_o, long H,
+                                        float eps, void* stream) {
+  const char* who = "hn_unpermute_add_rmsnorm";
+  HN_ARG_CHECK(T >= 0 && H > 0 && H % 8 == 0 && H <= 8 * kNormThreads * 4,
+               "%s: need 0 < H <= %d, H %% 8 == 0", who, 8 * kNormThreads * 4);
+  HN_ARG_CHECK(k > 0 && k <= kMaxTopK, "%s: k must be in (0, %d]", who, kMaxTopK);
+  HN_ARG_CHECK(al16(part) && ld_y % 4 == 0 && ks_stride % 4 == 0 && al16(x) && ld_x % 8 == 0 &&
+                   al16(x_out) && ld_xo % 8 == 0 && al16(w) && al16(out) && ld_o % 8 == 0 &&
+                   part && inv && idx && rw && x_out,
+               "%s: partials, rows and weights must be 16-byte aligned (x_out given)", who);
+  if (T == 0) return 0;
+  const UnpSrc U = {part, ks_stride, ld_y, inv, idx, (const h16*)rw, (int)k};
+  hipLaunchKernelGGL((add_rmsnorm_kernel<0, true>), dim3((unsigned)T), dim3(kNormThreads), 0,
+                     (hipStream_t)stream, (const h16*)x, ld_x, (const h16*)nullptr, 0L,
+                     (h16*)x_out, ld_xo, (const h16*)w, (h16*)out, ld_o, (int)H, eps,
+                     (const h16*)nullptr, 0L, 0, (float*)nullptr, U);
+  HN_LAUNCH_CHECK(who);
   return 0;
 }
 

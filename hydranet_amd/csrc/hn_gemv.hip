@@ -1011,6 +1011,16 @@ extern "C" int hn_moe_decode_layer_check(long T, long E, long k, long H, long I,
 // streaming kernel, the down projection in four K slices, the ordered
 // weighted unpermute.  Same results as hn_moe_route followed by
 // hn_moe_experts_decode.
+// Byte offset in hn_moe_decode_layer's workspace of the down projection's
+// four fp32 K-slice partials [4][T k][H] (slice stride T k H floats).
+extern "C" long hn_moe_decode_layer_partials(long T, long E, long k, long H, long I) {
+  (void)T;
+  (void)k;
+  const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
+                                                            : hn_cdiv(H, kTileN);
+  return (long)ctr_bytes(E * tmax);
+}
+
 extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
                                    const float* logits_in, long T, long E, long k,
                                    const void* table, long H, long I, long group, float eps,
@@ -1020,7 +1030,7 @@ extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w,
                                    long work_bytes, void* stream) {
   const char* who = "hn_moe_decode_layer";
   HN_ARG_CHECK(aligned16(h) && (logits_in || aligned16(gate_w)) && aligned16(h_ws) &&
-                   aligned16(out) && ld_o % 8 == 0,
+                   aligned16(out) && (!out || ld_o % 8 == 0),
                "%s: h, gate, h_ws and out rows must be 16-byte aligned", who);
   HN_ARG_CHECK(g_decode_path == 0, "%s: needs the streaming kernels (decode path 0)", who);
   hipStream_t s = (hipStream_t)stream;
@@ -1046,7 +1056,9 @@ extern "C" int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w,
   if (rc == 0)
     rc = hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, T, rows, H, I,
                                    group, part, s, 0);
-  if (rc == 0)
+  // out NULL: the caller does the unpermute from the partials
+  // (hn_moe_decode_layer_partials; e.g. hn_unpermute_add_rmsnorm)
+  if (rc == 0 && out)
     rc = hn_moe_unpermute_split4_impl(part, rows * H, inv, idx, w, T, k, nullptr, H, out, ld_o,
                                       H, stream);
   if (rc == HN_NOT_HANDLED) {

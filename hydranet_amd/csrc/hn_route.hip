@@ -24,6 +24,7 @@
 //                      addend as in GLM4MoELayer (model/glm4.py:473).
 #include "hn_common.h"
 #include "hn_topk.h"
+#include "hn_unpermute.h"
 
 #include <algorithm>
 
@@ -229,11 +230,12 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const h16* __restrict__
 
 // Workgroup (token, column block): each thread owns 8 consecutive columns
 // per pass (blockDim.x * 8 columns per block and pass, gridDim.y blocks
-// interleaved over H).  KS = 0:
-// y is fp16 [rows, ld_y]; KS > 0: y is given as KS fp32 partial sums
+// interleaved over H); the sum is unp_select / unp_cols (hn_unpermute.h).
+// KS = 0: y is fp16 [rows, ld_y]; KS > 0: y is given as KS fp32 partial sums
 // part[j * ks_stride + row * ld_y] (a K-split down projection), added in
 // slice order and rounded to fp16 once: the expert output the unsplit kernel
-// would write, up to fp32 summation order.
+// would write, up to fp32 summation order.  A shared expert's row, when
+// given, is added last: out = fp16(shared + acc).
 template <int KS>
 __global__ __launch_bounds__(256) void moe_unpermute_kernel(
     const h16* __restrict__ y, const float* __restrict__ part, long ks_stride, long ld_y,
@@ -241,88 +243,14 @@ __global__ __launch_bounds__(256) void moe_unpermute_kernel(
     const h16* __restrict__ shared, long ld_sh, h16* __restrict__ out, long ld_o, int H) {
   const int t = blockIdx.x;
   int pos[kMaxTopK];
-  int ex[kMaxTopK];
   float wt[kMaxTopK];
-  // the token's k (position, expert, weight) loaded together (one memory
-  // round trip, not one per assignment), then ordered by expert.  The loads
-  // are unconditional (index clamped to k - 1): a load under `if (s < k)`
-  // ends its own block, and the compiler then waits for each in turn.
-  int pv[kMaxTopK], ev[kMaxTopK];
-  h16 wv[kMaxTopK];
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    const int j = t * k + (s < k ? s : k - 1);
-    pv[s] = inv[j];
-    ev[s] = idx[j];
-    wv[s] = w[j];
-  }
-  int n = 0;
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    if (s >= k) break;
-    const int p = pv[s];
-    if (p < 0) continue;
-    const int e = ev[s];
-    // insertion by expert id (ascending): the reference visits experts in
-    // unique() order and accumulates into an fp16 buffer
-    int q = n;
-    while (q > 0 && ex[q - 1] > e) {
-      ex[q] = ex[q - 1];
-      pos[q] = pos[q - 1];
-      wt[q] = wt[q - 1];
-      --q;
-    }
-    ex[q] = e;
-    pos[q] = p;
-    wt[q] = (float)wv[s];
-    ++n;
-  }
-  // the rows of a batch of B selected experts are loaded before any is used
-  // (independent loads in flight together), then added in expert order
-  constexpr int B = KS == 0 ? 8 : 2;
+  const int n = unp_select(t, inv, idx, w, k, pos, wt);
   for (int c = (blockIdx.y * blockDim.x + threadIdx.x) * 8; c < H;
        c += gridDim.y * blockDim.x * 8) {
-    half8_t acc = {0, 0, 0, 0, 0, 0, 0, 0};
     // the shared expert's row is loaded with the first batch of rows
     half8_t sv = {0, 0, 0, 0, 0, 0, 0, 0};
     if (shared) sv = *reinterpret_cast<const half8_t*>(shared + (long)t * ld_sh + c);
-    for (int s0 = 0; s0 < n; s0 += B) {
-      half8_t v[B];
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const int s = s0 + u < n ? s0 + u : n - 1;
-        if constexpr (KS == 0) {
-          v[u] = *reinterpret_cast<const half8_t*>(y + (long)pos[s] * ld_y + c);
-        } else {
-          float f[8];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) f[q] = 0.f;
-#pragma unroll
-          for (int j = 0; j < KS; ++j) {
-            const float* pp = part + j * ks_stride + (long)pos[s] * ld_y + c;
-            const float4_t a = *reinterpret_cast<const float4_t*>(pp);
-            const float4_t b = *reinterpret_cast<const float4_t*>(pp + 4);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              f[q] += a[q];
-              f[4 + q] += b[q];
-            }
-          }
-#pragma unroll
-          for (int q = 0; q < 8; ++q) v[u][q] = (h16)f[q];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        if (s0 + u >= n) break;
-        const float ws = wt[s0 + u];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const h16 prod = (h16)((float)v[u][j] * ws);
-          acc[j] = (h16)((float)acc[j] + (float)prod);
-        }
-      }
-    }
+    half8_t acc = unp_cols<KS>(y, part, ks_stride, ld_y, pos, wt, n, c);
     if (shared) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = (h16)((float)sv[j] + (float)acc[j]);

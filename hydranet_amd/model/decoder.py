@@ -319,23 +319,30 @@ class DecoderBlock(nn.Module):
         self.moe = MixtralMoELayer(cfg.hidden_dim, cfg.num_experts, cfg.experts_per_token,
                                    layer_idx=layer_idx, slots=slots)
 
-    def forward(self, x, rope, pos, cache: KVCache, kv_len: int, mask, top_k: int,
-                pending: Optional[torch.Tensor] = None):
-        """x + attn(norm(x)), then + moe(norm(.)) (model/mixtral.py:407-427).
-        Returns (x after the attention residual, the MoE output still to be
-        added): the caller folds that add into the next RMSNorm.  pending: the
-        previous block's MoE output, added to x first."""
-        x, h = add_rmsnorm(x, pending, self.input_layernorm)
+    def forward(self, x, h, rope, pos, cache: KVCache, kv_len: int, mask, top_k: int,
+                next_norm: "RMSNorm", fold: bool = True):
+        """x + attn(h), then + moe(norm(.)) (model/mixtral.py:407-427), h =
+        input_layernorm(x) given by the caller.  Returns (x after both
+        residual adds, next_norm of it): the next block's input and its
+        normalised rows.  fold: the MoE output's residual add and next_norm
+        run inside the MoE block's last launch where it allows
+        (forward_folded), else as one more launch."""
         a = self.self_attn(h, rope, pos, cache, self.layer_idx, kv_len, mask)
         T = h.shape[0] * h.shape[1]
         gw = self.moe.router.gate.weight
+        lg = None
         if x.is_cuda and gw.dtype == torch.float16 and self.moe.takes_logits(T, top_k):
             # the router logits come out of the norm kernel (no gate product
             # in the routing launch)
             x, h, lg = add_rmsnorm(x, a, self.post_attention_layernorm, gate=gw)
-            return x, self.moe(h, top_k=top_k, logits=lg)
-        x, h = add_rmsnorm(x, a, self.post_attention_layernorm)
-        return x, self.moe(h, top_k=top_k)
+        else:
+            x, h = add_rmsnorm(x, a, self.post_attention_layernorm)
+        if fold:
+            r = self.moe.forward_folded(h, top_k, lg, x, next_norm.weight, next_norm.eps)
+            if r is not None:
+                return r
+        m = self.moe(h, top_k=top_k, logits=lg) if lg is not None else self.moe(h, top_k=top_k)
+        return add_rmsnorm(x, m, next_norm)
 
 
 class MixtralDecoder(nn.Module):
@@ -348,6 +355,9 @@ class MixtralDecoder(nn.Module):
         super().__init__()
         self.cfg = cfg
         self.decode_top_k = decode_top_k
+        # the MoE block's residual add and the next RMSNorm inside its last
+        # launch (hn_unpermute_add_rmsnorm) where the decode layer allows
+        self.fold_moe_norm = True
         self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_dim)
         self.layers = nn.ModuleList([DecoderBlock(cfg, i, slots[i])
                                      for i in range(cfg.num_layers)])
@@ -367,10 +377,12 @@ class MixtralDecoder(nn.Module):
         [S] (device int64), attention over the first kv_len cache positions.
         Does not move cache.cur_len."""
         x = self.embed_tokens(input_ids)
-        pending = None
-        for blk in self.layers:
-            x, pending = blk(x, self.rotary, pos, cache, kv_len, mask, top_k, pending)
-        _, h = add_rmsnorm(x, pending, self.norm)
+        x, h = add_rmsnorm(x, None, self.layers[0].input_layernorm)
+        n = len(self.layers)
+        for i, blk in enumerate(self.layers):
+            nxt = self.layers[i + 1].input_layernorm if i + 1 < n else self.norm
+            x, h = blk(x, h, self.rotary, pos, cache, kv_len, mask, top_k, nxt,
+                       fold=self.fold_moe_norm)
         return self.lm_head(h)
 
     @torch.no_grad()

@@ -226,13 +226,15 @@ def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torc
 
 def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: "ExpertTable",
                      want_logits: bool = False, logits: Optional[torch.Tensor] = None,
-                     usage: Optional[torch.Tensor] = None):
+                     usage: Optional[torch.Tensor] = None, fold=None):
     """One Mixtral MoE layer at decode in three launches (hn_moe_decode_layer):
     softmax top-k and the stable permutation computed in the gate/up kernel
     (with the fp16 gate logits, unless ``logits`` [T, E] are given), the down
     projection, the ordered weighted unpermute.  Returns (out [T, H] fp16,
     Routed) with the same routing outputs as moe_route (x_perm is not
-    written)."""
+    written).  fold = (x [T, H] fp16, norm weight [H] fp16, eps): the
+    unpermute also adds the residual stream x and applies the next RMSNorm
+    (hn_unpermute_add_rmsnorm); out is then (x + moe, RMSNorm(x + moe))."""
     T, H = hidden.shape
     _lib.require_gpu(hidden)
     dev = hidden.device
@@ -251,7 +253,7 @@ def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: 
         r.logits = torch.empty((T, E), dtype=torch.float32, device=dev)
     n = T * k
     h_ws = torch.empty((n, I), dtype=torch.float16, device=dev)
-    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    out = torch.empty((T, H), dtype=torch.float16, device=dev) if fold is None else None
     work = _lib.skinny_workspace(3, n, H, I, E, dev)
     _lib.call("hn_moe_decode_layer", _lib.ptr(x), x.stride(0), _lib.ptr(ww), ww.stride(0),
               _lib.ptr(lg_in), T, E, k, _lib.ptr(table.dev), H, I, g, 1e-9, 1.0,
@@ -260,7 +262,17 @@ def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: 
               _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(_usage_ptr(usage, E, dev)),
               _lib.ptr(h_ws), _lib.ptr(out), H,
               _lib.ptr(work), work.numel(), _lib.stream(dev))
-    return out, r
+    if fold is None:
+        return out, r
+    xr, nw, eps = fold
+    xr = _lib.aligned_rows(xr.reshape(T, H))
+    x_out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    h_out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    part = work.data_ptr() + _lib.lib().hn_moe_decode_layer_partials(T, E, k, H, I)
+    _lib.call("hn_unpermute_add_rmsnorm", part, n * H, H, _lib.ptr(r.inv), _lib.ptr(r.idx),
+              _lib.ptr(r.w), T, k, _lib.ptr(xr), xr.stride(0), _lib.ptr(x_out), H,
+              _lib.ptr(nw), _lib.ptr(h_out), H, H, float(eps), _lib.stream(dev))
+    return (x_out, h_out), r
 
 
 def moe_dispatch(r: Routed, table: ExpertTable,
@@ -474,6 +486,34 @@ class MixtralMoELayer(nn.Module):
         out = moe_experts_forward(flat, idx, w, table)
         self.last_routing = (idx, w)
         return out.view(B, S, H)
+
+    def forward_folded(self, hidden_states: torch.Tensor, top_k: int,
+                       logits: Optional[torch.Tensor], x: torch.Tensor, norm_weight: torch.Tensor,
+                       eps: float):
+        """The decode layer with the next RMSNorm folded into its last launch:
+        returns (x + moe(hidden_states), RMSNorm(x + moe) * norm_weight) [B,
+        S, H], bit-identical to forward() followed by the residual add and
+        RMSNorm, or None where the folded launch does not apply (the caller
+        then runs those two steps)."""
+        B, S, H = hidden_states.shape
+        T = B * S
+        rt = self.router
+        if not (hidden_states.is_cuda and route_fits(T, self.num_experts, top_k)):
+            return None
+        if rt.enable_affinity_bonus and rt._is_cached_fn is not None:
+            return None
+        table = self.experts.static_table(hidden_states.device)
+        if table is None or not decode_layer_fits(T, self.num_experts, top_k, table,
+                                                   rt.gate.weight, logits is not None):
+            return None
+        if norm_weight.dtype != torch.float16 or x.dtype != torch.float16:
+            return None
+        usage = None if rt.training else rt.usage_counts
+        (x_out, h_out), r = moe_decode_layer(hidden_states.reshape(T, H), rt.gate.weight, top_k,
+                                             table, logits=logits, usage=usage,
+                                             fold=(x, norm_weight, eps))
+        self.last_routing = (r.idx, r.w)
+        return x_out.view(B, S, H), h_out.view(B, S, H)
 
 
 _SIDE_STREAMS: dict = {}

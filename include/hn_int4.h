@@ -218,15 +218,22 @@ int hn_moe_decode_layer_check(long T, long E, long k, long H, long I, long group
  * hn_moe_route + hn_moe_experts_decode; the routing outputs (logits_out may be
  * NULL, idx, w, offsets [E + 1], perm, inv, active, n_active, usage) are
  * written as hn_moe_route writes them.  h_ws [T k, I] fp16; work:
- * hn_skinny_workspace_bytes(3, T k, H, I, E).  Replaces
- * MixtralMoELayer.forward's router call, per-expert loop and index_add_
- * (model/mixtral.py:283-368) at decode sizes. */
+ * hn_skinny_workspace_bytes(3, T k, H, I, E).  out NULL: no unpermute; the
+ * down projection's four fp32 K-slice partials stay in work at byte
+ * hn_moe_decode_layer_partials(T, E, k, H, I) for the caller (e.g.
+ * hn_unpermute_add_rmsnorm).  Replaces MixtralMoELayer.forward's router
+ * call, per-expert loop and index_add_ (model/mixtral.py:283-368) at decode
+ * sizes. */
 int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
                         const float* logits_in, long T, long E, long k, const void* table,
                         long H, long I, long group, float eps, float scaling, void* logits_out,
                         int* idx, void* w, int* offsets, int* perm, int* inv, int* active,
                         int* n_active, long long* usage, void* h_ws, void* out, long ld_o,
                         void* work, long work_bytes, void* stream);
+
+/* Byte offset in hn_moe_decode_layer's workspace of its down projection's
+ * four fp32 K-slice partials [4][T k][H] (slice stride T k H floats). */
+long hn_moe_decode_layer_partials(long T, long E, long k, long H, long I);
 
 /* 0 when hn_moe_route_experts_decode covers (T, E, k, mode, H, I, group) with
  * the current decode kernel family, else a nonzero code (no message set). */
@@ -330,6 +337,18 @@ int hn_add_rmsnorm_router(const void* x, long ld_x, const void* res, long ld_r, 
                           long ld_xo, const void* w, void* out, long ld_o, long T, long H,
                           float eps, const void* gate, long ld_g, long E, float* logits,
                           void* stream);
+/* hn_unpermute_add_rmsnorm: the MoE block's ordered weighted unpermute and
+ *   the next block's residual add + RMSNorm in one launch, per token row t:
+ *   m = the unpermute of hn_moe_unpermute from four fp32 K-slice partials
+ *   part[j * ks_stride + p * ld_y] (fp32 sum in slice order, one fp16
+ *   rounding; routing inv / idx / w [T k] as hn_moe_route writes them);
+ *   x_out[t] = fp16(x[t] + m); out[t] = RMSNorm(x_out[t]) * w as
+ *   hn_add_rmsnorm.  Bit-identical to hn_moe_unpermute's KS = 4 form followed
+ *   by hn_add_rmsnorm (model/mixtral.py:365-368 then 407-427). */
+int hn_unpermute_add_rmsnorm(const float* part, long ks_stride, long ld_y, const int* inv,
+                             const int* idx, const void* rw, long T, long k, const void* x,
+                             long ld_x, void* x_out, long ld_xo, const void* w, void* out,
+                             long ld_o, long H, float eps, void* stream);
 /* hn_attn_softmax: attention probabilities from fp16 scores [rows, L] (row
  *   stride ld_s, 1 <= L <= 1024): a = fp16(s * inv_scale), a = fp16(a +
  *   mask[row % mask_rows]) when mask [mask_rows, L] fp16 (0 / -inf) is given,

@@ -83,10 +83,14 @@ def test_c5_moe_blocks_match_oracle_dispatch(c5, top_k):
         return fn
 
     hs = [model.layers[li].moe.register_forward_hook(hook(li)) for li in picked]
+    # the MoE blocks' own forward (the folded launch, which the last test
+    # compares with it, does not run the module's hooks)
+    model.fold_moe_norm = False
     try:
         print(f"[c5] decode step, top-{top_k}", flush=True)
         model(tok, cache, top_k=top_k)
     finally:
+        model.fold_moe_norm = True
         for h in hs:
             h.remove()
     for li in picked:
@@ -96,3 +100,26 @@ def test_c5_moe_blocks_match_oracle_dispatch(c5, top_k):
                    enumerate(model.layers[li].moe.experts.table.slots)}
         ref = torch_ref.moe_dispatch(x.cpu(), idx.long().cpu(), w.cpu(), experts, 128)
         _close(y.cpu(), ref, 1e-2, 2e-3, f"layer {li} top-{top_k}")
+
+
+@pytest.mark.parametrize("top_k", [1, 2])
+def test_c5_folded_moe_norm_is_bit_identical(c5, top_k):
+    """A decode step with the MoE block's residual add and the next RMSNorm
+    inside its last launch (hn_unpermute_add_rmsnorm) gives the same logits,
+    bit for bit, as the step with the unpermute and the norm as two
+    launches; at top-2 (no folded launch for 128 routed rows) the two paths
+    are the same code."""
+    cfg, model, ids = c5
+    cache = model.new_cache(B, P + 2)
+    tok = model(ids[:, :P], cache)[:, -1].argmax(-1, keepdim=True)
+    pos = torch.full((1,), cache.cur_len, dtype=torch.int64, device=DEV)
+    print(f"[c5] folded vs unfolded decode step, top-{top_k}", flush=True)
+    with torch.no_grad():
+        model.fold_moe_norm = True
+        a = model.step(tok, pos, cache, cache.cur_len + 1, None, top_k)
+        model.fold_moe_norm = False
+        b = model.step(tok, pos, cache, cache.cur_len + 1, None, top_k)
+        model.fold_moe_norm = True
+    torch.cuda.synchronize()
+    assert torch.isfinite(a).all()
+    assert torch.equal(a, b)
