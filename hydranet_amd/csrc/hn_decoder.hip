@@ -313,9 +313,9 @@ __global__ __launch_bounds__(1024) void attn_decode_kernel(
     const float* __restrict__ sin_t, const long* __restrict__ pos) {
   constexpr int HD = kAttnHd;
   constexpr int NV = LMAX / 64;  // value positions per thread
-  // LDS arrays are read with the types they are written with: a vector
-  // load of query pairs written as scalars let the compiler keep only its
-  // first element (all query heads got head 0's scores)
+  // the query pairs are read as four scalars: read as one 16-byte vector
+  // and split by element extracts into v_dot2, the compiler fed element 0
+  // to every head's dot products (all heads got head 0's scores)
   __shared__ uint32_t s_q2[HD / 2][4];  // [i][r] = (q[r][2 i], q[r][2 i + 1])
   // scaled scores, then probabilities, [l][r]; 1024 rows whatever LMAX, so
   // every lane's position (8 pg + ds < 1024) has a row and the store after
