@@ -232,3 +232,10 @@ __device__ __forceinline__ void hn_counter_reset(unsigned long long* c) {
 }
 // Arrivals per counter are below 2^16.
 constexpr long kHnMaxArrivals = 0xffff;
+
+// K slices of the grouped decode's down projection.  Its fp32 partials are
+// part[j][rows][H], j < kHnDownSplit, in the caller's workspace: the stream
+// kernel's instantiation, the workspace size and both unpermutes that sum
+// the slices take the count from here, so they cannot disagree (a kernel
+// writing more slices than the workspace holds writes past its end).
+constexpr int kHnDownSplit = 4;

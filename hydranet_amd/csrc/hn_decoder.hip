@@ -34,7 +34,7 @@ constexpr int kMaxGate = 16;  // router experts the norm kernel can score
 // weighted sum of moe_unpermute_kernel<4>, unp_select / unp_cols), instead of
 // read: the MoE block's last launch and the next RMSNorm in one.
 struct UnpSrc {
-  const float* part;  // [4][rows][ld_y] fp32
+  const float* part;  // [kHnDownSplit][rows][ld_y] fp32
   long ks_stride;     // floats between slices
   long ld_y;
   const int* inv;
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
       if (UNP || rr) {
         half8_t b;
         if constexpr (UNP)
-          b = unp_cols<4>(nullptr, U.part, U.ks_stride, U.ld_y, upos, uwt, un, 8 * j);
+          b = unp_cols<kHnDownSplit>(nullptr, U.part, U.ks_stride, U.ld_y, upos, uwt, un, 8 * j);
         else
           b = rr[j];
 #pragma unroll

@@ -567,8 +567,8 @@ extern "C" long hn_skinny_workspace_bytes(int kind, long M, long N, long K, long
   const size_t a = part_bytes(pg.ks, 2, prow, I);
   const size_t b = part_bytes(pd.ks, 1, prow, H);
   size_t m = a > b ? a : b;
-  if (kind == 3) {  // hn_moe_experts_decode: 4 fp32 K-slice partials of the down projection
-    const size_t c = (size_t)4 * prow * H * 4;
+  if (kind == 3) {  // hn_moe_experts_decode: fp32 K-slice partials of the down projection
+    const size_t c = (size_t)kHnDownSplit * prow * H * 4;
     m = m > c ? m : c;
   }
   return (long)(ctr_bytes(ctr) + m);
@@ -1012,7 +1012,8 @@ extern "C" int hn_moe_decode_layer_check(long T, long E, long k, long H, long I,
 // weighted unpermute.  Same results as hn_moe_route followed by
 // hn_moe_experts_decode.
 // Byte offset in hn_moe_decode_layer's workspace of the down projection's
-// four fp32 K-slice partials [4][T k][H] (slice stride T k H floats).
+// kHnDownSplit fp32 K-slice partials [kHnDownSplit][T k][H] (slice stride T k H
+// floats).
 extern "C" long hn_moe_decode_layer_partials(long T, long E, long k, long H, long I) {
   (void)T;
   (void)k;

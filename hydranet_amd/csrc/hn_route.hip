@@ -655,8 +655,8 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
   return 0;
 }
 
-// Unpermute from 4 fp32 K-slice partials of the down projection
-// (hn_stream_down_split_impl): part[j * ks_stride + row * H], j < 4.
+// Unpermute from the kHnDownSplit = 4 fp32 K-slice partials of the down
+// projection (hn_stream_down_split_impl): part[j * ks_stride + row * H], j < 4.
 extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, const int* inv,
                                             const int* idx, const void* w, long T, long k,
                                             const void* shared, long ld_sh, void* out,
@@ -666,8 +666,8 @@ extern "C" int hn_moe_unpermute_split4_impl(const float* part, long ks_stride, c
                    (!shared || (al16(shared) && ld_sh % 8 == 0)),
                "hn_moe_unpermute: rows must be 16-byte aligned");
   if (T <= 0) return 0;
-  hipLaunchKernelGGL(moe_unpermute_kernel<4>, dim3((unsigned)T, unpermute_blocks(H, T)),
-                     dim3(unpermute_threads(T)), 0,
+  hipLaunchKernelGGL(moe_unpermute_kernel<kHnDownSplit>,
+                     dim3((unsigned)T, unpermute_blocks(H, T)), dim3(unpermute_threads(T)), 0,
                      (hipStream_t)stream, (const h16*)nullptr, part, ks_stride, H, inv, idx,
                      (const h16*)w, (int)k, (const h16*)shared, ld_sh, (h16*)out, ld_o, (int)H);
   HN_LAUNCH_CHECK("hn_moe_unpermute");

@@ -824,7 +824,7 @@ int launch_stream(const StreamArgs& A, const GroupedPtrs& g, const StreamPlan& p
 
 // Down projection in kDownSplit K slices: one slice of I = 14336 is 28
 // groups, 7 waves x 4 groups with three column buffers.
-constexpr int kDownSplit = 4;
+constexpr int kDownSplit = kHnDownSplit;
 
 // 16-token chunks for a grouped launch when its rows average 5 or more per
 // expert (e.g. 64 decode tokens at top-1 over 8 experts): an expert's rows
