@@ -643,6 +643,35 @@ def c1phase(args):
                       + T * I * 2 + T * H * 2, "copy_bytes": src.numel() * 2}), flush=True)
 
 
+def bench_copy(args):
+    """Reference rates for the 8 TB/s peak: torch's own device copy (read +
+    write) and fp32 sum (read) of 1 and 4 GiB fp16 tensors, best of 10 by HIP
+    events on the current stream."""
+    out = {}
+    for gib in (1, 4):
+        n = gib * (1 << 30) // 2
+        a = torch.randn(n, dtype=torch.float16, device="cuda")
+        b = torch.empty_like(a)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for name, fn, nbytes in (("copy", lambda: b.copy_(a), 4 * n),
+                                 ("sum", lambda: a.sum(dtype=torch.float32), 2 * n)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            best = float("inf")
+            for _ in range(10):
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                best = min(best, e0.elapsed_time(e1))
+            out[f"{name}_{gib}GiB"] = {"us": round(best * 1e3, 1),
+                                       "GB_s": round(nbytes / best / 1e6, 1)}
+        del a, b
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_h2d(args):
     """Expert-miss path of the residency layer, one Mixtral expert = one 90.8 MB
     blob (a18): (1) pinned staging -> HBM, GpuExpertSlot.load_from_pinned on a
@@ -895,12 +924,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3", "c4", "c5", "c1phase", "c2phase", "c4phase",
-                             "h2d"],
+                             "h2d", "copy"],
                     help="c2phase: only the C2 T=16 routing + gate/up kernel and a 512 MiB copy "
                          "(the two kernels whose rocprofv3 counters give roofline.traffic); "
                          "c4phase: only the C4 grouped GEMM launches (MFMA counters); "
                          "h2d: the expert-miss load path (pinned -> HBM, and from a store "
-                         "on disk)")
+                         "on disk); copy: torch's device copy and sum rates (HBM reference)")
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--shared-side-stream", type=int, default=None, choices=[0, 1],
                     help="c3: the shared expert on a second stream (1) or first on the "
@@ -953,6 +982,14 @@ def main():
         print(json.dumps({"metric": "expert H2D load GB/s (residency miss path, 1 GPU)",
                           "value": r["GB_s"], "unit": "GB/s", "n_gpus": 1,
                           "higher_is_better": True, "dtype": "u8", "data": "synthetic",
+                          "config": r}), flush=True)
+        return
+    if args.workload == "copy":
+        r = bench_copy(args)
+        _log("copy", r)
+        print(json.dumps({"metric": "torch device copy GB/s (read + write, HBM reference, 1 GPU)",
+                          "value": r["copy_4GiB"]["GB_s"], "unit": "GB/s", "n_gpus": 1,
+                          "higher_is_better": True, "dtype": "fp16", "data": "synthetic",
                           "config": r}), flush=True)
         return
     if args.workload == "c3":

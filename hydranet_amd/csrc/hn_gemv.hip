@@ -916,11 +916,28 @@ extern "C" int hn_grouped_expert_phase_int4(int phase, const void* x_perm, const
   return rc;
 }
 
+// Whether hn_moe_experts_decode takes the streaming path with the K-split down
+// projection for these sizes (the launches' own dry runs).
+static bool experts_split_ok(long E, long max_rows, long rows, long H, long I, long group) {
+  return rows > 0 && max_rows > 0 && stream_rows_ok(max_rows, rows, E) && g_decode_path == 0 &&
+         group % 128 == 0 && H % 128 == 0 && I % 128 == 0 &&
+         hn_stream_grouped_impl(0, nullptr, H, nullptr, nullptr, nullptr, nullptr, E, max_rows,
+                                rows, H, I, group, nullptr, I, nullptr, 1) == 0 &&
+         hn_stream_down_split_impl(nullptr, nullptr, nullptr, nullptr, nullptr, E, max_rows,
+                                   rows, H, I, group, nullptr, nullptr, 1) == 0;
+}
+
+extern "C" int hn_moe_experts_decode_split_check(long E, long max_rows_per_expert, long rows,
+                                                 long H, long I, long group) {
+  return experts_split_ok(E, max_rows_per_expert, rows, H, I, group) ? 0 : 1;
+}
+
 // The experts half of a decode MoE layer: grouped SwiGLU over the routed rows
 // and the ordered, weighted sum back per token.  Where the streaming kernels
 // apply, the down projection runs in four K slices whose fp32 partials (in
-// the workspace) the unpermute sums in slice order; otherwise this is
-// hn_grouped_expert_mlp_int4 into y_ws followed by hn_moe_unpermute.
+// the workspace) the unpermute sums in slice order (out NULL: left there for
+// the caller); otherwise this is hn_grouped_expert_mlp_int4 into y_ws
+// followed by hn_moe_unpermute.
 extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, const int* active,
                                      const int* n_active, const int* offsets, long E,
                                      long max_rows_per_expert, long rows, long H, long I,
@@ -931,17 +948,16 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
   const char* who = "hn_moe_experts_decode";
   HN_ARG_CHECK(E > 0 && E <= 256 && max_rows_per_expert >= 0 && rows >= 0 && T >= 0 && k > 0,
                "%s: bad sizes", who);
-  HN_ARG_CHECK(aligned16(out) && ld_o % 8 == 0 && H % 8 == 0, "%s: out rows must be 16-byte "
-               "aligned", who);
+  HN_ARG_CHECK(aligned16(out) && (!out || ld_o % 8 == 0) && H % 8 == 0,
+               "%s: out rows must be 16-byte aligned", who);
   hipStream_t s = (hipStream_t)stream;
-  const bool premul = (group % 128) != 0;
-  if (rows > 0 && max_rows_per_expert > 0 && stream_rows_ok(max_rows_per_expert, rows, E) &&
-      g_decode_path == 0 && !premul && H % 128 == 0 && I % 128 == 0 && aligned16(x_perm) &&
-      aligned16(h_ws) &&
-      hn_stream_grouped_impl(0, x_perm, H, table, active, n_active, offsets, E,
-                             max_rows_per_expert, rows, H, I, group, h_ws, I, s, 1) == 0 &&
-      hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E, max_rows_per_expert,
-                                rows, H, I, group, nullptr, s, 1) == 0) {
+  const bool split = experts_split_ok(E, max_rows_per_expert, rows, H, I, group) &&
+                     aligned16(x_perm) && aligned16(h_ws);
+  HN_ARG_CHECK(out || (split && !shared),
+               "%s: out NULL (partials left for the caller) needs the streaming path with the "
+               "K-split down projection (hn_moe_experts_decode_split_check) and no shared "
+               "expert", who);
+  if (split) {
     const long tmax = hn_cdiv(I, kTileN) > hn_cdiv(H, kTileN) ? hn_cdiv(I, kTileN)
                                                               : hn_cdiv(H, kTileN);
     const long need = hn_skinny_workspace_bytes(3, rows, H, I, E);
@@ -953,7 +969,7 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
     if (rc == 0)
       rc = hn_stream_down_split_impl(h_ws, table, active, n_active, offsets, E,
                                      max_rows_per_expert, rows, H, I, group, part, s, 0);
-    if (rc == 0)
+    if (rc == 0 && out)
       rc = hn_moe_unpermute_split4_impl(part, rows * H, inv, idx, w, T, k, shared, ld_sh, out,
                                         ld_o, H, stream);
     return rc;

@@ -224,6 +224,30 @@ def decode_layer_fits(T: int, E: int, k: int, table: "ExpertTable", gate_w: torc
     return _lib.lib().hn_moe_decode_layer_check(T, E, k, H, I, g, int(has_logits)) == 0
 
 
+def experts_split_fits(T: int, k: int, table: "ExpertTable") -> bool:
+    """Whether moe_dispatch at decode takes the streaming path with the K-split
+    down projection (then it can fold the next RMSNorm into its unpermute)."""
+    H, I, g = table.dims
+    return T <= _lib.DECODE_MAX_ROWS and _lib.lib().hn_moe_experts_decode_split_check(
+        table.num_experts, T, T * k, H, I, g) == 0
+
+
+def _unpermute_add_rmsnorm(work: torch.Tensor, r: "Routed", H: int, I: int, fold):
+    """(x + moe, RMSNorm(x + moe) * weight) from the down projection's fp32
+    K-slice partials left in ``work`` (hn_unpermute_add_rmsnorm)."""
+    T, k, E = r.T, r.k, r.E
+    dev = work.device
+    xr, nw, eps = fold
+    xr = _lib.aligned_rows(xr.reshape(T, H))
+    x_out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    h_out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    part = work.data_ptr() + _lib.lib().hn_moe_decode_layer_partials(T, E, k, H, I)
+    _lib.call("hn_unpermute_add_rmsnorm", part, T * k * H, H, _lib.ptr(r.inv), _lib.ptr(r.idx),
+              _lib.ptr(r.w), T, k, _lib.ptr(xr), xr.stride(0), _lib.ptr(x_out), H,
+              _lib.ptr(nw), _lib.ptr(h_out), H, H, float(eps), _lib.stream(dev))
+    return x_out, h_out
+
+
 def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: "ExpertTable",
                      want_logits: bool = False, logits: Optional[torch.Tensor] = None,
                      usage: Optional[torch.Tensor] = None, fold=None):
@@ -264,21 +288,17 @@ def moe_decode_layer(hidden: torch.Tensor, gate_w: torch.Tensor, k: int, table: 
               _lib.ptr(work), work.numel(), _lib.stream(dev))
     if fold is None:
         return out, r
-    xr, nw, eps = fold
-    xr = _lib.aligned_rows(xr.reshape(T, H))
-    x_out = torch.empty((T, H), dtype=torch.float16, device=dev)
-    h_out = torch.empty((T, H), dtype=torch.float16, device=dev)
-    part = work.data_ptr() + _lib.lib().hn_moe_decode_layer_partials(T, E, k, H, I)
-    _lib.call("hn_unpermute_add_rmsnorm", part, n * H, H, _lib.ptr(r.inv), _lib.ptr(r.idx),
-              _lib.ptr(r.w), T, k, _lib.ptr(xr), xr.stride(0), _lib.ptr(x_out), H,
-              _lib.ptr(nw), _lib.ptr(h_out), H, H, float(eps), _lib.stream(dev))
-    return (x_out, h_out), r
+    return _unpermute_add_rmsnorm(work, r, H, I, fold), r
 
 
 def moe_dispatch(r: Routed, table: ExpertTable,
-                 shared: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 shared: Optional[torch.Tensor] = None, fold=None):
     """Grouped SwiGLU over the routed rows and the weighted, ordered sum back
-    per token (the compute and unpermute halves of moe_experts_forward)."""
+    per token (the compute and unpermute halves of moe_experts_forward).
+    fold = (x [T, H] fp16, norm weight [H] fp16, eps), only where
+    experts_split_fits and without a shared expert: the unpermute also adds
+    the residual stream x and applies the next RMSNorm; returns (x + moe,
+    RMSNorm(x + moe))."""
     T, k, E = r.T, r.k, r.E
     H = r.x_perm.shape[1]
     Ht, I, g = table.dims
@@ -292,7 +312,9 @@ def moe_dispatch(r: Routed, table: ExpertTable,
     sh = None
     if shared is not None:
         sh = _lib.aligned_rows(shared.reshape(T, H).to(torch.float16))
-    out = torch.empty((T, H), dtype=torch.float16, device=dev)
+    assert fold is None or (shared is None and T <= _lib.DECODE_MAX_ROWS), \
+        "moe_dispatch: fold needs the decode path and no shared expert"
+    out = torch.empty((T, H), dtype=torch.float16, device=dev) if fold is None else None
     if T <= _lib.DECODE_MAX_ROWS:
         # decode: both expert phases and the unpermute (split down projection)
         work = _lib.skinny_workspace(3, n, H, I, E, dev)
@@ -301,7 +323,7 @@ def moe_dispatch(r: Routed, table: ExpertTable,
                   g, _lib.ptr(h_ws), _lib.ptr(y_perm), _lib.ptr(r.inv), _lib.ptr(r.idx),
                   _lib.ptr(r.w), T, k, _lib.ptr(sh), H if sh is None else sh.stride(0),
                   _lib.ptr(out), H, _lib.ptr(work), work.numel(), st)
-        return out
+        return out if fold is None else _unpermute_add_rmsnorm(work, r, H, I, fold)
     work = _lib.gemm_workspace(dev)  # stream-K split of the prefill GEMM
     _lib.call("hn_grouped_expert_mlp_int4", _lib.ptr(r.x_perm), _lib.ptr(table.dev),
               _lib.ptr(r.active), _lib.ptr(r.n_active), _lib.ptr(r.offsets), E, T, n, H, I, g,
@@ -503,15 +525,22 @@ class MixtralMoELayer(nn.Module):
         if rt.enable_affinity_bonus and rt._is_cached_fn is not None:
             return None
         table = self.experts.static_table(hidden_states.device)
-        if table is None or not decode_layer_fits(T, self.num_experts, top_k, table,
-                                                   rt.gate.weight, logits is not None):
-            return None
-        if norm_weight.dtype != torch.float16 or x.dtype != torch.float16:
+        if table is None or norm_weight.dtype != torch.float16 or x.dtype != torch.float16:
             return None
         usage = None if rt.training else rt.usage_counts
-        (x_out, h_out), r = moe_decode_layer(hidden_states.reshape(T, H), rt.gate.weight, top_k,
-                                             table, logits=logits, usage=usage,
-                                             fold=(x, norm_weight, eps))
+        flat = hidden_states.reshape(T, H)
+        fold = (x, norm_weight, eps)
+        if decode_layer_fits(T, self.num_experts, top_k, table, rt.gate.weight,
+                             logits is not None):
+            (x_out, h_out), r = moe_decode_layer(flat, rt.gate.weight, top_k, table,
+                                                 logits=logits, usage=usage, fold=fold)
+        elif table.num_experts == self.num_experts and experts_split_fits(T, top_k, table):
+            # e.g. 64 tokens at top-2: the routing launch, then the experts
+            # with the unpermute folded into the next RMSNorm
+            r = moe_route(flat, top_k, 0, gate_w=rt.gate.weight, logits=logits, usage=usage)
+            x_out, h_out = moe_dispatch(r, table, fold=fold)
+        else:
+            return None
         self.last_routing = (r.idx, r.w)
         return x_out.view(B, S, H), h_out.view(B, S, H)
 

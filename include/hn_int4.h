@@ -180,7 +180,11 @@ int hn_grouped_expert_mlp_int4(const void* x_perm, const void* table, const int*
  * hn_moe_unpermute, out [T, H]).  Where the streaming kernels apply, the down
  * projection runs in four K slices whose fp32 partials (kept in work) the
  * unpermute adds in slice order before the fp16 rounding; y_ws [rows, H] fp16
- * is then unused.  work: hn_skinny_workspace_bytes(3, rows, H, I, E).
+ * is then unused.  work: hn_skinny_workspace_bytes(3, rows, H, I, E).  out
+ * NULL (only on that streaming path, hn_moe_experts_decode_split_check, and
+ * without a shared expert): no unpermute; the partials stay in work at byte
+ * hn_moe_decode_layer_partials(T, E, k, H, I) for the caller (e.g.
+ * hn_unpermute_add_rmsnorm).
  * Replaces the per-expert loop and index_add_ of MixtralMoELayer.forward
  * (model/mixtral.py:327-368) / GLM4MoELayer.forward (model/glm4.py:421-473). */
 int hn_moe_experts_decode(const void* x_perm, const void* table, const int* active,
@@ -189,6 +193,13 @@ int hn_moe_experts_decode(const void* x_perm, const void* table, const int* acti
                           void* h_ws, void* y_ws, const int* inv, const int* idx, const void* w,
                           long T, long k, const void* shared, long ld_sh, void* out, long ld_o,
                           void* work, long work_bytes, void* stream);
+
+/* 0 when hn_moe_experts_decode takes its streaming path with the K-split down
+ * projection for (E, max_rows_per_expert, rows, H, I, group) under the current
+ * decode kernel family (then out may be NULL), else a nonzero code (no
+ * message set). */
+int hn_moe_experts_decode_split_check(long E, long max_rows_per_expert, long rows, long H,
+                                      long I, long group);
 
 /* The first launch of hn_moe_decode_layer alone: the routing computed in the
  * grouped gate/up streaming kernel and h_ws [T k, I] = fp16(silu(fp16(x Wg^T))
@@ -231,8 +242,10 @@ int hn_moe_decode_layer(const void* h, long ld_h, const void* gate_w, long ld_w,
                         int* n_active, long long* usage, void* h_ws, void* out, long ld_o,
                         void* work, long work_bytes, void* stream);
 
-/* Byte offset in hn_moe_decode_layer's workspace of its down projection's
- * four fp32 K-slice partials [4][T k][H] (slice stride T k H floats). */
+/* Byte offset in the workspace of hn_moe_decode_layer (and of
+ * hn_moe_experts_decode with rows = T k on its split path) of the down
+ * projection's four fp32 K-slice partials [4][T k][H] (slice stride T k H
+ * floats). */
 long hn_moe_decode_layer_partials(long T, long E, long k, long H, long I);
 
 /* 0 when hn_moe_route_experts_decode covers (T, E, k, mode, H, I, group) with

@@ -107,9 +107,16 @@ def test_c5_folded_moe_norm_is_bit_identical(c5, top_k):
     """A decode step with the MoE block's residual add and the next RMSNorm
     inside its last launch (hn_unpermute_add_rmsnorm) gives the same logits,
     bit for bit, as the step with the unpermute and the norm as two
-    launches; at top-2 (no folded launch for 128 routed rows) the two paths
-    are the same code."""
+    launches: at top-1 after the decode layer (routing in the gate/up
+    kernel), at top-2 (128 routed rows) after the routing launch and the
+    experts' split down projection."""
+    from hydranet_amd.model.moe import decode_layer_fits, experts_split_fits
     cfg, model, ids = c5
+    moe = model.layers[0].moe
+    table = moe.experts.static_table(DEV)
+    fused = decode_layer_fits(B, moe.num_experts, top_k, table, moe.router.gate.weight, True)
+    assert fused == (top_k == 1)
+    assert fused or experts_split_fits(B, top_k, table), "the folded launch does not apply"
     cache = model.new_cache(B, P + 2)
     tok = model(ids[:, :P], cache)[:, -1].argmax(-1, keepdim=True)
     pos = torch.full((1,), cache.cur_len, dtype=torch.int64, device=DEV)
