@@ -78,6 +78,14 @@ def _graph(fn, reps: int):
     return g
 
 
+def _warm_replay(g) -> None:
+    """One untimed replay of a freshly captured graph (its first replay carries
+    one-time setup), then a device sync; part of the warm-up."""
+    if g is not None:
+        g.replay()
+    torch.cuda.synchronize()
+
+
 def _time_graph(g: torch.cuda.CUDAGraph, replays: int) -> float:
     """Average ms per replay, with events on the current stream."""
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -129,7 +137,7 @@ def bench_c1(args):
     chunk = _chunk(args.steps)
     state["i"] = 0
     gr = _graph(step, chunk)
-    torch.cuda.synchronize()
+    _warm_replay(gr)
     t0 = time.perf_counter()
     if gr is not None:
         for _ in range(args.steps // chunk):
@@ -231,7 +239,7 @@ def bench_c2(args, T: int, n_layers: int = 4, phases: bool = False):
     chunk = _chunk(args.steps)
     state["i"] = 0
     gr = _graph(step, chunk)
-    torch.cuda.synchronize()
+    _warm_replay(gr)
     t0 = time.perf_counter()
     if gr is not None:
         for _ in range(args.steps // chunk):
@@ -379,7 +387,7 @@ def bench_c3(args, T: int = 32, n_layers: int = 2):
     chunk = _chunk(args.steps)
     state["i"] = 0
     gr = _graph(step, chunk)
-    torch.cuda.synchronize()
+    _warm_replay(gr)
     t0 = time.perf_counter()
     if gr is not None:
         for _ in range(args.steps // chunk):
@@ -435,6 +443,7 @@ def bench_c4(args):
     torch.cuda.synchronize()
     steps = max(5, args.steps // 10)
     gr = _graph(step, steps)
+    _warm_replay(gr)
     t0 = time.perf_counter()
     if gr is not None:
         gr.replay()
