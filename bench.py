@@ -110,7 +110,7 @@ def bench_c1(args):
     slots = [make_expert_slot(expert_seed(0, e), H, I, g, slot_idx=e) for e in range(n_exp)]
     x = normal_f16((T, H), 1234, std=1.0)
     blob = slots[0].layout.total_size
-    bytes_step = blob + 2 * T * H * 2  # blob + x + y (SURVEY C1 accounting)
+    bytes_step = blob + 2 * T * H * 2  # the expert's blob + x + y
 
     outs = [torch.empty(T, H, dtype=torch.float16, device="cuda") for _ in range(n_exp)]
     hws = [torch.empty(T, I, dtype=torch.float16, device="cuda") for _ in range(n_exp)]
@@ -966,7 +966,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only; the INT4 expert path is "
-                                   "benchmarked per GPU (see DESIGN.md for how it shards)",
+                                   "benchmarked per GPU (with expert parallelism each GPU "
+                                   "runs this same grouped path on its own experts)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if not torch.cuda.is_available():

@@ -1,10 +1,13 @@
 """Mixtral-shaped decoder around the gfx950 MoE layer: the whole-model decode
-harness.
+harness (64 sequences of the Mixtral-8x7B shape, decode tokens/s).
 
-Attention, RoPE, RMSNorm, embeddings and the LM head are stock PyTorch fp16
-(they are not the INT4 expert path); every MoE block is MixtralMoELayer on the
-gfx950 kernels with its experts resident in HBM.  Structure and arithmetic
-follow the reference:
+Every MoE block is MixtralMoELayer on the gfx950 kernels with its experts
+resident in HBM.  Around it, on the GPU: RMSNorm (with the router logits of
+its rows, and with the MoE block's unpermute folded in) and, for one-token
+decode steps, RoPE + cache append + attention in one launch are library
+kernels; the q/k/v, o and LM-head products, embeddings and prefill
+attention are PyTorch fp16 (hipBLASLt).  Structure and arithmetic follow the
+reference:
 
 * RMSNorm in fp32, scaled by the weight, cast back (model/mixtral.py:23-37);
 * RoPE with a cos/sin cache, rotate_half (model/mixtral.py:40-101);
