@@ -655,7 +655,12 @@ def c1phase(args):
 def bench_copy(args):
     """Reference rates for the 8 TB/s peak: torch's own device copy (read +
     write) and fp32 sum (read) of 1 and 4 GiB fp16 tensors, best of 10 by HIP
-    events on the current stream."""
+    events on the current stream; then hn_hbm_read_probe (a plain streaming
+    read) at the expert kernels' bytes per launch: 48 back-to-back launches,
+    each over the next chunk of a 4 GiB buffer (no reuse from the 256 MB
+    Infinity Cache), between two HIP events, as the roofline region times
+    the expert kernels."""
+    from hydranet_amd import _lib
     out = {}
     for gib in (1, 4):
         n = gib * (1 << 30) // 2
@@ -678,6 +683,35 @@ def bench_copy(args):
                                        "GB_s": round(nbytes / best / 1e6, 1)}
         del a, b
         torch.cuda.empty_cache()
+    buf = torch.ones(4 << 30, dtype=torch.uint8, device="cuda")
+    nwg = 2048
+    sink = torch.zeros(nwg, dtype=torch.float32, device="cuda")
+    st = _lib.stream()
+    # C1 down, C1 gate/up, C2 T=16 down, C2 T=16 gate/up (algorithmic bytes)
+    for name, target in (("30MB", 30_314_496), ("61MB", 60_592_128),
+                         ("245MB", 245_235_712), ("486MB", 485_556_224)):
+        chunk = target // (nwg * 16) * nwg * 16
+        nchunks = buf.numel() // chunk
+        base = buf.data_ptr()
+
+        def launch(i):
+            _lib.call("hn_hbm_read_probe", base + (i % nchunks) * chunk, chunk, nwg,
+                      _lib.ptr(sink), st)
+
+        for i in range(8):
+            launch(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(48):
+            launch(i + 8)
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 48
+        out[f"read_{name}"] = {"bytes": chunk, "us": round(us, 2),
+                               "GB_s": round(chunk / us / 1e3, 1)}
+    del buf
+    torch.cuda.empty_cache()
     return out
 
 

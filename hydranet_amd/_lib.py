@@ -44,6 +44,7 @@ SIGNATURES: dict[str, list] = {
     "hn_unpermute_add_rmsnorm": [P, L, L, P, P, P, L, L, P, L, P, L, P, P, L, L, F, P],
     "hn_moe_decode_layer_partials": [L, L, L, L, L],
     "hn_moe_experts_decode_split_check": [L, L, L, L, L, L],
+    "hn_hbm_read_probe": [P, L, L, P, P],
     "hn_attn_decode_rope": [P, L, P, P, P, P, P, L, L, L, L, L, L, P, F, P, L, P],
     "hn_rope_append": [P, L, P, L, P, L, P, P, P, L, L, L, L, L, P, P, P, L, P],
     "hn_grouped_expert_mlp_int4": [P, P, P, P, P, L, L, L, L, L, L, P, P, P, L, P],

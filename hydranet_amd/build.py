@@ -18,7 +18,7 @@ LIB = os.path.join(PKG, "libhn_int4.so")
 ARCH = os.environ.get("HN_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["hn_abi.cpp", "hn_quant.hip", "hn_gemv.hip", "hn_route.hip", "hn_stream.hip",
-           "hn_gemm.hip", "hn_decoder.hip", "hn_noalloc.hip"]
+           "hn_gemm.hip", "hn_decoder.hip", "hn_noalloc.hip", "hn_probe.hip"]
 
 
 def _hipcc() -> str:

@@ -416,6 +416,14 @@ int hn_rope_append(const void* q, long ld_q, const void* k, long ld_k, const voi
  * in the reference; for A/B measurement and tests. */
 int hn_set_decode_path(int path);
 
+/* A plain streaming read of bytes of buf (nwg workgroups, each one slice of
+ * bytes / nwg; bytes a multiple of nwg x 16, under 2^31 bytes per
+ * workgroup): the rate a launch that only reads its bytes reaches, the
+ * yardstick for the expert kernels' HBM rates.  sink [nwg] fp32 is written
+ * only if the folded data hits one fixed word (normally never).  No
+ * counterpart in the reference; for measurement (bench.py --workload copy). */
+int hn_hbm_read_probe(const void* buf, long bytes, long nwg, float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -261,3 +261,22 @@ def test_int4linear_module():
     got = q(x.to(DEV))
     _close(got, torch.from_numpy(ref))
 
+
+
+def test_hbm_read_probe_reads_and_rejects_bad_sizes():
+    """hn_hbm_read_probe (the plain streaming read bench.py times) runs over a
+    buffer split into workgroup slices without touching its sink for data
+    that does not fold to the sink's trigger word, and rejects sizes that do
+    not split into 16-byte slices."""
+    from hydranet_amd import _lib
+    nwg = 64
+    buf = torch.zeros(nwg * 4096 * 3, dtype=torch.uint8, device=DEV)
+    sink = torch.zeros(nwg, dtype=torch.float32, device=DEV)
+    print("[probe] 64 workgroups x 12 KiB", flush=True)
+    _lib.call("hn_hbm_read_probe", buf.data_ptr(), buf.numel(), nwg, _lib.ptr(sink),
+              _lib.stream())
+    torch.cuda.synchronize()
+    assert not sink.any()
+    with pytest.raises(RuntimeError, match="multiple of nwg x 16"):
+        _lib.call("hn_hbm_read_probe", buf.data_ptr(), buf.numel() - 8, nwg, _lib.ptr(sink),
+                  _lib.stream())
