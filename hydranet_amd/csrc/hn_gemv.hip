@@ -951,6 +951,7 @@ extern "C" int hn_moe_experts_decode(const void* x_perm, const void* table, cons
   HN_ARG_CHECK(aligned16(out) && (!out || ld_o % 8 == 0) && H % 8 == 0,
                "%s: out rows must be 16-byte aligned", who);
   hipStream_t s = (hipStream_t)stream;
+  if (!out && rows == 0) return 0;  // no rows: no partials to leave
   const bool split = experts_split_ok(E, max_rows_per_expert, rows, H, I, group) &&
                      aligned16(x_perm) && aligned16(h_ws);
   HN_ARG_CHECK(out || (split && !shared),
