@@ -25,8 +25,11 @@ not from the 256 MB Infinity Cache.  Steps are replayed from a HIP graph.
 
 roofline: the dominant kernel's algorithmic bytes (flops) per launch divided by
 its average duration, timed with HIP events on the stream the kernel runs on
-(c2: around each launch of the routing + gate/up kernel inside eager layer
-sequences).
+(c2: after a warm-up pass of whole layers, 48 back-to-back launches of the
+routing + gate/up kernel over the rotating layers between two events; the
+down kernel likewise).  roofline.read_probe: the same bytes read by a plain
+streaming read (hn_hbm_read_probe, timed the same way) and the kernel's time
+as a fraction of it.
 cpu_baseline: the torch-CPU restatement of the reference's
 dequantise-then-matmul path (oracle/torch_ref.py) on this host: the headline
 C2 layer at T = 16 (value) and T = 1, 4 (per_T), and one C1 expert ("c1").
@@ -655,12 +658,8 @@ def c1phase(args):
 def bench_copy(args):
     """Reference rates for the 8 TB/s peak: torch's own device copy (read +
     write) and fp32 sum (read) of 1 and 4 GiB fp16 tensors, best of 10 by HIP
-    events on the current stream; then hn_hbm_read_probe (a plain streaming
-    read) at the expert kernels' bytes per launch: 48 back-to-back launches,
-    each over the next chunk of a 4 GiB buffer (no reuse from the 256 MB
-    Infinity Cache), between two HIP events, as the roofline region times
-    the expert kernels."""
-    from hydranet_amd import _lib
+    events on the current stream; then read_probe at the expert kernels'
+    bytes per launch."""
     out = {}
     for gib in (1, 4):
         n = gib * (1 << 30) // 2
@@ -683,13 +682,25 @@ def bench_copy(args):
                                        "GB_s": round(nbytes / best / 1e6, 1)}
         del a, b
         torch.cuda.empty_cache()
+    # C1 down, C1 gate/up, C2 T=16 down, C2 T=16 gate/up (algorithmic bytes)
+    out.update(read_probe({"read_30MB": 30_314_496, "read_61MB": 60_592_128,
+                           "read_245MB": 245_235_712, "read_486MB": 485_556_224}))
+    return out
+
+
+def read_probe(targets: dict) -> dict:
+    """hn_hbm_read_probe (a plain streaming read, 2048 workgroups) at each
+    target's bytes per launch (rounded down to a multiple of 32 KiB): 48
+    back-to-back launches, each over the next chunk of a 4 GiB buffer (no
+    reuse from the 256 MB Infinity Cache), between two HIP events on the
+    launch stream, after 8 untimed launches."""
+    from hydranet_amd import _lib
     buf = torch.ones(4 << 30, dtype=torch.uint8, device="cuda")
     nwg = 2048
     sink = torch.zeros(nwg, dtype=torch.float32, device="cuda")
     st = _lib.stream()
-    # C1 down, C1 gate/up, C2 T=16 down, C2 T=16 gate/up (algorithmic bytes)
-    for name, target in (("30MB", 30_314_496), ("61MB", 60_592_128),
-                         ("245MB", 245_235_712), ("486MB", 485_556_224)):
+    out = {}
+    for name, target in targets.items():
         chunk = target // (nwg * 16) * nwg * 16
         nchunks = buf.numel() // chunk
         base = buf.data_ptr()
@@ -708,9 +719,8 @@ def bench_copy(args):
         e1.record()
         e1.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / 48
-        out[f"read_{name}"] = {"bytes": chunk, "us": round(us, 2),
-                               "GB_s": round(chunk / us / 1e3, 1)}
-    del buf
+        out[name] = {"bytes": chunk, "us": round(us, 2), "GB_s": round(chunk / us / 1e3, 1)}
+    del buf, sink
     torch.cuda.empty_cache()
     return out
 
@@ -1093,6 +1103,15 @@ def main():
                 "traffic_source": None,
                 "bytes_per_launch": gu["bytes_per_launch"], "avg_us": gu["avg_us"],
                 "down": ph["down_4slices"], "active_experts": ph["active_experts"]}
+            # the same bytes read by a plain streaming read: what a launch that
+            # only reads them reaches (context for frac, whose peak is nominal)
+            rp = read_probe({"gate_up": gu["bytes_per_launch"],
+                             "down": ph["down_4slices"]["bytes_per_launch"]})
+            res["roofline"]["read_probe"] = {
+                **rp["gate_up"], "kernel_over_read": round(rp["gate_up"]["us"] / gu["avg_us"], 3)}
+            res["roofline"]["down"]["read_probe"] = {
+                **rp["down"],
+                "kernel_over_read": round(rp["down"]["us"] / ph["down_4slices"]["avg_us"], 3)}
             if ph["active_experts"] == 8:
                 res["roofline"]["traffic"] = ROUTE_GATE_UP_C2_T16_TRAFFIC
                 res["roofline"]["traffic_source"] = (
