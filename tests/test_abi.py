@@ -37,6 +37,46 @@ def test_ctypes_table_matches_header():
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
 
 
+def _declared_params():
+    """name -> parameter kinds ('P' pointer, 'L' long, 'I' int, 'F' float) of
+    every function include/*.h declares."""
+    out = {}
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if not fn.endswith(".h"):
+            continue
+        src = re.sub(r"/\*.*?\*/", " ", open(os.path.join(ROOT, "include", fn)).read(), flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?\w+\*?\s+\*?(hn_\w+)\s*\(([^)]*)\)\s*;", src,
+                             re.M):
+            params = " ".join(m.group(2).split())
+            kinds = []
+            if params and params != "void":
+                for prm in params.split(","):
+                    t = prm.strip()
+                    if "*" in t:
+                        kinds.append("P")
+                    elif re.match(r"(const\s+)?long\b", t):
+                        kinds.append("L")
+                    elif re.match(r"(const\s+)?int\b", t):
+                        kinds.append("I")
+                    elif re.match(r"(const\s+)?float\b", t):
+                        kinds.append("F")
+                    else:
+                        kinds.append("?" + t)
+            out[m.group(1)] = kinds
+    return out
+
+
+def test_ctypes_argument_kinds_match_header():
+    """Every ctypes signature has the header's parameter count and kinds, so a
+    changed declaration cannot silently shift the arguments of a call."""
+    from hydranet_amd import _lib
+    code = {_lib.P: "P", _lib.L: "L", _lib.I: "I", _lib.F: "F"}
+    decl = _declared_params()
+    assert set(_lib.SIGNATURES) <= set(decl)
+    for name, sig in _lib.SIGNATURES.items():
+        assert [code[t] for t in sig] == decl[name], name
+
+
 def test_workspace_query():
     from hydranet_amd import _lib
     h = _lib.lib()
