@@ -37,33 +37,6 @@ __device__ __forceinline__ bool topk_beats(float bv, int be, float av, int ae) {
 // (exp in double, rounded once: it also ranks the experts), / (sum + eps) * scaling
 // (model/glm4.py:282-307); mode 2 sigmoid * scaling.  Compact loops: each element's value is recomputed
 // where it is needed (same arithmetic each time) instead of kept in arrays.
-__device__ __noinline__ void topk_weights(const float* l, const int* sel, int k, int mode,
-                                          float eps, float scaling, h16* w_o) {
-  if (mode == 0) {
-    // fp32 softmax as F.softmax(topk_logits.float()) (exp of x - max)
-    const float mx = l[sel[0]];
-    float z = 0.f;
-#pragma unroll 1
-    for (int i = 0; i < k; ++i) z += expf(l[sel[i]] - mx);
-    float s = 0.f;
-#pragma unroll 1
-    for (int i = 0; i < k; ++i) s += expf(l[sel[i]] - mx) / z;
-#pragma unroll 1
-    for (int i = 0; i < k; ++i) w_o[i] = (h16)((expf(l[sel[i]] - mx) / z) / s);
-  } else if (mode == 1) {
-    float s = 0.f;
-#pragma unroll 1
-    for (int i = 0; i < k; ++i) s += sigmoid_f32(l[sel[i]]);
-    const float d = s + eps;
-#pragma unroll 1
-    for (int i = 0; i < k; ++i) w_o[i] = (h16)f32_mul(sigmoid_f32(l[sel[i]]) / d, scaling);
-  } else {
-#pragma unroll 1
-    for (int i = 0; i < k; ++i) w_o[i] = (h16)f32_mul(sigmoid_f32(l[sel[i]]), scaling);
-  }
-}
-
-// Unsigned key with the order of the float: larger value, larger key.
 __device__ __forceinline__ uint32_t order_key(float v) {
   const uint32_t u = __builtin_bit_cast(uint32_t, v);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -93,7 +66,7 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // (ballots, lowest register then lowest lane); the winner's key is cleared
 // for the next round.  Rounds pick in selection order (value desc, expert
 // asc), so the weights sum the selected in that order: the same selection
-// and weight arithmetic as topk_small / topk_weights.
+// and weight arithmetic as topk_small.
 // The selection bias of the lane's four candidates (experts lane + 64 j),
 // loaded once per wave and reused for every token: unconditional loads
 // (index clamped to E - 1) that go out together.  Zero without a bias.
@@ -167,7 +140,7 @@ __device__ __forceinline__ void topk_wave(const float* l, const TopkBias& bias, 
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_raw), r));
   };
   if (mode == 0) {
-    // fp32 softmax over the selected logits, renormalised (topk_weights)
+    // fp32 softmax over the selected logits, renormalised (as topk_small)
     const float mx = at(0);
     float z = 0.f;
     for (int r = 0; r < k; ++r) z += expf(at(r) - mx);
@@ -194,19 +167,24 @@ __device__ __forceinline__ void topk_wave(const float* l, const TopkBias& bias, 
 }
 
 // Top-k of one token's row by one thread for E <= EB experts: every loop is
-// unrolled over compile-time bounds, so the candidates and the selection
-// stay in registers.  Same selection and weight arithmetic as topk_wave.
+// unrolled over compile-time bounds, so the candidates, the selection and the
+// selected logits stay in registers (the weights read no memory).  Same
+// selection and weight arithmetic as topk_wave: mode 0, fp32 softmax over the
+// selected logits (exp of x - max), renormalised, as
+// F.softmax(topk_logits.float()); mode 1, sigmoid / (sum + eps) * scaling;
+// mode 2, sigmoid * scaling; each sum in selection order.
 template <int EB, int KB = kMaxTopK, int MODE = -1>
 __device__ __forceinline__ void topk_small(const float* l, const float* bias, int E, int k,
                                            int mode_rt, float eps, float scaling, int* idx_o,
                                            h16* w_o) {
   const int mode = MODE >= 0 ? MODE : mode_rt;
-  float cv[EB];
+  float lv[EB], cv[EB];
   bool ok[EB];
 #pragma unroll
   for (int e = 0; e < EB; ++e) {
     ok[e] = e < E;
-    float v = ok[e] ? l[e] : 0.f;
+    lv[e] = ok[e] ? l[e] : 0.f;
+    float v = lv[e];
     if (mode >= 1 && ok[e]) {
       v = sigmoid_f32(v);
       if (bias) v = v + bias[e];
@@ -214,16 +192,23 @@ __device__ __forceinline__ void topk_small(const float* l, const float* bias, in
     cv[e] = v;
   }
   int sel[KB];
+  float sr[KB];  // the selected experts' logits
 #pragma unroll
   for (int i = 0; i < KB; ++i) {
     sel[i] = -1;
+    sr[i] = 0.f;
     if (i < k) {
-      float bv = -__builtin_inff();
+      float bv = -__builtin_inff(), br = 0.f;
       int be = 0x7fffffff;
 #pragma unroll
       for (int e = 0; e < EB; ++e)
-        if (ok[e] && topk_beats(cv[e], e, bv, be)) { bv = cv[e]; be = e; }
+        if (ok[e] && topk_beats(cv[e], e, bv, be)) {
+          bv = cv[e];
+          be = e;
+          br = lv[e];
+        }
       sel[i] = be < E ? be : -1;
+      sr[i] = br;
 #pragma unroll
       for (int e = 0; e < EB; ++e)
         if (e == be) ok[e] = false;
@@ -232,7 +217,33 @@ __device__ __forceinline__ void topk_small(const float* l, const float* bias, in
 #pragma unroll
   for (int i = 0; i < KB; ++i)
     if (i < k) idx_o[i] = sel[i];
-  topk_weights(l, idx_o, k, mode, eps, scaling, w_o);
+  if (mode == 0) {
+    const float mx = sr[0];
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (i < k) z += expf(sr[i] - mx);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (i < k) s += expf(sr[i] - mx) / z;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (i < k) w_o[i] = (h16)((expf(sr[i] - mx) / z) / s);
+  } else if (mode == 1) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (i < k) s += sigmoid_f32(sr[i]);
+    const float d = s + eps;
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (i < k) w_o[i] = (h16)f32_mul(sigmoid_f32(sr[i]) / d, scaling);
+  } else {
+#pragma unroll
+    for (int i = 0; i < KB; ++i)
+      if (i < k) w_o[i] = (h16)f32_mul(sigmoid_f32(sr[i]), scaling);
+  }
 }
 
 }  // namespace
