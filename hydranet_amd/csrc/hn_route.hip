@@ -646,6 +646,10 @@ extern "C" int hn_moe_route(const void* h, long ld_h, const void* w, long ld_w, 
     else if (lgv == 1) HN_ROUTE_LAUNCH(h16, true, 1, 0);
     else if (lgv == 2) HN_ROUTE_LAUNCH(h16, true, 2, 0);
     else if (lgv == 4) HN_ROUTE_LAUNCH(h16, true, 4, 0);
+    // given logits (or no MFMA logits) with Mixtral's top-2: the top-2
+    // specialisation, not the generic top-k (whose unrolled guards for up
+    // to 16 picks and every mode cost a thread about 5 us of branches)
+    else if (mix) HN_ROUTE_LAUNCH(h16, true, 0, 1);
     else HN_ROUTE_LAUNCH(h16, true, 0, 0);
   } else {
     HN_ROUTE_LAUNCH(float, false, 0, 0);

@@ -508,6 +508,14 @@ def test_fused_route_matches_separate_kernels(T, E, k, mode):
         _logits_within(r.logits.cpu(), ref_lg, ulp.cpu() + 1.6e-5)
         # top-k, permutation and gather bit for bit from the fused logits
         ref = _separate_route(h, gw, k, 0, logits=r.logits)
+        # the same launch given those logits (no gate product; Mixtral's
+        # top-2 takes its specialised top-k there too) routes identically
+        rg = moe_route(h, k, 0, logits=r.logits.clone())
+        m = T * k
+        assert torch.equal(rg.idx, r.idx) and torch.equal(rg.w, r.w)
+        assert torch.equal(rg.offsets, r.offsets)
+        assert torch.equal(rg.perm[:m], r.perm[:m]) and torch.equal(rg.inv[:m], r.inv[:m])
+        assert torch.equal(rg.x_perm[:m], r.x_perm[:m])
     else:
         gw = (torch.randn(E, H, generator=g) * 0.02).float().to(DEV)
         bias = (torch.rand(E, generator=g) * 0.1).to(DEV)
