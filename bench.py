@@ -967,7 +967,7 @@ def bench_c5(args):
 # --pmc passes over `bench.py --workload c2phase`, each scaled by the same
 # counter on a 512 MiB copy.  Commands, raw counter values and scale factors:
 # profiles/route_gate_up_c2_t16_traffic.md.  Re-measure after a kernel change.
-ROUTE_GATE_UP_C2_T16_TRAFFIC = 487_510_777
+ROUTE_GATE_UP_C2_T16_TRAFFIC = 487_504_833
 
 
 def main():
